@@ -1,0 +1,267 @@
+"""Benchmark of the sparse-voxel convolution path on one MI355X.
+
+Default workload (the north-star target): 2x sparse
+subdivide of ~0.32M R=256 shell parents (Bernoulli(0.5) per child) into ~1.26M
+R=512 children, hash + kernel map of the children, parent->child feature
+broadcast (skip_repeat 256->256) and a 3x3x3 submanifold conv 256->128, all in
+bf16 storage with fp32 accumulation.  One step = that whole chain, with every
+input (parent coordinates, logits, parent features, weights) resident in HBM
+when the timed region starts.
+
+Prints one JSON line.  `value` is whole-step effective conv TFLOP/s
+(2*P*Ci*Co per step / step time); `roofline` is the conv kernel's own rate from
+HIP events recorded on the backend stream around each conv launch;
+`cpu_baseline` is the single-threaded CPU oracle (a restatement of the
+reference CPU backend) on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "trellis2.c_amd"))
+
+import numpy as np  # noqa: E402
+
+import sparse_hip as sh  # noqa: E402
+import workloads as wl  # noqa: E402
+
+PEAK_TFLOPS = {sh.F32: 157.3, sh.F16: 2516.6, sh.BF16: 2516.6}
+PEAK_HBM_GBS = 8000.0
+METRIC = "submanifold conv effective TFLOP/s + hash/kernel-map Mvoxels/s, 1 MI355X"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Cfg3:
+    """Subdivide -> hash/map -> broadcast -> conv on device-resident inputs."""
+
+    def __init__(self, be, w):
+        self.be = be
+        self.w = w
+        dt = be.dtype
+        self.parents = w["parent_coords"].shape[0]
+        self.pmap = be.upload_coords(w["parent_coords"])
+        self.logits = be.upload(w["logits"])
+        self.pfeats = be.upload(w["parent_feats"])
+        self.weight = be.keep(np.ascontiguousarray(w["weight"], np.float32))
+        self.ci, self.co = w["ci"], w["co"]
+        # Size the child buffers once from a first pass (not timed).
+        dm = be.build_c2s_map_device(self.logits, self.parents, coords_map=self.pmap)
+        self.m = dm.n
+        rb = be.build_rulebook_for_c2s_map(dm)
+        self.pairs = be.rulebook_stats(rb)["pairs"]
+        rb.free()
+        be.free_map(dm)
+        self.xc = be.alloc(self.m * self.ci)
+        self.y = be.alloc(self.m * self.co)
+        self.dtype = dt
+
+    def step(self):
+        be = self.be
+        dm = be.build_c2s_map_device(self.logits, self.parents, coords_map=self.pmap)
+        rb = be.build_rulebook_for_c2s_map(dm)
+        be.skip_repeat_device(self.pfeats, dm, self.xc, self.ci, self.ci)
+        be.conv(rb, self.xc, self.weight, None, self.y, self.ci, self.co)
+        rb.free()
+        be.free_map(dm)
+
+    def describe(self):
+        return {"workload": self.w["name"], "parents": int(self.parents), "voxels": int(self.m),
+                "pairs": int(self.pairs), "ci": self.ci, "co": self.co, "grid": "R=256 -> R=512",
+                "subdivide": "Bernoulli(0.5) per child", "broadcast": "skip_repeat 256->256"}
+
+    def flops(self):
+        return wl.conv_flops(self.pairs, self.ci, self.co)
+
+
+class ConvOnly:
+    """Configs 1, 4, 5: hash + kernel map rebuild and one conv per step."""
+
+    def __init__(self, be, w):
+        self.be = be
+        self.w = w
+        self.n = w["coords"].shape[0]
+        self.cmap = be.upload_coords(w["coords"])
+        self.x = be.upload(w["feats"])
+        self.weight = be.keep(np.ascontiguousarray(w["weight"], np.float32))
+        self.ci, self.co = w["ci"], w["co"]
+        self.y = be.alloc(self.n * self.co)
+        rb = be.build_rulebook_for_c2s_map(self.cmap)
+        self.pairs = be.rulebook_stats(rb)["pairs"]
+        rb.free()
+        self.m = self.n
+
+    def step(self):
+        rb = self.be.build_rulebook_for_c2s_map(self.cmap)
+        self.be.conv(rb, self.x, self.weight, None, self.y, self.ci, self.co)
+        rb.free()
+
+    def describe(self):
+        return {"workload": self.w["name"], "voxels": int(self.n), "pairs": int(self.pairs), "ci": self.ci,
+                "co": self.co}
+
+    def flops(self):
+        return wl.conv_flops(self.pairs, self.ci, self.co)
+
+
+class Cfg2(ConvOnly):
+    """Residual block: conv -> LayerNorm -> SiLU -> conv -> + skip (fp16)."""
+
+    def __init__(self, be, w):
+        super().__init__(be, w)
+        self.weight2 = be.keep(np.ascontiguousarray(w["weight2"], np.float32))
+        self.gamma = be.keep(w["gamma"])
+        self.beta = be.keep(w["beta"])
+        self.h = be.alloc(self.n * self.co)
+        self.out = be.alloc(self.n * self.co)
+
+    def step(self):
+        be = self.be
+        rb = be.build_rulebook_for_c2s_map(self.cmap)
+        be.conv(rb, self.x, self.weight, None, self.y, self.ci, self.co)
+        be.row_norm(self.y, self.gamma, self.beta, self.h, self.n, self.co, 1e-6, silu=True)
+        be.conv(rb, self.h, self.weight2, None, self.y, self.co, self.co)
+        be.add(self.y, self.x, self.out, self.n * self.co)
+        rb.free()
+
+    def flops(self):
+        return 2 * wl.conv_flops(self.pairs, self.ci, self.co)
+
+
+def cpu_baseline(cfg, w, stride):
+    """Single-threaded CPU oracle on a bounded sample of the same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as orc
+
+    dt = wl.CONFIGS[cfg]["dtype"]
+    rnd = (lambda a: sh.storage_round(a, dt))
+    t = {}
+    if cfg == 3:
+        t0 = time.perf_counter()
+        rc, cc, pp, ss = orc.c2s_map(w["parent_coords"], w["logits"])
+        t["subdivide"] = time.perf_counter() - t0
+        coords = cc
+        t0 = time.perf_counter()
+        feats = orc.skip_repeat(rnd(w["parent_feats"]), pp, ss, w["ci"], w["ci"])
+        t["broadcast"] = time.perf_counter() - t0
+    else:
+        coords = w["coords"]
+        feats = rnd(w["feats"])
+    n = coords.shape[0]
+    t0 = time.perf_counter()
+    rb = orc.Rulebook(coords)
+    t["hash"] = time.perf_counter() - t0
+    nbr = rb.neighbors()
+    pairs_total = int((nbr >= 0).sum())
+    rows = (0, n, stride)
+    pairs_sample = int((nbr[::stride] >= 0).sum())
+    convs = 2 if cfg == 2 else 1
+    t0 = time.perf_counter()
+    rb.conv(feats, rnd(w["weight"]), None, w["ci"], w["co"], rows=rows)
+    t_sample = time.perf_counter() - t0
+    t["conv"] = convs * t_sample * pairs_total / max(1, pairs_sample)
+    total = sum(t.values())
+    flops = convs * wl.conv_flops(pairs_total, w["ci"], w["co"])
+    sample = (f"cfg{cfg}: subdivide/broadcast/hash on the full set, conv timed on every {stride}th output row "
+              f"({pairs_sample} of {pairs_total} pairs) and extrapolated by pair count; 1 thread")
+    return {"value": flops / total / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port", "sample": sample,
+            "seconds_full_estimate": round(total, 3), "stage_seconds": {k: round(v, 4) for k, v in t.items()},
+            "host_cpu": platform.processor() or platform.machine(), "host_nproc": os.cpu_count()}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-stride", type=int, default=16)
+    ap.add_argument("--conv-algo", type=int, default=sh.CONV_AUTO)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU sharding design is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if sh.device_count() < 1:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+
+    cfg = args.config
+    spec = wl.CONFIGS[cfg]
+    log(f"bench: generating cfg{cfg} ({spec['name']})")
+    w = wl.workload(cfg)
+    be = sh.Backend(0, spec["dtype"], conv_algo=args.conv_algo)
+    job = {3: Cfg3, 2: Cfg2}.get(cfg, ConvOnly)(be, w)
+    log(f"bench: {job.describe()}")
+    for _ in range(args.warmup):
+        job.step()
+    be.synchronize()
+    be.profile(True)
+    be.profile_read(reset=True)
+    be.synchronize()
+    t0 = time.perf_counter()
+    be.event(0)
+    for _ in range(args.steps):
+        job.step()
+    be.event(1)
+    be.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    dev_ms = be.elapsed(0, 1)
+    stages = be.profile_read(reset=True)
+    be.profile(False)
+    ms_per_step = max(dev_ms, wall) / args.steps
+    flops = job.flops()
+    conv_ms, conv_launches = stages["conv"]
+    conv_avg = conv_ms / max(1, conv_launches)
+    per_launch_flops = wl.conv_flops(job.pairs, job.ci, job.co)
+    achieved = per_launch_flops / (conv_avg * 1e-3) / 1e12 if conv_avg > 0 else 0.0
+    hm_ms = (stages["hash"][0] + stages["map"][0]) / args.steps
+    elem = 4 if spec["dtype"] == sh.F32 else 2
+    result = {
+        "metric": METRIC,
+        "value": round(flops / (ms_per_step * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl.DTYPE_NAMES[spec["dtype"]],
+        "data": "synthetic (seeded generator, random-init weights)",
+        "config": job.describe(),
+        "hash_map_mvoxels_per_s": round(job.m / (hm_ms * 1e-3) / 1e6, 1) if hm_ms > 0 else None,
+        "conv_kernel_tflops": round(achieved, 2),
+        "stage_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in stages.items()},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "sparse_conv3d",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_TFLOPS[spec["dtype"]],
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS[spec["dtype"]], 4),
+            "traffic": None,
+            "algorithmic_bytes": wl.conv_bytes(job.m, job.ci, job.co, elem),
+            "avg_launch_ms": round(conv_avg, 4),
+        },
+        "timing": {"device_event_ms": round(dev_ms, 3), "wall_ms": round(wall, 3)},
+    }
+    if not args.no_cpu_baseline:
+        log("bench: timing the CPU oracle baseline")
+        result["cpu_baseline"] = cpu_baseline(cfg, w, args.cpu_stride)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    be.destroy()
+
+
+if __name__ == "__main__":
+    main()

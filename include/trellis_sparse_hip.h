@@ -1,0 +1,304 @@
+/*
+ * trellis_sparse_hip.h - C ABI of the MI355X (gfx950) sparse-voxel backend.
+ *
+ * The library is a drop-in backend behind trellis2.c's sparse backend vtable.
+ * It plugs in where the CPU and Vulkan backends plug in today:
+ *
+ *   reference: src/ops/sparse/trellis_sparse_backend.h:24-201  (ops table)
+ *              src/ops/sparse/trellis_sparse_backend.h:203-207 (backend object)
+ *              src/ops/sparse/trellis_sparse_backend.h:209-210 (factories)
+ *
+ * The ops table below is ABI-identical to trellis_sparse_backend_ops: the same
+ * 27 function pointers in the same order with the same C signatures, so a
+ * backend created here can be handed to the reference executors
+ * (src/architectures/sparse_unet_{decoder,encoder}/executor.c) unchanged.
+ *
+ * Include order inside the reference tree: include "trellis.h" and
+ * "sparse/trellis_sparse_backend.h" first; this header then reuses their
+ * definitions (guarded by their include guards) and only adds the
+ * trellis_sparse_hip_* entry points.  Standalone, it defines the shared types
+ * itself with the reference's exact enumerator values.
+ *
+ * Everything is plain C: pointers, sizes, status codes.  No HIP, torch or C++
+ * types appear in any signature.
+ */
+#ifndef TRELLIS_SPARSE_HIP_H
+#define TRELLIS_SPARSE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Types shared with the reference (include/trellis.h:30-40, :55-59).        */
+/* ------------------------------------------------------------------------ */
+#ifndef TRELLIS2_C_TRELLIS_H
+typedef enum trellis_status {
+    TRELLIS_STATUS_OK = 0,
+    TRELLIS_STATUS_ERROR = 1,
+    TRELLIS_STATUS_INVALID_ARGUMENT = 2,
+    TRELLIS_STATUS_IO_ERROR = 3,
+    TRELLIS_STATUS_PARSE_ERROR = 4,
+    TRELLIS_STATUS_OUT_OF_MEMORY = 5,
+    TRELLIS_STATUS_CUDA_UNAVAILABLE = 6,
+    TRELLIS_STATUS_NOT_FOUND = 7,
+    TRELLIS_STATUS_NOT_IMPLEMENTED = 8
+} trellis_status;
+
+typedef enum trellis_sparse_backend_kind {
+    TRELLIS_SPARSE_BACKEND_CUDA = 0,
+    TRELLIS_SPARSE_BACKEND_CPU = 1,
+    TRELLIS_SPARSE_BACKEND_VULKAN = 2
+} trellis_sparse_backend_kind;
+#endif
+
+/* New backend kind value for this library.  A caller selects it through
+ * trellis_sparse_unet_vae_{decoder,encoder}_forward_options.backend_kind
+ * together with options.sparse_backend (executor.c:619-621 requires
+ * backend->kind == options->backend_kind). */
+#define TRELLIS_SPARSE_BACKEND_HIP ((trellis_sparse_backend_kind) 3)
+
+/* ------------------------------------------------------------------------ */
+/* Sparse backend vtable (src/ops/sparse/trellis_sparse_backend.h:9-207).    */
+/* ------------------------------------------------------------------------ */
+#ifndef TRELLIS2_C_OPS_SPARSE_BACKEND_H
+typedef struct trellis_sparse_buffer trellis_sparse_buffer;
+typedef struct trellis_sparse_rulebook trellis_sparse_rulebook;
+typedef struct trellis_sparse_c2s_device_map trellis_sparse_c2s_device_map;
+typedef struct trellis_sparse_backend trellis_sparse_backend;
+struct trellis_pixal_camera;
+struct trellis_pixal_naf_attention_desc;
+
+enum {
+    TRELLIS_SPARSE_TRIM_FREE_BUFFERS = 1u << 0,
+    TRELLIS_SPARSE_TRIM_WEIGHTS = 1u << 1,
+    TRELLIS_SPARSE_TRIM_ALL = (1u << 0) | (1u << 1)
+};
+
+typedef struct trellis_sparse_backend_ops {
+    void (*destroy)(trellis_sparse_backend * backend);
+
+    trellis_status (*alloc_f32)(trellis_sparse_backend * backend, size_t count, trellis_sparse_buffer ** out);
+    trellis_status (*upload_f32)(trellis_sparse_backend * backend, const float * src, size_t count, trellis_sparse_buffer ** out);
+    trellis_status (*upload_i32)(trellis_sparse_backend * backend, const int32_t * src, size_t count, trellis_sparse_buffer ** out);
+    trellis_status (*download_f32)(trellis_sparse_backend * backend, const trellis_sparse_buffer * src, float * dst, size_t count);
+    void (*free_buffer)(trellis_sparse_backend * backend, trellis_sparse_buffer * buffer);
+
+    trellis_status (*linear)(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                             const float * weight, const float * bias, trellis_sparse_buffer * y,
+                             int64_t n, int in_channels, int out_channels);
+    trellis_status (*linear_silu)(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                  const float * weight, const float * bias, trellis_sparse_buffer * y,
+                                  int64_t n, int in_channels, int out_channels);
+    trellis_status (*row_norm)(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                               const float * gamma, const float * beta, trellis_sparse_buffer * y,
+                               int64_t n, int channels, float eps);
+    trellis_status (*row_norm_silu)(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                    const float * gamma, const float * beta, trellis_sparse_buffer * y,
+                                    int64_t n, int channels, float eps);
+    trellis_status (*silu_inplace)(trellis_sparse_backend * backend, trellis_sparse_buffer * x, size_t count);
+    trellis_status (*add)(trellis_sparse_backend * backend, const trellis_sparse_buffer * a,
+                          const trellis_sparse_buffer * b, trellis_sparse_buffer * y, size_t count);
+
+    trellis_status (*build_rulebook)(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                                     int64_t n, trellis_sparse_rulebook ** out);
+    trellis_status (*sparse_conv3d)(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                                    const trellis_sparse_buffer * feats, const float * weight, const float * bias,
+                                    trellis_sparse_buffer * out, int64_t n, int in_channels, int out_channels);
+    void (*free_rulebook)(trellis_sparse_backend * backend, trellis_sparse_rulebook * rulebook);
+
+    trellis_status (*c2s_gather)(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                 const int32_t * parent, const int32_t * subidx, trellis_sparse_buffer * y,
+                                 int64_t n_out, int out_channels);
+    trellis_status (*skip_repeat)(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                  const int32_t * parent, const int32_t * subidx, trellis_sparse_buffer * y,
+                                  int64_t n_out, int in_channels, int out_channels);
+    trellis_status (*build_c2s_map)(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                                    const trellis_sparse_buffer * logits, int64_t n, int32_t ** coords_out,
+                                    int32_t ** parent_out, int32_t ** subidx_out, int64_t * n_out);
+    trellis_status (*alias_c2s_map)(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                                    const int32_t * parent, const int32_t * subidx, int64_t n,
+                                    const int32_t * alias_coords_bxyz, const int32_t * alias_parent,
+                                    const int32_t * alias_subidx);
+    trellis_status (*build_c2s_map_device)(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                                           const trellis_sparse_c2s_device_map * coords_map,
+                                           const trellis_sparse_buffer * logits, int64_t n,
+                                           trellis_sparse_c2s_device_map ** map_out, int64_t * n_out);
+    trellis_status (*build_rulebook_for_c2s_map)(trellis_sparse_backend * backend,
+                                                 const trellis_sparse_c2s_device_map * map,
+                                                 trellis_sparse_rulebook ** out);
+    trellis_status (*c2s_gather_device)(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                        const trellis_sparse_c2s_device_map * map, trellis_sparse_buffer * y,
+                                        int64_t n_out, int out_channels);
+    trellis_status (*skip_repeat_device)(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                         const trellis_sparse_c2s_device_map * map, trellis_sparse_buffer * y,
+                                         int64_t n_out, int in_channels, int out_channels);
+    trellis_status (*download_c2s_coords)(trellis_sparse_backend * backend,
+                                          const trellis_sparse_c2s_device_map * map,
+                                          int32_t * coords_out, int64_t n);
+    trellis_status (*download_c2s_map)(trellis_sparse_backend * backend,
+                                       const trellis_sparse_c2s_device_map * map, int32_t * coords_out,
+                                       int32_t * parent_out, int32_t * subidx_out, int64_t n);
+    /* Releases backend caches only. Device-resident C2S maps remain valid. */
+    trellis_status (*trim)(trellis_sparse_backend * backend, unsigned flags, size_t * released_bytes);
+    trellis_status (*pixal_naf_attention_project_sparse)(
+        trellis_sparse_backend * backend, const float * queries, const float * keys, const float * values,
+        const int32_t * coords_bxyz, int64_t n_coords, const struct trellis_pixal_camera * cameras,
+        const struct trellis_pixal_naf_attention_desc * desc, float * projected_out, size_t projected_count);
+} trellis_sparse_backend_ops;
+
+struct trellis_sparse_backend {
+    const trellis_sparse_backend_ops * ops;
+    trellis_sparse_backend_kind kind;
+    int device;
+};
+#endif /* TRELLIS2_C_OPS_SPARSE_BACKEND_H */
+
+/* ------------------------------------------------------------------------ */
+/* Creation-time policy.                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Storage / MFMA input type of every buffer the backend owns.  The vtable
+ * edges stay fp32 (upload_f32 rounds to the storage type with
+ * round-to-nearest-even, download_f32 widens), and all arithmetic accumulates
+ * in fp32.  Mirrors the per-component compute_dtype policy of the reference
+ * model package (models/trellis2/model.json:90-107). */
+typedef enum trellis_sparse_hip_dtype {
+    TRELLIS_SPARSE_HIP_F32 = 0,
+    TRELLIS_SPARSE_HIP_F16 = 1,
+    TRELLIS_SPARSE_HIP_BF16 = 2
+} trellis_sparse_hip_dtype;
+
+/* Convolution schedule.  AUTO picks by channel counts and dtype.  The choice
+ * never changes which pairs contribute, only the order of fp32 summation. */
+typedef enum trellis_sparse_hip_conv_algo {
+    TRELLIS_SPARSE_HIP_CONV_AUTO = 0,
+    TRELLIS_SPARSE_HIP_CONV_GENERIC = 1,   /* one lane per output element, any channels */
+    TRELLIS_SPARSE_HIP_CONV_MASKED = 2,    /* output-stationary implicit GEMM over the neighbour table */
+    TRELLIS_SPARSE_HIP_CONV_COMPACT = 3    /* output-stationary over compacted per-offset pair lists */
+} trellis_sparse_hip_conv_algo;
+
+typedef struct trellis_sparse_hip_policy {
+    uint32_t struct_size;      /* sizeof(trellis_sparse_hip_policy) */
+    int32_t compute_dtype;     /* trellis_sparse_hip_dtype */
+    int32_t conv_algo;         /* trellis_sparse_hip_conv_algo */
+    int32_t cache_weights;     /* 1: keep device copies of host weights keyed by (pointer, count) until
+                                  trim(TRELLIS_SPARSE_TRIM_WEIGHTS) or destroy, like the Vulkan backend
+                                  (trellis_sparse_vulkan.c:1019-1052). 0: convert on every call. */
+    int32_t reject_duplicates; /* 0: duplicate coordinates resolve to the last row, as the CPU backend does
+                                  (trellis_sparse_cpu.c:314-318). 1: build_rulebook returns
+                                  TRELLIS_STATUS_INVALID_ARGUMENT on a duplicate. */
+} trellis_sparse_hip_policy;
+
+/* Fills *policy with the defaults: F32, AUTO, cache_weights=1, reject_duplicates=0. */
+void trellis_sparse_hip_policy_init(trellis_sparse_hip_policy * policy);
+
+/* ------------------------------------------------------------------------ */
+/* Factories.  Replace trellis_sparse_vulkan_backend_create                  */
+/* (src/ops/sparse/trellis_sparse_backend.h:210) with the same contract:     */
+/* *out is NULL on failure; no usable device -> TRELLIS_STATUS_CUDA_UNAVAILABLE */
+/* (the reference's "device absent" code, trellis_sparse_vulkan.c:4017-4019). */
+/* ------------------------------------------------------------------------ */
+trellis_status trellis_sparse_hip_backend_create(int device, trellis_sparse_backend ** out);
+trellis_status trellis_sparse_hip_backend_create_ex(int device, const trellis_sparse_hip_policy * policy,
+                                                    trellis_sparse_backend ** out);
+
+/* Number of visible HIP devices (0 when none or when the runtime is absent). */
+int trellis_sparse_hip_device_count(void);
+
+/* Message for the last failing call on this backend ("" if none).  Valid until the next call. */
+const char * trellis_sparse_hip_last_error(const trellis_sparse_backend * backend);
+
+/* Waits for all work queued by this backend. */
+trellis_status trellis_sparse_hip_synchronize(trellis_sparse_backend * backend);
+
+/* ------------------------------------------------------------------------ */
+/* Inspection (no counterpart in the reference vtable; used by parity tests */
+/* and the benchmark).  All downloads are synchronous.                       */
+/* ------------------------------------------------------------------------ */
+
+/* Voxel count, valid (in,out) pairs including the centre (downloads the 27
+ * per-offset counts, synchronising), hash slots and occupied bricks. */
+trellis_status trellis_sparse_hip_rulebook_stats(trellis_sparse_backend * backend,
+                                                 const trellis_sparse_rulebook * rulebook, int64_t * n,
+                                                 int64_t * pairs, int64_t * table_slots, int64_t * bricks);
+
+/* Neighbour table, int32 [n][27]: nbr[i][k] is the row of the voxel at
+ * (b, x+kd-1, y+kh-1, z+kw-1), k = kd*9 + kh*3 + kw, or -1.  Coordinates wrap
+ * modulo 2^16 exactly as the reference key packing does
+ * (trellis_sparse_cpu.c:24-31). */
+trellis_status trellis_sparse_hip_download_neighbors(trellis_sparse_backend * backend,
+                                                     const trellis_sparse_rulebook * rulebook,
+                                                     int32_t * nbr_out, int64_t n);
+
+/* Per-offset pair lists in canonical order: offset-major, destination row
+ * ascending within an offset.  counts_out[27] receives the per-offset counts;
+ * src_out/dst_out receive sum(counts) entries (capacity given in entries). */
+trellis_status trellis_sparse_hip_download_pairs(trellis_sparse_backend * backend,
+                                                 const trellis_sparse_rulebook * rulebook, int64_t * counts_out,
+                                                 int32_t * src_out, int32_t * dst_out, int64_t capacity);
+
+/* Storage-type I/O without conversion: count elements of the backend's
+ * compute_dtype (4 bytes for F32, 2 bytes for F16/BF16). */
+trellis_status trellis_sparse_hip_upload_raw(trellis_sparse_backend * backend, const void * src, size_t count,
+                                             trellis_sparse_buffer ** out);
+trellis_status trellis_sparse_hip_download_raw(trellis_sparse_backend * backend,
+                                               const trellis_sparse_buffer * src, void * dst, size_t count);
+
+/* ------------------------------------------------------------------------ */
+/* Device-resident coordinates and C2S map lifetime (no counterpart in the   */
+/* reference vtable, whose device maps live until destroy; the Vulkan        */
+/* backend keeps uploaded coordinates in a host-pointer cache instead,       */
+/* trellis_sparse_vulkan.c:2059-2096).                                       */
+/* ------------------------------------------------------------------------ */
+
+/* Uploads coordinates [n][4] into a backend-owned device map without parent /
+ * subidx arrays.  The map can be passed as coords_map to build_c2s_map_device
+ * and to build_rulebook_for_c2s_map, so a level's coordinates cross PCIe once.
+ * c2s_gather_device, skip_repeat_device and download_c2s_map reject it. */
+trellis_status trellis_sparse_hip_upload_coords(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                                                int64_t n, trellis_sparse_c2s_device_map ** map_out);
+
+/* Releases a device map early (otherwise it lives until destroy).  Rulebooks
+ * built from the map with build_rulebook_for_c2s_map borrow its coordinates and
+ * must be freed first. */
+trellis_status trellis_sparse_hip_free_c2s_map(trellis_sparse_backend * backend,
+                                               trellis_sparse_c2s_device_map * map);
+
+/* ------------------------------------------------------------------------ */
+/* Stage timing with HIP events recorded on the backend's own stream.        */
+/* ------------------------------------------------------------------------ */
+typedef enum trellis_sparse_hip_stage {
+    TRELLIS_SPARSE_HIP_STAGE_HASH = 0,      /* brick table + voxel pool build */
+    TRELLIS_SPARSE_HIP_STAGE_MAP = 1,       /* neighbour table + per-offset pair lists */
+    TRELLIS_SPARSE_HIP_STAGE_CONV = 2,      /* sparse_conv3d kernels */
+    TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE = 3, /* C2S count/scan/fill */
+    TRELLIS_SPARSE_HIP_STAGE_BROADCAST = 4, /* c2s_gather / skip_repeat */
+    TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE = 5, /* norms, SiLU, add, linear */
+    TRELLIS_SPARSE_HIP_STAGE_COUNT = 6
+} trellis_sparse_hip_stage;
+
+typedef struct trellis_sparse_hip_stage_times {
+    double ms[TRELLIS_SPARSE_HIP_STAGE_COUNT];       /* summed event time per stage */
+    int64_t launches[TRELLIS_SPARSE_HIP_STAGE_COUNT]; /* timed launches per stage */
+} trellis_sparse_hip_stage_times;
+
+/* Turns per-stage event bracketing on or off (off by default). */
+trellis_status trellis_sparse_hip_profile_enable(trellis_sparse_backend * backend, int enable);
+/* Synchronises, then returns the accumulated stage times; reset != 0 clears them. */
+trellis_status trellis_sparse_hip_profile_read(trellis_sparse_backend * backend,
+                                               trellis_sparse_hip_stage_times * out, int reset);
+
+/* Records event `slot` (0..15) on the backend stream; elapsed() synchronises on slot b. */
+trellis_status trellis_sparse_hip_event_record(trellis_sparse_backend * backend, int slot);
+trellis_status trellis_sparse_hip_event_elapsed(trellis_sparse_backend * backend, int slot_a, int slot_b,
+                                                float * ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRELLIS_SPARSE_HIP_H */

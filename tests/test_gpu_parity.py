@@ -1,0 +1,385 @@
+"""GPU parity: the HIP backend through the C ABI vs the CPU oracle.
+
+Bar: bit-exact for neighbour tables, pair lists, subdivide maps and copies;
+fp32 conv within 1e-5 (and checked bit-exact against the reference operation
+order); bf16/fp16 within 2e-2 with the oracle run on the same rounded inputs.
+Error measure: check_close of tests/test_sparse_decoder_backend.c:16-24,
+|a-b| <= tol * max(1, |a|, |b|).
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+import sparse_hip as sh
+import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+TOL = {sh.F32: 1e-5, sh.F16: 2e-2, sh.BF16: 2e-2}
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def max_rel_err(got, exp):
+    got = np.asarray(got, dtype=np.float64)
+    exp = np.asarray(exp, dtype=np.float64)
+    scale = np.maximum(1.0, np.maximum(np.abs(got), np.abs(exp)))
+    return float(np.max(np.abs(got - exp) / scale)) if got.size else 0.0
+
+
+@pytest.fixture(scope="module")
+def be32():
+    b = sh.Backend(0, sh.F32)
+    yield b
+    b.destroy()
+
+
+@pytest.fixture(scope="module")
+def be16():
+    b = sh.Backend(0, sh.F16)
+    yield b
+    b.destroy()
+
+
+@pytest.fixture(scope="module")
+def bebf():
+    b = sh.Backend(0, sh.BF16)
+    yield b
+    b.destroy()
+
+
+def backend_for(dtype, be32, be16, bebf):
+    return {sh.F32: be32, sh.F16: be16, sh.BF16: bebf}[dtype]
+
+
+# ------------------------------------------------------------ hash / kernel map
+
+def edge_coord_sets():
+    rng = np.random.default_rng(11)
+    dup = np.stack([rng.integers(0, 2, 700), rng.integers(-3, 9, 700), rng.integers(-3, 9, 700),
+                    rng.integers(-3, 9, 700)], 1).astype(np.int32)
+    dup[-40:] = dup[:40]  # later duplicates win
+    wrap = np.array([[0, 0, 5, 5], [0, 65535, 5, 5], [0, 1, 5, 5], [3, 65535, 65535, 65535], [3, 0, 0, 0]], np.int32)
+    single = np.array([[7, 100, 200, 300]], np.int32)
+    ragged = wl.make_coords(1)[:1000 + 37]
+    batches = wl.make_coords(5)[::7]
+    return {"duplicates": dup, "wrap": wrap, "single": single, "ragged": ragged, "batches": batches}
+
+
+@pytest.mark.parametrize("name", ["duplicates", "wrap", "single", "ragged", "batches"])
+def test_kernel_map_edge_cases_bitexact(be32, name):
+    c = edge_coord_sets()[name]
+    say(f"kernel map edge case {name}: n={c.shape[0]}")
+    rb = be32.build_rulebook(c)
+    exp = orc.Rulebook(c).neighbors()
+    got = be32.neighbors(rb)
+    assert np.array_equal(got, exp)
+    counts, src, dst = be32.pairs(rb)
+    ec, es, ed = orc.pairs(exp)
+    assert np.array_equal(counts, ec) and np.array_equal(src, es) and np.array_equal(dst, ed)
+    rb.free()
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 4, 5])
+def test_kernel_map_configs_bitexact(be32, cfg):
+    c = wl.make_coords(cfg)
+    say(f"kernel map cfg{cfg}: n={c.shape[0]}")
+    rb = be32.build_rulebook(c)
+    stats = be32.rulebook_stats(rb)
+    exp = orc.Rulebook(c).neighbors()
+    assert stats["pairs"] == int((exp >= 0).sum())
+    if cfg == 1:
+        assert stats["pairs"] == 261416
+    assert np.array_equal(be32.neighbors(rb), exp)
+    counts, src, dst = be32.pairs(rb)
+    ec, es, ed = orc.pairs(exp)
+    assert np.array_equal(counts, ec) and np.array_equal(src, es) and np.array_equal(dst, ed)
+    rb.free()
+
+
+def test_rulebook_rejects_bad_arguments(be32):
+    with pytest.raises(sh.HipError) as e:
+        be32.build_rulebook(np.zeros((0, 4), np.int32))
+    assert e.value.status == sh.INVALID_ARGUMENT
+
+
+def test_reject_duplicates_policy():
+    b = sh.Backend(0, sh.F32, reject_duplicates=True)
+    c = np.array([[0, 1, 1, 1], [0, 2, 2, 2], [0, 1, 1, 1]], np.int32)
+    with pytest.raises(sh.HipError) as e:
+        b.build_rulebook(c)
+    assert e.value.status == sh.INVALID_ARGUMENT
+    b.build_rulebook(c[:2]).free()
+    b.destroy()
+
+
+# ------------------------------------------------------------------------ conv
+
+def run_conv(be, coords, feats, w, bias, ci, co):
+    rb = be.build_rulebook(coords)
+    x = be.upload(feats)
+    y = be.alloc(coords.shape[0] * co)
+    be.conv(rb, x, w, bias, y, ci, co)
+    out = be.download(y).reshape(-1, co)
+    rb.free()
+    x.free()
+    y.free()
+    return out
+
+
+def small_conv_cases():
+    from test_oracle import reference_direct_case, reference_trellis_case
+
+    return {"direct": reference_direct_case(), "trellis": reference_trellis_case()}
+
+
+@pytest.mark.parametrize("name", ["direct", "trellis"])
+def test_conv_fp32_reference_inputs(be32, name):
+    coords, feats, w, bias, ci, co = small_conv_cases()[name]
+    got = run_conv(be32, coords, feats, w, bias, ci, co)
+    exp = orc.Rulebook(coords).conv(feats, w, bias, ci, co)
+    assert max_rel_err(got, exp) <= 1e-5
+    assert np.array_equal(got, exp), "fp32 generic path follows the reference operation order"
+
+
+def test_conv_fp32_config1_full(be32):
+    w = wl.workload(1)
+    c, x, wt = w["coords"], w["feats"], w["weight"]
+    rng = np.random.default_rng(1)
+    bias = rng.standard_normal(64).astype(np.float32) * 0.1
+    say(f"cfg1 fp32 conv n={c.shape[0]}")
+    got = run_conv(be32, c, x, wt, bias, 64, 64)
+    exp = orc.Rulebook(c).conv(x, wt, bias, 64, 64)
+    err = max_rel_err(got, exp)
+    say(f"cfg1 fp32 max_rel_err={err:.3e} bitexact={np.array_equal(got, exp)}")
+    assert err <= 1e-5
+    assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])
+@pytest.mark.parametrize("ci,co", [(64, 64), (128, 128), (256, 128), (32, 192)])
+def test_conv_mfma_vs_oracle(be32, be16, bebf, dtype, ci, co):
+    be = backend_for(dtype, be32, be16, bebf)
+    c = wl.make_coords(1)
+    rng = np.random.default_rng(ci + co + dtype)
+    x = sh.storage_round(rng.standard_normal((c.shape[0], ci)).astype(np.float32), dtype)
+    w = (rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci)).astype(np.float32)
+    bias = rng.standard_normal(co).astype(np.float32) * 0.1
+    wr = sh.storage_round(w, dtype)
+    got = run_conv(be, c, x, w, bias, ci, co)
+    exp = orc.Rulebook(c).conv(x, wr, bias, ci, co)
+    err = max_rel_err(got, exp)
+    say(f"mfma dtype={dtype} ci={ci} co={co} max_rel_err={err:.3e}")
+    assert err <= TOL[dtype]
+
+
+def test_conv_mfma_dense_block_vs_torch(bebf):
+    from test_oracle import dense_block, torch_dense_conv
+
+    coords, feats, w, bias, side = dense_block(side=12, ci=64, co=64, seed=3)
+    x = sh.bf16_round(feats)
+    wr = sh.bf16_round(w)
+    got = run_conv(bebf, coords, x, w, bias, 64, 64)
+    exp = torch_dense_conv(x, wr, bias, side)
+    err = max_rel_err(got, exp)
+    say(f"dense block bf16 vs torch conv3d max_rel_err={err:.3e}")
+    assert err <= 2e-2
+
+
+def test_conv_generic_small_channels_all_dtypes(be32, be16, bebf):
+    coords, feats, w, bias, ci, co = small_conv_cases()["direct"]
+    for dtype in (sh.F16, sh.BF16):
+        be = backend_for(dtype, be32, be16, bebf)
+        x = sh.storage_round(feats, dtype)
+        got = run_conv(be, coords, x, w, bias, ci, co)
+        exp = orc.Rulebook(coords).conv(x, w, bias, ci, co)
+        assert max_rel_err(got, exp) <= TOL[dtype]
+
+
+def test_conv_deterministic(bebf):
+    c = wl.make_coords(1)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((c.shape[0], 128)).astype(np.float32)
+    w = (rng.standard_normal((128, 27, 128)) * 0.02).astype(np.float32)
+    a = run_conv(bebf, c, x, w, None, 128, 128)
+    b = run_conv(bebf, c, x, w, None, 128, 128)
+    assert np.array_equal(a, b)
+
+
+def test_conv_argument_errors(be32):
+    c = wl.make_coords(1)[:100]
+    rb = be32.build_rulebook(c)
+    x = be32.upload(np.zeros((100, 8), np.float32))
+    y = be32.alloc(100 * 4)
+    w = np.zeros((4, 27, 8), np.float32)
+    with pytest.raises(sh.HipError) as e:
+        be32.conv(rb, x, w, None, y, 8, 5)  # output too small
+    assert e.value.status == sh.INVALID_ARGUMENT
+    with pytest.raises(sh.HipError):
+        be32.conv(rb, x, w, None, y, 9, 4)  # input too small
+    rb.free()
+
+
+def test_large_dispatch_centre_only(be32):
+    """tests/test_sparse_decoder_backend.c:461-590: 102x102x101 stride-2 grid (no
+    neighbours but the centre), centre-only weights, rows at the old grid limits."""
+    dx, dy, dz, ci, co = 102, 102, 101, 3, 2
+    n = dx * dy * dz
+    iz, iy, ix = np.meshgrid(np.arange(dz), np.arange(dy), np.arange(dx), indexing="ij")
+    coords = np.stack([np.zeros(n, np.int32), (ix * 2).ravel(), (iy * 2).ravel(), (iz * 2).ravel()], 1).astype(np.int32)
+    r = np.arange(n)
+    x = np.stack([np.sin((r % 997) * 0.013 + c * 0.17) + 0.001 * ((r + c * 11) % 23) for c in range(ci)],
+                 1).astype(np.float32)
+    w = np.zeros((co, 27, ci), np.float32)
+    for o in range(co):
+        for i in range(ci):
+            w[o, 13, i] = 0.07 * (o + 1) - 0.03 * i
+    bias = np.array([-0.05, 0.15], np.float32)
+    got = run_conv(be32, coords, x, w, bias, ci, co)
+    for row in (0, 1, 65535 * 16 - 1, 65535 * 16, n - 1):
+        exp = bias + x[row].astype(np.float64) @ w[:, 13, :].T
+        assert max_rel_err(got[row], exp) <= 2e-4
+
+
+# -------------------------------------------------------------------- subdivide
+
+def test_c2s_known_answer_host_and_device(be32):
+    from test_oracle import c2s_kat
+
+    coords, subdiv, ec, ep, es = c2s_kat()
+    lg = be32.upload(subdiv)
+    oc, op, os_ = be32.build_c2s_map(coords, lg)
+    assert np.array_equal(oc, ec) and np.array_equal(op, ep) and np.array_equal(os_, es)
+    dm = be32.build_c2s_map_device(lg, 4, coords=coords)
+    assert dm.n == 6
+    c2, p2, s2 = be32.download_c2s_map(dm)
+    assert np.array_equal(c2, ec) and np.array_equal(p2, ep) and np.array_equal(s2, es)
+    assert np.array_equal(be32.download_c2s_coords(dm), ec)
+    # A second level can take the first level's device map as its coordinates.
+    lg2 = be32.upload(np.where(np.arange(48).reshape(6, 8) % 3 == 0, 1.0, -1.0).astype(np.float32))
+    dm2 = be32.build_c2s_map_device(lg2, 6, coords_map=dm)
+    rc, e2c, e2p, e2s = orc.c2s_map(ec, np.where(np.arange(48).reshape(6, 8) % 3 == 0, 1.0, -1.0))
+    c3, p3, s3 = be32.download_c2s_map(dm2)
+    assert np.array_equal(c3, e2c) and np.array_equal(p3, e2p) and np.array_equal(s3, e2s)
+
+
+def test_c2s_no_children_is_error(be32):
+    lg = be32.upload(-np.ones((3, 8), np.float32))
+    with pytest.raises(sh.HipError) as e:
+        be32.build_c2s_map(np.zeros((3, 4), np.int32), lg)
+    assert e.value.status == sh.ERROR
+    with pytest.raises(sh.HipError) as e:
+        be32.build_c2s_map_device(lg, 3, coords=np.zeros((3, 4), np.int32))
+    assert e.value.status == sh.ERROR
+
+
+@pytest.mark.parametrize("dtype", [sh.F32, sh.BF16])
+def test_c2s_config3_full_pipeline(be32, be16, bebf, dtype):
+    be = backend_for(dtype, be32, be16, bebf)
+    w = wl.workload(3)
+    pc, logits, pf = w["parent_coords"], w["logits"], w["parent_feats"]
+    say(f"cfg3 pipeline dtype={dtype} parents={pc.shape[0]}")
+    rc, ec, ep, es = orc.c2s_map(pc, logits)
+    assert rc == 0
+    lg = be.upload(logits)
+    dm = be.build_c2s_map_device(lg, pc.shape[0], coords=pc)
+    assert dm.n == ec.shape[0]
+    c2, p2, s2 = be.download_c2s_map(dm)
+    assert np.array_equal(c2, ec) and np.array_equal(p2, ep) and np.array_equal(s2, es)
+    rb = be.build_rulebook_for_c2s_map(dm)
+    exp_nbr = orc.Rulebook(ec).neighbors()
+    assert np.array_equal(be.neighbors(rb), exp_nbr)
+    # Broadcast parent features to the children, then conv 256 -> 128.
+    xr = sh.storage_round(pf, dtype)
+    xp = be.upload(xr)
+    xc = be.alloc(dm.n * 256)
+    be.skip_repeat_device(xp, dm, xc, 256, 256)
+    child = be.download(xc).reshape(-1, 256)
+    exp_child = orc.skip_repeat(xr, ep, es, 256, 256)
+    assert np.array_equal(child, exp_child)
+    y = be.alloc(dm.n * 128)
+    be.conv(rb, xc, w["weight"], None, y, 256, 128)
+    got = be.download(y).reshape(-1, 128)
+    rows = (5, dm.n, 61)
+    exp = orc.Rulebook(ec).conv(exp_child, sh.storage_round(w["weight"], dtype), None, 256, 128, rows=rows)
+    err = max_rel_err(got[rows[0]:rows[1]:rows[2]], exp)
+    say(f"cfg3 conv dtype={dtype} max_rel_err={err:.3e} on {exp.shape[0]} rows")
+    assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [sh.F32, sh.F16, sh.BF16])
+@pytest.mark.parametrize("ci,co", [(256, 256), (3, 2), (16, 24), (128, 64)])
+def test_broadcasts_bitexact(be32, be16, bebf, dtype, ci, co):
+    be = backend_for(dtype, be32, be16, bebf)
+    rng = np.random.default_rng(ci * 7 + co)
+    npar, m = 50, 300
+    parent = np.sort(rng.integers(0, npar, m)).astype(np.int32)
+    sub = rng.integers(0, 8, m).astype(np.int32)
+    x = sh.storage_round(rng.standard_normal((npar, ci)), dtype)
+    xb = be.upload(x)
+    y = be.alloc(m * co)
+    be.skip_repeat(xb, parent, sub, y, ci, co)
+    assert np.array_equal(be.download(y).reshape(m, co), orc.skip_repeat(x, parent, sub, ci, co))
+    x8 = sh.storage_round(rng.standard_normal((npar, 8 * co)), dtype)
+    x8b = be.upload(x8)
+    be.c2s_gather(x8b, parent, sub, y, co)
+    assert np.array_equal(be.download(y).reshape(m, co), orc.c2s_gather(x8, parent, sub, co))
+
+
+def test_broadcast_rejects_out_of_range_parent(be32):
+    x = be32.upload(np.zeros((4, 8), np.float32))
+    y = be32.alloc(2 * 8)
+    with pytest.raises(sh.HipError):
+        be32.skip_repeat(x, [0, 4], [0, 1], y, 8, 8)
+
+
+# --------------------------------------------------------------------- row ops
+
+@pytest.mark.parametrize("dtype", [sh.F32, sh.BF16])
+def test_row_ops(be32, be16, bebf, dtype):
+    be = backend_for(dtype, be32, be16, bebf)
+    rng = np.random.default_rng(8)
+    n, c = 1031, 128
+    x = sh.storage_round(rng.standard_normal((n, c)) * 2 + 0.5, dtype)
+    g = rng.standard_normal(c).astype(np.float32)
+    b = rng.standard_normal(c).astype(np.float32)
+    xb = be.upload(x)
+    yb = be.alloc(n * c)
+    tol = TOL[dtype]
+    for silu in (False, True):
+        for gg, bb in ((g, b), (None, None)):
+            be.row_norm(xb, gg, bb, yb, n, c, 1e-6, silu=silu)
+            assert max_rel_err(be.download(yb), orc.row_norm(x, gg, bb, n, c, 1e-6, silu)) <= tol
+    be.silu_inplace(xb, n * c)
+    assert max_rel_err(be.download(xb), orc.silu(x)) <= tol
+    a = be.upload(x)
+    bb_ = be.upload(sh.storage_round(x * 0.5, dtype))
+    be.add(a, bb_, yb, n * c)
+    assert max_rel_err(be.download(yb), orc.add(x, sh.storage_round(x * 0.5, dtype))) <= tol
+    w = (rng.standard_normal((48, c)) * 0.1).astype(np.float32)
+    bias = rng.standard_normal(48).astype(np.float32)
+    y2 = be.alloc(n * 48)
+    for silu in (False, True):
+        be.linear(a, w, bias, y2, n, c, 48, silu=silu)
+        exp = orc.linear(x, w, bias, n, c, 48, silu)
+        got = be.download(y2)
+        assert max_rel_err(got, exp) <= tol
+        if dtype == sh.F32:
+            assert np.array_equal(got.reshape(n, 48), exp)
+
+
+def test_trim_releases_and_weights_reload(be32):
+    coords, feats, w, bias, ci, co = small_conv_cases()["direct"]
+    a = run_conv(be32, coords, feats, w, bias, ci, co)
+    released = be32.trim(sh.TRIM_FREE_BUFFERS | sh.TRIM_WEIGHTS)
+    assert released > 0
+    b = run_conv(be32, coords, feats, w, bias, ci, co)
+    assert np.array_equal(a, b)
+    with pytest.raises(sh.HipError):
+        be32.trim(8)

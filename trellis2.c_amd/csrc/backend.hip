@@ -1,0 +1,1326 @@
+// backend.hip - trellis_sparse_backend_ops implementation for MI355X (gfx950).
+//
+// Host side of the drop-in backend: argument and status contract of the
+// reference CPU backend (src/ops/sparse/trellis_sparse_cpu.c), device buffer
+// pool, weight cache keyed by host pointer (the Vulkan backend's contract,
+// src/ops/sparse/trellis_sparse_vulkan.c:1019-1052), device-resident C2S maps
+// (vtable slots 18-25, src/ops/sparse/trellis_sparse_backend.h:119-182) and
+// stage timing with HIP events on the backend's stream.
+//
+// Threading: one backend instance is single-threaded, like the reference
+// backends (trellis_sparse_vulkan.c:163-187); separate instances are
+// independent.  Every call enqueues on the instance's own stream; calls that
+// hand data back to the host (download_*, build_c2s_map*, n_out) synchronise.
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+
+#include "tsh_internal.h"
+
+namespace tsh {
+
+struct WeightKey {
+    const void * ptr;
+    size_t count;
+    int layout;
+    int ci, co;
+    bool operator==(const WeightKey & o) const {
+        return ptr == o.ptr && count == o.count && layout == o.layout && ci == o.ci && co == o.co;
+    }
+};
+struct WeightKeyHash {
+    size_t operator()(const WeightKey & k) const {
+        return std::hash<const void *>()(k.ptr) ^ (k.count * 0x9e3779b97f4a7c15ull) ^ ((size_t) k.layout << 56) ^
+               ((size_t) k.ci << 20) ^ (size_t) k.co;
+    }
+};
+
+enum WeightLayout : int {
+    kLayoutConvF32 = 1,   // fp32 [27][ci][co]
+    kLayoutConvMfma = 2,  // storage type [27][ci/8][co][8]
+    kLayoutLinearT = 3,   // fp32 [ci][co]
+    kLayoutVector = 4     // fp32 [count]
+};
+
+struct StageMark {
+    hipEvent_t a = nullptr, b = nullptr;
+    int stage = 0;
+};
+
+struct Backend {
+    trellis_sparse_backend base;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    trellis_sparse_hip_policy policy{};
+    std::string last_error;
+    // Pool: size class -> free device blocks.
+    std::map<size_t, std::vector<void *>> free_blocks;
+    size_t pooled_bytes = 0;
+    // Weight cache.
+    std::unordered_map<WeightKey, DevMem, WeightKeyHash> weights;
+    std::vector<DevMem> transient;  // uncached weights of the current call
+    // Device C2S maps (valid until destroy).
+    std::vector<trellis_sparse_c2s_device_map *> maps;
+    // Timing.
+    bool profiling = false;
+    std::vector<StageMark> pending;
+    std::vector<hipEvent_t> spare_events;
+    trellis_sparse_hip_stage_times times{};
+    hipEvent_t user_events[16] = {};
+    StageMark open[TRELLIS_SPARSE_HIP_STAGE_COUNT];
+};
+
+namespace {
+
+Backend * as_backend(trellis_sparse_backend * b) { return reinterpret_cast<Backend *>(b); }
+const Backend * as_backend(const trellis_sparse_backend * b) { return reinterpret_cast<const Backend *>(b); }
+
+trellis_status fail(Backend * be, trellis_status st, const char * what) {
+    if (be != nullptr) be->last_error = what;
+    return st;
+}
+
+trellis_status hip_status(Backend * be, hipError_t err, const char * where) {
+    if (err == hipSuccess) return TRELLIS_STATUS_OK;
+    if (be != nullptr) {
+        be->last_error = std::string(where) + ": " + hipGetErrorString(err);
+    }
+    (void) hipGetLastError();
+    return err == hipErrorOutOfMemory ? TRELLIS_STATUS_OUT_OF_MEMORY : TRELLIS_STATUS_ERROR;
+}
+
+#define TSH_TRY(be, expr)                                            \
+    do {                                                             \
+        const hipError_t tsh_err_ = (expr);                          \
+        if (tsh_err_ != hipSuccess) return hip_status(be, tsh_err_, #expr); \
+    } while (0)
+
+size_t size_class(size_t bytes) {
+    if (bytes <= 4096) return 4096;
+    // Four classes per power of two (at most 25% slack).
+    size_t p = 4096;
+    while (p * 2 < bytes) p *= 2;
+    const size_t step = p / 4;
+    return (bytes + step - 1) / step * step;
+}
+
+trellis_status dev_alloc(Backend * be, size_t bytes, DevMem * out) {
+    out->ptr = nullptr;
+    out->bytes = 0;
+    if (bytes == 0) return TRELLIS_STATUS_OK;
+    const size_t cls = size_class(bytes);
+    auto it = be->free_blocks.find(cls);
+    if (it != be->free_blocks.end() && !it->second.empty()) {
+        out->ptr = it->second.back();
+        it->second.pop_back();
+        be->pooled_bytes -= cls;
+        out->bytes = cls;
+        return TRELLIS_STATUS_OK;
+    }
+    void * p = nullptr;
+    hipError_t err = hipMalloc(&p, cls);
+    if (err == hipErrorOutOfMemory && be->pooled_bytes > 0) {
+        // Release cached blocks and retry once.
+        (void) hipGetLastError();
+        (void) hipStreamSynchronize(be->stream);
+        for (auto & kv : be->free_blocks) {
+            for (void * q : kv.second) (void) hipFree(q);
+            kv.second.clear();
+        }
+        be->pooled_bytes = 0;
+        err = hipMalloc(&p, cls);
+    }
+    if (err != hipSuccess) {
+        return hip_status(be, err, "hipMalloc");
+    }
+    out->ptr = p;
+    out->bytes = cls;
+    return TRELLIS_STATUS_OK;
+}
+
+// Returns a block to the pool.  Work already queued on the backend stream may
+// still use it; any later user is queued behind that work on the same stream.
+void dev_release(Backend * be, DevMem * m) {
+    if (m == nullptr || m->ptr == nullptr) return;
+    be->free_blocks[m->bytes].push_back(m->ptr);
+    be->pooled_bytes += m->bytes;
+    m->ptr = nullptr;
+    m->bytes = 0;
+}
+
+void select_device(Backend * be) { (void) hipSetDevice(be->device); }
+
+// ---- stage timing -----------------------------------------------------------
+hipEvent_t take_event(Backend * be) {
+    if (!be->spare_events.empty()) {
+        hipEvent_t e = be->spare_events.back();
+        be->spare_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) {
+        (void) hipGetLastError();
+        return nullptr;
+    }
+    return e;
+}
+
+void stage_begin(Backend * be, int stage) {
+    if (!be->profiling) return;
+    StageMark & m = be->open[stage];
+    m.stage = stage;
+    m.a = take_event(be);
+    m.b = take_event(be);
+    if (m.a != nullptr) (void) hipEventRecord(m.a, be->stream);
+}
+
+void stage_end(Backend * be, int stage) {
+    if (!be->profiling) return;
+    StageMark m = be->open[stage];
+    be->open[stage] = StageMark{};
+    if (m.a == nullptr || m.b == nullptr) return;
+    (void) hipEventRecord(m.b, be->stream);
+    be->pending.push_back(m);
+}
+
+// ---- buffers ---------------------------------------------------------------
+trellis_status new_buffer(Backend * be, size_t count, int dtype, trellis_sparse_buffer ** out) {
+    const size_t elem = dtype < 0 ? 4u : dtype_bytes(dtype);
+    if (count > SIZE_MAX / elem) return fail(be, TRELLIS_STATUS_OUT_OF_MEMORY, "buffer size overflow");
+    auto * b = (trellis_sparse_buffer *) calloc(1, sizeof(trellis_sparse_buffer));
+    if (b == nullptr) return fail(be, TRELLIS_STATUS_OUT_OF_MEMORY, "host allocation");
+    DevMem m;
+    const trellis_status st = dev_alloc(be, count * elem, &m);
+    if (st != TRELLIS_STATUS_OK) {
+        free(b);
+        return st;
+    }
+    b->ptr = m.ptr;
+    b->count = count;
+    b->bytes = count * elem;
+    b->cap = m.bytes;
+    b->dtype = dtype;
+    *out = b;
+    return TRELLIS_STATUS_OK;
+}
+
+bool float_buffer_ok(const Backend * be, const trellis_sparse_buffer * b, size_t need) {
+    return b != nullptr && b->dtype == be->policy.compute_dtype && b->count >= need && (need == 0 || b->ptr != nullptr);
+}
+
+// Uploads host bytes to a device block through the backend stream and waits,
+// so the caller's memory may be reused on return.
+trellis_status upload_bytes(Backend * be, const void * src, size_t bytes, DevMem * out) {
+    trellis_status st = dev_alloc(be, bytes, out);
+    if (st != TRELLIS_STATUS_OK) return st;
+    if (bytes == 0) return TRELLIS_STATUS_OK;
+    TSH_TRY(be, hipMemcpyAsync(out->ptr, src, bytes, hipMemcpyHostToDevice, be->stream));
+    TSH_TRY(be, hipStreamSynchronize(be->stream));
+    return TRELLIS_STATUS_OK;
+}
+
+// ---- weight / vector cache ---------------------------------------------------
+trellis_status get_weight(Backend * be, const float * host, size_t count, int layout, int ci, int co,
+                          const void ** dev_out) {
+    *dev_out = nullptr;
+    if (host == nullptr) return TRELLIS_STATUS_OK;
+    const WeightKey key{host, count, layout, ci, co};
+    if (be->policy.cache_weights) {
+        auto it = be->weights.find(key);
+        if (it != be->weights.end()) {
+            *dev_out = it->second.ptr;
+            return TRELLIS_STATUS_OK;
+        }
+    }
+    std::vector<unsigned char> staged;
+    const int dt = be->policy.compute_dtype;
+    switch (layout) {
+        case kLayoutConvF32: {  // [co][27][ci] -> [27][ci][co]
+            staged.resize((size_t) 27 * ci * co * sizeof(float));
+            float * w = (float *) staged.data();
+            for (int o = 0; o < co; ++o)
+                for (int k = 0; k < 27; ++k)
+                    for (int c = 0; c < ci; ++c)
+                        w[((size_t) k * ci + c) * co + o] = host[((size_t) o * 27 + k) * ci + c];
+            break;
+        }
+        case kLayoutConvMfma: {  // [co][27][ci] -> [27][ci/8][co][8] in the storage type
+            const size_t elems = (size_t) 27 * ci * co;
+            staged.resize(elems * 2);
+            uint16_t * w = (uint16_t *) staged.data();
+            const int ci8 = ci / 8;
+            for (int o = 0; o < co; ++o)
+                for (int k = 0; k < 27; ++k)
+                    for (int c = 0; c < ci; ++c) {
+                        const float v = host[((size_t) o * 27 + k) * ci + c];
+                        uint16_t h;
+                        if (dt == kBF16) {
+                            h = f32_to_bf16(v);
+                        } else {
+                            const _Float16 f = (_Float16) v;
+                            memcpy(&h, &f, 2);
+                        }
+                        w[((((size_t) k * ci8 + c / 8) * co + o) * 8) + (c & 7)] = h;
+                    }
+            break;
+        }
+        case kLayoutLinearT: {  // [co][ci] -> [ci][co]
+            staged.resize((size_t) ci * co * sizeof(float));
+            float * w = (float *) staged.data();
+            for (int o = 0; o < co; ++o)
+                for (int c = 0; c < ci; ++c) w[(size_t) c * co + o] = host[(size_t) o * ci + c];
+            break;
+        }
+        case kLayoutVector: {
+            staged.resize(count * sizeof(float));
+            memcpy(staged.data(), host, count * sizeof(float));
+            break;
+        }
+        default:
+            return fail(be, TRELLIS_STATUS_ERROR, "unknown weight layout");
+    }
+    DevMem m;
+    const trellis_status st = upload_bytes(be, staged.data(), staged.size(), &m);
+    if (st != TRELLIS_STATUS_OK) return st;
+    if (be->policy.cache_weights) {
+        be->weights[key] = m;
+    } else {
+        be->transient.push_back(m);
+    }
+    *dev_out = m.ptr;
+    return TRELLIS_STATUS_OK;
+}
+
+void end_call(Backend * be) {
+    for (DevMem & m : be->transient) dev_release(be, &m);
+    be->transient.clear();
+}
+
+struct CallScope {
+    Backend * be;
+    explicit CallScope(Backend * b) : be(b) { select_device(b); }
+    ~CallScope() { end_call(be); }
+};
+
+// ---- ops ---------------------------------------------------------------------
+void op_destroy(trellis_sparse_backend * backend);
+
+trellis_status op_alloc_f32(trellis_sparse_backend * backend, size_t count, trellis_sparse_buffer ** out) {
+    if (backend == nullptr || out == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    *out = nullptr;
+    Backend * be = as_backend(backend);
+    CallScope scope(be);
+    return new_buffer(be, count, be->policy.compute_dtype, out);
+}
+
+trellis_status op_upload_f32(trellis_sparse_backend * backend, const float * src, size_t count,
+                             trellis_sparse_buffer ** out) {
+    if (backend == nullptr || out == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    *out = nullptr;
+    if (src == nullptr && count != 0) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    CallScope scope(be);
+    const int dt = be->policy.compute_dtype;
+    trellis_sparse_buffer * b = nullptr;
+    trellis_status st = new_buffer(be, count, dt, &b);
+    if (st != TRELLIS_STATUS_OK) return st;
+    if (count != 0) {
+        if (dt == kF32) {
+            hipError_t err = hipMemcpyAsync(b->ptr, src, count * 4, hipMemcpyHostToDevice, be->stream);
+            if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
+            st = hip_status(be, err, "upload_f32");
+        } else {
+            DevMem tmp;
+            st = upload_bytes(be, src, count * 4, &tmp);
+            if (st == TRELLIS_STATUS_OK) {
+                st = hip_status(be, launch_convert_from_f32(dt, (const float *) tmp.ptr, b->ptr, (int64_t) count, be->stream),
+                                "convert_from_f32");
+            }
+            dev_release(be, &tmp);
+        }
+    }
+    if (st != TRELLIS_STATUS_OK) {
+        DevMem m{b->ptr, b->cap};
+        dev_release(be, &m);
+        free(b);
+        return st;
+    }
+    *out = b;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_upload_i32(trellis_sparse_backend * backend, const int32_t * src, size_t count,
+                             trellis_sparse_buffer ** out) {
+    if (backend == nullptr || out == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    *out = nullptr;
+    if (src == nullptr && count != 0) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    CallScope scope(be);
+    trellis_sparse_buffer * b = nullptr;
+    trellis_status st = new_buffer(be, count, -1, &b);
+    if (st != TRELLIS_STATUS_OK) return st;
+    if (count != 0) {
+        hipError_t err = hipMemcpyAsync(b->ptr, src, count * 4, hipMemcpyHostToDevice, be->stream);
+        if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
+        st = hip_status(be, err, "upload_i32");
+        if (st != TRELLIS_STATUS_OK) {
+            DevMem m{b->ptr, b->cap};
+            dev_release(be, &m);
+            free(b);
+            return st;
+        }
+    }
+    *out = b;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_download_f32(trellis_sparse_backend * backend, const trellis_sparse_buffer * src, float * dst,
+                               size_t count) {
+    if (backend == nullptr || src == nullptr || dst == nullptr || count > src->count) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    Backend * be = as_backend(backend);
+    CallScope scope(be);
+    if (count == 0) return TRELLIS_STATUS_OK;
+    if (src->dtype == kF32 || src->dtype < 0) {
+        TSH_TRY(be, hipMemcpyAsync(dst, src->ptr, count * 4, hipMemcpyDeviceToHost, be->stream));
+        TSH_TRY(be, hipStreamSynchronize(be->stream));
+        return TRELLIS_STATUS_OK;
+    }
+    DevMem tmp;
+    trellis_status st = dev_alloc(be, count * 4, &tmp);
+    if (st != TRELLIS_STATUS_OK) return st;
+    hipError_t err = launch_convert_to_f32(src->dtype, src->ptr, (float *) tmp.ptr, (int64_t) count, be->stream);
+    if (err == hipSuccess) err = hipMemcpyAsync(dst, tmp.ptr, count * 4, hipMemcpyDeviceToHost, be->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
+    dev_release(be, &tmp);
+    return hip_status(be, err, "download_f32");
+}
+
+void op_free_buffer(trellis_sparse_backend * backend, trellis_sparse_buffer * buffer) {
+    if (backend == nullptr || buffer == nullptr) return;
+    Backend * be = as_backend(backend);
+    DevMem m{buffer->ptr, buffer->cap};
+    dev_release(be, &m);
+    free(buffer);
+}
+
+trellis_status linear_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * weight,
+                           const float * bias, trellis_sparse_buffer * y, int64_t n, int ci, int co, int silu) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (weight == nullptr || n <= 0 || ci <= 0 || co <= 0 || !float_buffer_ok(be, x, (size_t) n * ci) ||
+        !float_buffer_ok(be, y, (size_t) n * co)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "linear: bad argument");
+    }
+    CallScope scope(be);
+    const void * wt = nullptr;
+    const void * bd = nullptr;
+    trellis_status st = get_weight(be, weight, (size_t) ci * co, kLayoutLinearT, ci, co, &wt);
+    if (st == TRELLIS_STATUS_OK) st = get_weight(be, bias, (size_t) co, kLayoutVector, 0, co, &bd);
+    if (st != TRELLIS_STATUS_OK) return st;
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+    const hipError_t err = launch_linear(be->policy.compute_dtype, x->ptr, (const float *) wt, (const float *) bd,
+                                         y->ptr, n, ci, co, silu, be->stream);
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+    return hip_status(be, err, "linear");
+}
+
+trellis_status op_linear(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * weight,
+                         const float * bias, trellis_sparse_buffer * y, int64_t n, int ci, int co) {
+    return linear_impl(backend, x, weight, bias, y, n, ci, co, 0);
+}
+
+trellis_status op_linear_silu(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * weight,
+                              const float * bias, trellis_sparse_buffer * y, int64_t n, int ci, int co) {
+    return linear_impl(backend, x, weight, bias, y, n, ci, co, 1);
+}
+
+trellis_status norm_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * gamma,
+                         const float * beta, trellis_sparse_buffer * y, int64_t n, int c, float eps, int silu) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (n <= 0 || c <= 0 || !(eps > 0.0f) || !float_buffer_ok(be, x, (size_t) n * c) ||
+        !float_buffer_ok(be, y, (size_t) n * c)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "row_norm: bad argument");
+    }
+    CallScope scope(be);
+    const void * g = nullptr;
+    const void * b = nullptr;
+    trellis_status st = get_weight(be, gamma, (size_t) c, kLayoutVector, 0, c, &g);
+    if (st == TRELLIS_STATUS_OK) st = get_weight(be, beta, (size_t) c, kLayoutVector, 0, c, &b);
+    if (st != TRELLIS_STATUS_OK) return st;
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+    const hipError_t err = launch_row_norm(be->policy.compute_dtype, x->ptr, (const float *) g, (const float *) b,
+                                           y->ptr, n, c, eps, silu, be->stream);
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+    return hip_status(be, err, "row_norm");
+}
+
+trellis_status op_row_norm(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * gamma,
+                           const float * beta, trellis_sparse_buffer * y, int64_t n, int c, float eps) {
+    return norm_impl(backend, x, gamma, beta, y, n, c, eps, 0);
+}
+
+trellis_status op_row_norm_silu(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                const float * gamma, const float * beta, trellis_sparse_buffer * y, int64_t n, int c,
+                                float eps) {
+    return norm_impl(backend, x, gamma, beta, y, n, c, eps, 1);
+}
+
+trellis_status op_silu_inplace(trellis_sparse_backend * backend, trellis_sparse_buffer * x, size_t count) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (!float_buffer_ok(be, x, count)) return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "silu: bad argument");
+    CallScope scope(be);
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+    const hipError_t err = launch_silu(be->policy.compute_dtype, x->ptr, (int64_t) count, be->stream);
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+    return hip_status(be, err, "silu");
+}
+
+trellis_status op_add(trellis_sparse_backend * backend, const trellis_sparse_buffer * a,
+                      const trellis_sparse_buffer * b, trellis_sparse_buffer * y, size_t count) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (!float_buffer_ok(be, a, count) || !float_buffer_ok(be, b, count) || !float_buffer_ok(be, y, count)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "add: bad argument");
+    }
+    CallScope scope(be);
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+    const hipError_t err = launch_add(be->policy.compute_dtype, a->ptr, b->ptr, y->ptr, (int64_t) count, be->stream);
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+    return hip_status(be, err, "add");
+}
+
+// ---- rulebook -------------------------------------------------------------------
+void rulebook_release(Backend * be, trellis_sparse_rulebook * r) {
+    if (r == nullptr) return;
+    DevMem * mems[] = {&r->coords_mem, &r->bkeys, &r->bidx, &r->pool, &r->counters, &r->nbr, &r->mask,
+                       &r->tile_counts, &r->tile_off, &r->k_count, &r->pair_src, &r->pair_dst};
+    for (DevMem * m : mems) dev_release(be, m);
+    delete r;
+}
+
+int64_t next_pow2(int64_t v) {
+    int64_t p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+// Builds the brick hash and the kernel map for device coordinates `coords`.
+trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64_t n, trellis_sparse_rulebook * r) {
+    r->n = n;
+    r->coords = const_cast<int32_t *>(coords);
+    r->table_slots = std::max<int64_t>(64, next_pow2(2 * n));
+    r->n_tiles = (n + kMapTile - 1) / kMapTile;
+    const size_t slots = (size_t) r->table_slots;
+    struct Need {
+        DevMem * m;
+        size_t bytes;
+    } need[] = {
+        {&r->bkeys, slots * 8},
+        {&r->bidx, slots * 4},
+        {&r->pool, (size_t) n * kBrickCells * 4},
+        {&r->counters, 64},
+        {&r->nbr, (size_t) n * 27 * 4},
+        {&r->mask, (size_t) n * 4},
+        {&r->tile_counts, (size_t) r->n_tiles * 27 * 4},
+        {&r->tile_off, (size_t) r->n_tiles * 27 * 4},
+        {&r->k_count, 27 * 4},
+        {&r->pair_src, (size_t) n * 27 * 4},
+        {&r->pair_dst, (size_t) n * 27 * 4},
+    };
+    for (const Need & q : need) {
+        const trellis_status st = dev_alloc(be, q.bytes, q.m);
+        if (st != TRELLIS_STATUS_OK) return st;
+    }
+    hipStream_t s = be->stream;
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_HASH);
+    TSH_TRY(be, launch_fill_u64((uint64_t *) r->bkeys.ptr, r->table_slots, 0ull, s));
+    TSH_TRY(be, launch_fill_i32((int32_t *) r->counters.ptr, 16, 0, s));
+    TSH_TRY(be, launch_brick_insert(coords, n, (uint64_t *) r->bkeys.ptr, (int32_t *) r->bidx.ptr, r->table_slots,
+                                    (int32_t *) r->counters.ptr, s));
+    TSH_TRY(be, launch_pool_init((int32_t *) r->pool.ptr, (const int32_t *) r->counters.ptr, n * kBrickCells, s));
+    TSH_TRY(be, launch_voxel_insert(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
+                                    r->table_slots, (int32_t *) r->pool.ptr, (int32_t *) r->counters.ptr, s));
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_HASH);
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
+    TSH_TRY(be, launch_neighbors(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
+                                 r->table_slots, (const int32_t *) r->pool.ptr, (int32_t *) r->nbr.ptr,
+                                 (uint32_t *) r->mask.ptr, (int32_t *) r->tile_counts.ptr, s));
+    TSH_TRY(be, launch_tile_scan((const int32_t *) r->tile_counts.ptr, r->n_tiles, (int32_t *) r->tile_off.ptr,
+                                 (int32_t *) r->k_count.ptr, s));
+    TSH_TRY(be, launch_fill_pairs((const int32_t *) r->nbr.ptr, (const uint32_t *) r->mask.ptr, n,
+                                  (const int32_t *) r->tile_off.ptr, (int32_t *) r->pair_src.ptr,
+                                  (int32_t *) r->pair_dst.ptr, s));
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
+    if (be->policy.reject_duplicates) {
+        int32_t flags[4] = {0, 0, 0, 0};
+        TSH_TRY(be, hipMemcpyAsync(flags, r->counters.ptr, sizeof(flags), hipMemcpyDeviceToHost, s));
+        TSH_TRY(be, hipStreamSynchronize(s));
+        if (flags[1] != 0) return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "build_rulebook: duplicate coordinates");
+    }
+    return TRELLIS_STATUS_OK;
+}
+
+bool n_ok(int64_t n) { return n > 0 && n <= (int64_t) (INT32_MAX / 27); }
+
+trellis_status op_build_rulebook(trellis_sparse_backend * backend, const int32_t * coords_bxyz, int64_t n,
+                                 trellis_sparse_rulebook ** out) {
+    if (backend == nullptr || coords_bxyz == nullptr || out == nullptr || n <= 0) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    *out = nullptr;
+    Backend * be = as_backend(backend);
+    if (!n_ok(n)) return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "build_rulebook: n*27 must fit int32");
+    CallScope scope(be);
+    auto * r = new (std::nothrow) trellis_sparse_rulebook();
+    if (r == nullptr) return TRELLIS_STATUS_OUT_OF_MEMORY;
+    trellis_status st = upload_bytes(be, coords_bxyz, (size_t) n * 16, &r->coords_mem);
+    if (st == TRELLIS_STATUS_OK) st = rulebook_build_device(be, (const int32_t *) r->coords_mem.ptr, n, r);
+    if (st != TRELLIS_STATUS_OK) {
+        rulebook_release(be, r);
+        return st;
+    }
+    *out = r;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                                const trellis_sparse_buffer * feats, const float * weight, const float * bias,
+                                trellis_sparse_buffer * out, int64_t n, int ci, int co) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (rulebook == nullptr || weight == nullptr || n <= 0 || ci <= 0 || co <= 0 || n != rulebook->n ||
+        !float_buffer_ok(be, feats, (size_t) n * ci) || !float_buffer_ok(be, out, (size_t) n * co)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "sparse_conv3d: bad argument");
+    }
+    CallScope scope(be);
+    const int dt = be->policy.compute_dtype;
+    int algo = be->policy.conv_algo;
+    if (algo == TRELLIS_SPARSE_HIP_CONV_AUTO || algo == TRELLIS_SPARSE_HIP_CONV_COMPACT) {
+        algo = conv_mfma_supported(dt, ci, co) ? TRELLIS_SPARSE_HIP_CONV_MASKED : TRELLIS_SPARSE_HIP_CONV_GENERIC;
+    }
+    if (algo == TRELLIS_SPARSE_HIP_CONV_MASKED && !conv_mfma_supported(dt, ci, co)) {
+        algo = TRELLIS_SPARSE_HIP_CONV_GENERIC;
+    }
+    const void * bd = nullptr;
+    trellis_status st = get_weight(be, bias, (size_t) co, kLayoutVector, 0, co, &bd);
+    if (st != TRELLIS_STATUS_OK) return st;
+    const size_t wcount = (size_t) co * 27 * ci;
+    hipError_t err;
+    if (algo == TRELLIS_SPARSE_HIP_CONV_MASKED) {
+        const void * w = nullptr;
+        st = get_weight(be, weight, wcount, kLayoutConvMfma, ci, co, &w);
+        if (st != TRELLIS_STATUS_OK) return st;
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
+        err = launch_conv_mfma_masked(dt, feats->ptr, (const int32_t *) rulebook->nbr.ptr,
+                                      (const uint32_t *) rulebook->mask.ptr, w, (const float *) bd, out->ptr, n, ci,
+                                      co, be->stream);
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
+    } else {
+        const void * w = nullptr;
+        st = get_weight(be, weight, wcount, kLayoutConvF32, ci, co, &w);
+        if (st != TRELLIS_STATUS_OK) return st;
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
+        err = launch_conv_generic(dt, feats->ptr, (const int32_t *) rulebook->nbr.ptr, (const float *) w,
+                                  (const float *) bd, out->ptr, n, ci, co, be->stream);
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
+    }
+    return hip_status(be, err, "sparse_conv3d");
+}
+
+void op_free_rulebook(trellis_sparse_backend * backend, trellis_sparse_rulebook * rulebook) {
+    if (backend == nullptr || rulebook == nullptr) return;
+    rulebook_release(as_backend(backend), rulebook);
+}
+
+// ---- subdivide (C2S) --------------------------------------------------------------
+trellis_status upload_index_pair(Backend * be, const int32_t * a, const int32_t * b, int64_t n, DevMem * da,
+                                 DevMem * db) {
+    trellis_status st = upload_bytes(be, a, (size_t) n * 4, da);
+    if (st == TRELLIS_STATUS_OK) st = upload_bytes(be, b, (size_t) n * 4, db);
+    return st;
+}
+
+trellis_status op_c2s_gather(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                             const int32_t * parent, const int32_t * subidx, trellis_sparse_buffer * y, int64_t n_out,
+                             int co) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (x == nullptr || y == nullptr || parent == nullptr || subidx == nullptr || n_out <= 0 || co <= 0 ||
+        !float_buffer_ok(be, y, (size_t) n_out * co) || x->dtype != be->policy.compute_dtype || x->ptr == nullptr) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "c2s_gather: bad argument");
+    }
+    CallScope scope(be);
+    // Every parent index must address a row of x ([n_parent][8*co]).
+    const int64_t x_rows = (int64_t) (x->count / ((size_t) co * 8));
+    for (int64_t r = 0; r < n_out; ++r) {
+        if (parent[r] < 0 || parent[r] >= x_rows || subidx[r] < 0 || subidx[r] > 7) {
+            return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "c2s_gather: parent/subidx out of range");
+        }
+    }
+    DevMem dp, ds;
+    trellis_status st = upload_index_pair(be, parent, subidx, n_out, &dp, &ds);
+    if (st == TRELLIS_STATUS_OK) {
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+        st = hip_status(be, launch_c2s_gather(be->policy.compute_dtype, x->ptr, (const int32_t *) dp.ptr,
+                                              (const int32_t *) ds.ptr, y->ptr, n_out, co, be->stream),
+                        "c2s_gather");
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+    }
+    dev_release(be, &dp);
+    dev_release(be, &ds);
+    return st;
+}
+
+trellis_status op_skip_repeat(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                              const int32_t * parent, const int32_t * subidx, trellis_sparse_buffer * y,
+                              int64_t n_out, int ci, int co) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (x == nullptr || y == nullptr || parent == nullptr || subidx == nullptr || n_out <= 0 || ci <= 0 || co <= 0 ||
+        !float_buffer_ok(be, y, (size_t) n_out * co) || x->dtype != be->policy.compute_dtype || x->ptr == nullptr) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "skip_repeat: bad argument");
+    }
+    CallScope scope(be);
+    const int64_t x_rows = (int64_t) (x->count / (size_t) ci);
+    for (int64_t r = 0; r < n_out; ++r) {
+        if (parent[r] < 0 || parent[r] >= x_rows || subidx[r] < 0 || subidx[r] > 7) {
+            return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "skip_repeat: parent/subidx out of range");
+        }
+    }
+    DevMem dp, ds;
+    trellis_status st = upload_index_pair(be, parent, subidx, n_out, &dp, &ds);
+    if (st == TRELLIS_STATUS_OK) {
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+        st = hip_status(be, launch_skip_repeat(be->policy.compute_dtype, x->ptr, (const int32_t *) dp.ptr,
+                                               (const int32_t *) ds.ptr, y->ptr, n_out, ci, co, be->stream),
+                        "skip_repeat");
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+    }
+    dev_release(be, &dp);
+    dev_release(be, &ds);
+    return st;
+}
+
+void map_release(Backend * be, trellis_sparse_c2s_device_map * m) {
+    if (m == nullptr) return;
+    dev_release(be, &m->coords);
+    dev_release(be, &m->parent);
+    dev_release(be, &m->subidx);
+    delete m;
+}
+
+bool map_known(const Backend * be, const trellis_sparse_c2s_device_map * m) {
+    return m != nullptr && std::find(be->maps.begin(), be->maps.end(), m) != be->maps.end();
+}
+
+// Count -> exclusive scan -> fill, with the child total read back once.
+trellis_status c2s_build(Backend * be, const int32_t * coords_dev, const trellis_sparse_buffer * logits, int64_t n,
+                         trellis_sparse_c2s_device_map ** map_out) {
+    *map_out = nullptr;
+    DevMem counts, offsets, total, tmp;
+    hipStream_t s = be->stream;
+    trellis_status st = dev_alloc(be, (size_t) n * 4, &counts);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) n * 4, &offsets);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, 16, &total);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, scan_tmp_bytes(n), &tmp);
+    int32_t m = 0;
+    if (st == TRELLIS_STATUS_OK) {
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
+        hipError_t err = launch_c2s_count(be->policy.compute_dtype, logits->ptr, n, (int32_t *) counts.ptr, s);
+        if (err == hipSuccess) {
+            err = launch_scan_exclusive((const int32_t *) counts.ptr, (int32_t *) offsets.ptr, n,
+                                        (int32_t *) total.ptr, tmp.ptr, s);
+        }
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
+        if (err == hipSuccess) err = hipMemcpyAsync(&m, total.ptr, 4, hipMemcpyDeviceToHost, s);
+        if (err == hipSuccess) err = hipStreamSynchronize(s);
+        st = hip_status(be, err, "c2s count/scan");
+    }
+    if (st == TRELLIS_STATUS_OK && m <= 0) {
+        st = fail(be, TRELLIS_STATUS_ERROR, "subdivide produced no children (all logits <= 0)");
+    }
+    trellis_sparse_c2s_device_map * map = nullptr;
+    if (st == TRELLIS_STATUS_OK) {
+        map = new (std::nothrow) trellis_sparse_c2s_device_map();
+        if (map == nullptr) st = TRELLIS_STATUS_OUT_OF_MEMORY;
+    }
+    if (st == TRELLIS_STATUS_OK) {
+        map->n = m;
+        map->n_parent = n;
+        st = dev_alloc(be, (size_t) m * 16, &map->coords);
+        if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) m * 4, &map->parent);
+        if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) m * 4, &map->subidx);
+    }
+    if (st == TRELLIS_STATUS_OK) {
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
+        st = hip_status(be,
+                        launch_c2s_fill(be->policy.compute_dtype, coords_dev, logits->ptr,
+                                        (const int32_t *) offsets.ptr, n, (int32_t *) map->coords.ptr,
+                                        (int32_t *) map->parent.ptr, (int32_t *) map->subidx.ptr, s),
+                        "c2s_fill");
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
+    }
+    dev_release(be, &counts);
+    dev_release(be, &offsets);
+    dev_release(be, &total);
+    dev_release(be, &tmp);
+    if (st != TRELLIS_STATUS_OK) {
+        map_release(be, map);
+        return st;
+    }
+    *map_out = map;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_build_c2s_map(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                                const trellis_sparse_buffer * logits, int64_t n, int32_t ** coords_out,
+                                int32_t ** parent_out, int32_t ** subidx_out, int64_t * n_out) {
+    if (backend == nullptr || coords_bxyz == nullptr || coords_out == nullptr || parent_out == nullptr ||
+        subidx_out == nullptr || n_out == nullptr || n <= 0) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    *coords_out = nullptr;
+    *parent_out = nullptr;
+    *subidx_out = nullptr;
+    *n_out = 0;
+    Backend * be = as_backend(backend);
+    if (!float_buffer_ok(be, logits, (size_t) n * 8) || n > INT32_MAX / 8) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "build_c2s_map: bad argument");
+    }
+    CallScope scope(be);
+    DevMem cd;
+    trellis_status st = upload_bytes(be, coords_bxyz, (size_t) n * 16, &cd);
+    trellis_sparse_c2s_device_map * map = nullptr;
+    if (st == TRELLIS_STATUS_OK) st = c2s_build(be, (const int32_t *) cd.ptr, logits, n, &map);
+    dev_release(be, &cd);
+    if (st != TRELLIS_STATUS_OK) return st;
+    const int64_t m = map->n;
+    int32_t * hc = (int32_t *) malloc((size_t) m * 16);
+    int32_t * hp = (int32_t *) malloc((size_t) m * 4);
+    int32_t * hs = (int32_t *) malloc((size_t) m * 4);
+    if (hc == nullptr || hp == nullptr || hs == nullptr) {
+        st = TRELLIS_STATUS_OUT_OF_MEMORY;
+    } else {
+        hipError_t err = hipMemcpyAsync(hc, map->coords.ptr, (size_t) m * 16, hipMemcpyDeviceToHost, be->stream);
+        if (err == hipSuccess) err = hipMemcpyAsync(hp, map->parent.ptr, (size_t) m * 4, hipMemcpyDeviceToHost, be->stream);
+        if (err == hipSuccess) err = hipMemcpyAsync(hs, map->subidx.ptr, (size_t) m * 4, hipMemcpyDeviceToHost, be->stream);
+        if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
+        st = hip_status(be, err, "build_c2s_map download");
+    }
+    map_release(be, map);
+    if (st != TRELLIS_STATUS_OK) {
+        free(hc);
+        free(hp);
+        free(hs);
+        return st;
+    }
+    *coords_out = hc;
+    *parent_out = hp;
+    *subidx_out = hs;
+    *n_out = m;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_alias_c2s_map(trellis_sparse_backend * backend, const int32_t * coords_bxyz, const int32_t * parent,
+                                const int32_t * subidx, int64_t n, const int32_t * alias_coords_bxyz,
+                                const int32_t * alias_parent, const int32_t * alias_subidx) {
+    // A cache hint in the Vulkan backend (trellis_sparse_vulkan.c:2849-2878).
+    // This backend keeps no host-pointer cache, so there is nothing to alias.
+    if (backend == nullptr || coords_bxyz == nullptr || parent == nullptr || subidx == nullptr ||
+        alias_coords_bxyz == nullptr || alias_parent == nullptr || alias_subidx == nullptr || n <= 0) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_build_c2s_map_device(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                                       const trellis_sparse_c2s_device_map * coords_map,
+                                       const trellis_sparse_buffer * logits, int64_t n,
+                                       trellis_sparse_c2s_device_map ** map_out, int64_t * n_out) {
+    if (backend == nullptr || map_out == nullptr || n_out == nullptr || (coords_bxyz == nullptr && coords_map == nullptr) ||
+        n <= 0) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    *map_out = nullptr;
+    *n_out = 0;
+    Backend * be = as_backend(backend);
+    if (!float_buffer_ok(be, logits, (size_t) n * 8) || n > INT32_MAX / 8) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "build_c2s_map_device: bad argument");
+    }
+    if (coords_map != nullptr && (!map_known(be, coords_map) || coords_map->n != n)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "build_c2s_map_device: unknown coords_map or n mismatch");
+    }
+    CallScope scope(be);
+    DevMem cd;
+    const int32_t * coords_dev = nullptr;
+    trellis_status st = TRELLIS_STATUS_OK;
+    if (coords_map != nullptr) {
+        coords_dev = (const int32_t *) coords_map->coords.ptr;
+    } else {
+        st = upload_bytes(be, coords_bxyz, (size_t) n * 16, &cd);
+        coords_dev = (const int32_t *) cd.ptr;
+    }
+    trellis_sparse_c2s_device_map * map = nullptr;
+    if (st == TRELLIS_STATUS_OK) st = c2s_build(be, coords_dev, logits, n, &map);
+    dev_release(be, &cd);
+    if (st != TRELLIS_STATUS_OK) return st;
+    be->maps.push_back(map);
+    *map_out = map;
+    *n_out = map->n;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_build_rulebook_for_c2s_map(trellis_sparse_backend * backend,
+                                             const trellis_sparse_c2s_device_map * map, trellis_sparse_rulebook ** out) {
+    if (backend == nullptr || out == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    *out = nullptr;
+    Backend * be = as_backend(backend);
+    if (!map_known(be, map)) return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "build_rulebook_for_c2s_map: unknown map");
+    if (!n_ok(map->n)) return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "build_rulebook_for_c2s_map: n too large");
+    CallScope scope(be);
+    auto * r = new (std::nothrow) trellis_sparse_rulebook();
+    if (r == nullptr) return TRELLIS_STATUS_OUT_OF_MEMORY;
+    // The map owns the coordinates and outlives the rulebook (maps live until destroy).
+    const trellis_status st = rulebook_build_device(be, (const int32_t *) map->coords.ptr, map->n, r);
+    if (st != TRELLIS_STATUS_OK) {
+        rulebook_release(be, r);
+        return st;
+    }
+    *out = r;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_c2s_gather_device(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                    const trellis_sparse_c2s_device_map * map, trellis_sparse_buffer * y,
+                                    int64_t n_out, int co) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (!map_known(be, map) || map->parent.ptr == nullptr || x == nullptr || x->dtype != be->policy.compute_dtype ||
+        x->ptr == nullptr || n_out != map->n || co <= 0 || !float_buffer_ok(be, y, (size_t) n_out * co) ||
+        x->count < (size_t) map->n_parent * 8u * (size_t) co) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "c2s_gather_device: bad argument");
+    }
+    CallScope scope(be);
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+    const hipError_t err = launch_c2s_gather(be->policy.compute_dtype, x->ptr, (const int32_t *) map->parent.ptr,
+                                             (const int32_t *) map->subidx.ptr, y->ptr, n_out, co, be->stream);
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+    return hip_status(be, err, "c2s_gather_device");
+}
+
+trellis_status op_skip_repeat_device(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                     const trellis_sparse_c2s_device_map * map, trellis_sparse_buffer * y,
+                                     int64_t n_out, int ci, int co) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (!map_known(be, map) || map->parent.ptr == nullptr || x == nullptr || x->dtype != be->policy.compute_dtype ||
+        x->ptr == nullptr || n_out != map->n || ci <= 0 || co <= 0 || !float_buffer_ok(be, y, (size_t) n_out * co) ||
+        x->count < (size_t) map->n_parent * (size_t) ci) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "skip_repeat_device: bad argument");
+    }
+    CallScope scope(be);
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+    const hipError_t err = launch_skip_repeat(be->policy.compute_dtype, x->ptr, (const int32_t *) map->parent.ptr,
+                                              (const int32_t *) map->subidx.ptr, y->ptr, n_out, ci, co, be->stream);
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+    return hip_status(be, err, "skip_repeat_device");
+}
+
+trellis_status op_download_c2s_coords(trellis_sparse_backend * backend, const trellis_sparse_c2s_device_map * map,
+                                      int32_t * coords_out, int64_t n) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (!map_known(be, map) || coords_out == nullptr || n != map->n) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "download_c2s_coords: bad argument");
+    }
+    CallScope scope(be);
+    TSH_TRY(be, hipMemcpyAsync(coords_out, map->coords.ptr, (size_t) n * 16, hipMemcpyDeviceToHost, be->stream));
+    TSH_TRY(be, hipStreamSynchronize(be->stream));
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_download_c2s_map(trellis_sparse_backend * backend, const trellis_sparse_c2s_device_map * map,
+                                   int32_t * coords_out, int32_t * parent_out, int32_t * subidx_out, int64_t n) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (!map_known(be, map) || map->parent.ptr == nullptr || coords_out == nullptr || parent_out == nullptr ||
+        subidx_out == nullptr || n != map->n) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "download_c2s_map: bad argument");
+    }
+    CallScope scope(be);
+    TSH_TRY(be, hipMemcpyAsync(coords_out, map->coords.ptr, (size_t) n * 16, hipMemcpyDeviceToHost, be->stream));
+    TSH_TRY(be, hipMemcpyAsync(parent_out, map->parent.ptr, (size_t) n * 4, hipMemcpyDeviceToHost, be->stream));
+    TSH_TRY(be, hipMemcpyAsync(subidx_out, map->subidx.ptr, (size_t) n * 4, hipMemcpyDeviceToHost, be->stream));
+    TSH_TRY(be, hipStreamSynchronize(be->stream));
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_trim(trellis_sparse_backend * backend, unsigned flags, size_t * released_bytes) {
+    if (released_bytes != nullptr) *released_bytes = 0;
+    if (backend == nullptr || (flags & ~(unsigned) TRELLIS_SPARSE_TRIM_ALL) != 0) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    if (flags == 0) return TRELLIS_STATUS_OK;
+    Backend * be = as_backend(backend);
+    CallScope scope(be);
+    TSH_TRY(be, hipStreamSynchronize(be->stream));
+    size_t released = 0;
+    if (flags & TRELLIS_SPARSE_TRIM_WEIGHTS) {
+        for (auto & kv : be->weights) {
+            released += kv.second.bytes;
+            (void) hipFree(kv.second.ptr);
+        }
+        be->weights.clear();
+    }
+    if (flags & TRELLIS_SPARSE_TRIM_FREE_BUFFERS) {
+        for (auto & kv : be->free_blocks) {
+            for (void * p : kv.second) {
+                (void) hipFree(p);
+                released += kv.first;
+            }
+        }
+        be->free_blocks.clear();
+        be->pooled_bytes = 0;
+    }
+    if (released_bytes != nullptr) *released_bytes = released;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status op_naf(trellis_sparse_backend *, const float *, const float *, const float *, const int32_t *, int64_t,
+                      const struct trellis_pixal_camera *, const struct trellis_pixal_naf_attention_desc *, float *,
+                      size_t) {
+    // Pixal3D NAF attention is not part of the sparse-convolution path.
+    return TRELLIS_STATUS_NOT_IMPLEMENTED;
+}
+
+const trellis_sparse_backend_ops g_ops = {
+    op_destroy,
+    op_alloc_f32,
+    op_upload_f32,
+    op_upload_i32,
+    op_download_f32,
+    op_free_buffer,
+    op_linear,
+    op_linear_silu,
+    op_row_norm,
+    op_row_norm_silu,
+    op_silu_inplace,
+    op_add,
+    op_build_rulebook,
+    op_sparse_conv3d,
+    op_free_rulebook,
+    op_c2s_gather,
+    op_skip_repeat,
+    op_build_c2s_map,
+    op_alias_c2s_map,
+    op_build_c2s_map_device,
+    op_build_rulebook_for_c2s_map,
+    op_c2s_gather_device,
+    op_skip_repeat_device,
+    op_download_c2s_coords,
+    op_download_c2s_map,
+    op_trim,
+    op_naf,
+};
+
+void op_destroy(trellis_sparse_backend * backend) {
+    if (backend == nullptr) return;
+    Backend * be = as_backend(backend);
+    select_device(be);
+    (void) hipStreamSynchronize(be->stream);
+    for (auto * m : be->maps) map_release(be, m);
+    be->maps.clear();
+    for (auto & kv : be->weights) dev_release(be, &kv.second);
+    be->weights.clear();
+    for (auto & kv : be->free_blocks)
+        for (void * p : kv.second) (void) hipFree(p);
+    for (auto & m : be->pending) {
+        (void) hipEventDestroy(m.a);
+        (void) hipEventDestroy(m.b);
+    }
+    for (hipEvent_t e : be->spare_events) (void) hipEventDestroy(e);
+    for (hipEvent_t e : be->user_events)
+        if (e != nullptr) (void) hipEventDestroy(e);
+    (void) hipStreamDestroy(be->stream);
+    delete be;
+}
+
+}  // namespace
+}  // namespace tsh
+
+using tsh::Backend;
+
+extern "C" {
+
+void trellis_sparse_hip_policy_init(trellis_sparse_hip_policy * policy) {
+    if (policy == nullptr) return;
+    memset(policy, 0, sizeof(*policy));
+    policy->struct_size = sizeof(*policy);
+    policy->compute_dtype = TRELLIS_SPARSE_HIP_F32;
+    policy->conv_algo = TRELLIS_SPARSE_HIP_CONV_AUTO;
+    policy->cache_weights = 1;
+    policy->reject_duplicates = 0;
+}
+
+int trellis_sparse_hip_device_count(void) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess) {
+        (void) hipGetLastError();
+        return 0;
+    }
+    return count;
+}
+
+trellis_status trellis_sparse_hip_backend_create_ex(int device, const trellis_sparse_hip_policy * policy,
+                                                    trellis_sparse_backend ** out) {
+    if (out == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    *out = nullptr;
+    trellis_sparse_hip_policy p;
+    trellis_sparse_hip_policy_init(&p);
+    if (policy != nullptr) {
+        if (policy->struct_size != sizeof(trellis_sparse_hip_policy)) return TRELLIS_STATUS_INVALID_ARGUMENT;
+        p = *policy;
+    }
+    if (p.compute_dtype < TRELLIS_SPARSE_HIP_F32 || p.compute_dtype > TRELLIS_SPARSE_HIP_BF16 ||
+        p.conv_algo < TRELLIS_SPARSE_HIP_CONV_AUTO || p.conv_algo > TRELLIS_SPARSE_HIP_CONV_COMPACT) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    const int count = trellis_sparse_hip_device_count();
+    if (device < 0 || device >= count) return TRELLIS_STATUS_CUDA_UNAVAILABLE;
+    if (hipSetDevice(device) != hipSuccess) {
+        (void) hipGetLastError();
+        return TRELLIS_STATUS_CUDA_UNAVAILABLE;
+    }
+    auto * be = new (std::nothrow) Backend();
+    if (be == nullptr) return TRELLIS_STATUS_OUT_OF_MEMORY;
+    if (hipStreamCreateWithFlags(&be->stream, hipStreamNonBlocking) != hipSuccess) {
+        (void) hipGetLastError();
+        delete be;
+        return TRELLIS_STATUS_CUDA_UNAVAILABLE;
+    }
+    be->base.ops = &tsh::g_ops;
+    be->base.kind = TRELLIS_SPARSE_BACKEND_HIP;
+    be->base.device = device;
+    be->device = device;
+    be->policy = p;
+    *out = &be->base;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_backend_create(int device, trellis_sparse_backend ** out) {
+    return trellis_sparse_hip_backend_create_ex(device, nullptr, out);
+}
+
+const char * trellis_sparse_hip_last_error(const trellis_sparse_backend * backend) {
+    if (backend == nullptr) return "";
+    return tsh::as_backend(backend)->last_error.c_str();
+}
+
+trellis_status trellis_sparse_hip_synchronize(trellis_sparse_backend * backend) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = tsh::as_backend(backend);
+    tsh::select_device(be);
+    return tsh::hip_status(be, hipStreamSynchronize(be->stream), "synchronize");
+}
+
+trellis_status trellis_sparse_hip_rulebook_stats(trellis_sparse_backend * backend,
+                                                 const trellis_sparse_rulebook * rulebook, int64_t * n,
+                                                 int64_t * pairs, int64_t * table_slots, int64_t * bricks) {
+    if (backend == nullptr || rulebook == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = tsh::as_backend(backend);
+    tsh::select_device(be);
+    int32_t counts[27];
+    int32_t ctr[4];
+    hipError_t err = hipMemcpyAsync(counts, rulebook->k_count.ptr, sizeof(counts), hipMemcpyDeviceToHost, be->stream);
+    if (err == hipSuccess) err = hipMemcpyAsync(ctr, rulebook->counters.ptr, sizeof(ctr), hipMemcpyDeviceToHost, be->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
+    if (err != hipSuccess) return tsh::hip_status(be, err, "rulebook_stats");
+    int64_t total = 0;
+    for (int k = 0; k < 27; ++k) total += counts[k];
+    if (n != nullptr) *n = rulebook->n;
+    if (pairs != nullptr) *pairs = total;
+    if (table_slots != nullptr) *table_slots = rulebook->table_slots;
+    if (bricks != nullptr) *bricks = ctr[0];
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_download_neighbors(trellis_sparse_backend * backend,
+                                                     const trellis_sparse_rulebook * rulebook, int32_t * nbr_out,
+                                                     int64_t n) {
+    if (backend == nullptr || rulebook == nullptr || nbr_out == nullptr || n != rulebook->n) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    Backend * be = tsh::as_backend(backend);
+    tsh::select_device(be);
+    hipError_t err = hipMemcpyAsync(nbr_out, rulebook->nbr.ptr, (size_t) n * 27 * 4, hipMemcpyDeviceToHost, be->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
+    return tsh::hip_status(be, err, "download_neighbors");
+}
+
+trellis_status trellis_sparse_hip_download_pairs(trellis_sparse_backend * backend,
+                                                 const trellis_sparse_rulebook * rulebook, int64_t * counts_out,
+                                                 int32_t * src_out, int32_t * dst_out, int64_t capacity) {
+    if (backend == nullptr || rulebook == nullptr || counts_out == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = tsh::as_backend(backend);
+    tsh::select_device(be);
+    int32_t counts[27];
+    hipError_t err = hipMemcpyAsync(counts, rulebook->k_count.ptr, sizeof(counts), hipMemcpyDeviceToHost, be->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
+    if (err != hipSuccess) return tsh::hip_status(be, err, "download_pairs");
+    int64_t total = 0;
+    for (int k = 0; k < 27; ++k) {
+        counts_out[k] = counts[k];
+        total += counts[k];
+    }
+    if (src_out == nullptr && dst_out == nullptr) return TRELLIS_STATUS_OK;
+    if (total > capacity) return tsh::fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "download_pairs: capacity too small");
+    int64_t at = 0;
+    const int64_t n = rulebook->n;
+    for (int k = 0; k < 27 && err == hipSuccess; ++k) {
+        const size_t bytes = (size_t) counts[k] * 4;
+        if (bytes == 0) continue;
+        if (src_out != nullptr) {
+            err = hipMemcpyAsync(src_out + at, (const int32_t *) rulebook->pair_src.ptr + (int64_t) k * n, bytes,
+                                 hipMemcpyDeviceToHost, be->stream);
+        }
+        if (err == hipSuccess && dst_out != nullptr) {
+            err = hipMemcpyAsync(dst_out + at, (const int32_t *) rulebook->pair_dst.ptr + (int64_t) k * n, bytes,
+                                 hipMemcpyDeviceToHost, be->stream);
+        }
+        at += counts[k];
+    }
+    if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
+    return tsh::hip_status(be, err, "download_pairs");
+}
+
+trellis_status trellis_sparse_hip_upload_raw(trellis_sparse_backend * backend, const void * src, size_t count,
+                                             trellis_sparse_buffer ** out) {
+    if (backend == nullptr || out == nullptr || (src == nullptr && count != 0)) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    *out = nullptr;
+    Backend * be = tsh::as_backend(backend);
+    tsh::select_device(be);
+    trellis_sparse_buffer * b = nullptr;
+    trellis_status st = tsh::new_buffer(be, count, be->policy.compute_dtype, &b);
+    if (st != TRELLIS_STATUS_OK) return st;
+    if (count != 0) {
+        hipError_t err = hipMemcpyAsync(b->ptr, src, b->bytes, hipMemcpyHostToDevice, be->stream);
+        if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
+        st = tsh::hip_status(be, err, "upload_raw");
+    }
+    if (st != TRELLIS_STATUS_OK) {
+        tsh::op_free_buffer(backend, b);
+        return st;
+    }
+    *out = b;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_download_raw(trellis_sparse_backend * backend, const trellis_sparse_buffer * src,
+                                               void * dst, size_t count) {
+    if (backend == nullptr || src == nullptr || dst == nullptr || count > src->count) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    Backend * be = tsh::as_backend(backend);
+    tsh::select_device(be);
+    const size_t elem = src->dtype < 0 ? 4u : tsh::dtype_bytes(src->dtype);
+    hipError_t err = hipMemcpyAsync(dst, src->ptr, count * elem, hipMemcpyDeviceToHost, be->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
+    return tsh::hip_status(be, err, "download_raw");
+}
+
+trellis_status trellis_sparse_hip_upload_coords(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                                                int64_t n, trellis_sparse_c2s_device_map ** map_out) {
+    if (backend == nullptr || coords_bxyz == nullptr || map_out == nullptr || n <= 0) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    *map_out = nullptr;
+    Backend * be = tsh::as_backend(backend);
+    if (!tsh::n_ok(n)) return tsh::fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "upload_coords: n too large");
+    tsh::select_device(be);
+    auto * map = new (std::nothrow) trellis_sparse_c2s_device_map();
+    if (map == nullptr) return TRELLIS_STATUS_OUT_OF_MEMORY;
+    map->n = n;
+    const trellis_status st = tsh::upload_bytes(be, coords_bxyz, (size_t) n * 16, &map->coords);
+    if (st != TRELLIS_STATUS_OK) {
+        tsh::map_release(be, map);
+        return st;
+    }
+    be->maps.push_back(map);
+    *map_out = map;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_free_c2s_map(trellis_sparse_backend * backend, trellis_sparse_c2s_device_map * map) {
+    if (backend == nullptr || map == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = tsh::as_backend(backend);
+    auto it = std::find(be->maps.begin(), be->maps.end(), map);
+    if (it == be->maps.end()) return tsh::fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "free_c2s_map: unknown map");
+    be->maps.erase(it);
+    tsh::select_device(be);
+    tsh::map_release(be, map);
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_profile_enable(trellis_sparse_backend * backend, int enable) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    tsh::as_backend(backend)->profiling = enable != 0;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_profile_read(trellis_sparse_backend * backend, trellis_sparse_hip_stage_times * out,
+                                               int reset) {
+    if (backend == nullptr || out == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = tsh::as_backend(backend);
+    tsh::select_device(be);
+    const hipError_t err = hipStreamSynchronize(be->stream);
+    if (err != hipSuccess) return tsh::hip_status(be, err, "profile_read");
+    for (auto & m : be->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, m.a, m.b) == hipSuccess) {
+            be->times.ms[m.stage] += ms;
+            be->times.launches[m.stage] += 1;
+        } else {
+            (void) hipGetLastError();
+        }
+        be->spare_events.push_back(m.a);
+        be->spare_events.push_back(m.b);
+    }
+    be->pending.clear();
+    *out = be->times;
+    if (reset) be->times = trellis_sparse_hip_stage_times{};
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_event_record(trellis_sparse_backend * backend, int slot) {
+    if (backend == nullptr || slot < 0 || slot >= 16) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = tsh::as_backend(backend);
+    tsh::select_device(be);
+    if (be->user_events[slot] == nullptr) {
+        const hipError_t err = hipEventCreate(&be->user_events[slot]);
+        if (err != hipSuccess) return tsh::hip_status(be, err, "event_create");
+    }
+    return tsh::hip_status(be, hipEventRecord(be->user_events[slot], be->stream), "event_record");
+}
+
+trellis_status trellis_sparse_hip_event_elapsed(trellis_sparse_backend * backend, int slot_a, int slot_b, float * ms) {
+    if (backend == nullptr || ms == nullptr || slot_a < 0 || slot_a >= 16 || slot_b < 0 || slot_b >= 16) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    Backend * be = tsh::as_backend(backend);
+    tsh::select_device(be);
+    if (be->user_events[slot_a] == nullptr || be->user_events[slot_b] == nullptr) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    hipError_t err = hipEventSynchronize(be->user_events[slot_b]);
+    if (err == hipSuccess) err = hipEventElapsedTime(ms, be->user_events[slot_a], be->user_events[slot_b]);
+    return tsh::hip_status(be, err, "event_elapsed");
+}
+
+}  // extern "C"

@@ -1,0 +1,410 @@
+// kernels_map.hip - GPU voxel hash and 3x3x3 submanifold kernel map for gfx950.
+//
+// Reference semantics (src/ops/sparse/trellis_sparse_cpu.c):
+//   key packing with 16-bit fields  :24-31   (coordinates wrap modulo 2^16)
+//   last duplicate wins             :314-318
+//   neighbour (b, x+kd-1, y+kh-1, z+kw-1), k = kd*9+kh*3+kw, never across b  :348-358
+//
+// Layout in HBM (all sized from n, no host synchronisation):
+//   brick table  uint64 keys[slots] + int32 idx[slots], slots = nextpow2(2n).
+//                Key = (b:16 | x>>2:14 | y>>2:14 | z>>2:14) + 1, 0 = empty,
+//                linear probing from splitmix64(key).
+//   voxel pool   int32 [bricks][64]: row of the voxel at cell (x&3)|(y&3)<<2|(z&3)<<4, -1 = empty.
+//   nbr          int32 [n][27]
+//   mask         uint32 [n], bit k <=> nbr[i][k] >= 0
+//   tile_counts  int32 [n_tiles][27] valid pairs per 256-row tile and offset
+//   pairs        int32 src/dst [27][n], offset k in [k*n, k*n + count_k), dst ascending.
+//
+// A voxel's 27 neighbours lie in at most 8 bricks (on average 3.4), so the
+// kernel map does a few hash probes per voxel plus 27 reads from 256-byte
+// brick rows that neighbouring lanes share, instead of 27 random probes.
+#include "tsh_internal.h"
+
+namespace tsh {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ uint64_t mix64(uint64_t v) {
+    v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ull;
+    v = (v ^ (v >> 27)) * 0x94d049bb133111ebull;
+    return v ^ (v >> 31);
+}
+
+__device__ __forceinline__ uint64_t brick_key(uint32_t b, uint32_t bx, uint32_t by, uint32_t bz) {
+    return (((uint64_t) b << 42) | ((uint64_t) bx << 28) | ((uint64_t) by << 14) | (uint64_t) bz) + 1ull;
+}
+
+__device__ __forceinline__ int32_t brick_find(const uint64_t * __restrict__ bkeys, const int32_t * __restrict__ bidx,
+                                              uint64_t mask, uint64_t key) {
+    uint64_t s = mix64(key) & mask;
+    for (uint64_t step = 0; step <= mask; ++step) {
+        const uint64_t k = bkeys[s];
+        if (k == key) {
+            return bidx[s];
+        }
+        if (k == 0) {
+            return -1;
+        }
+        s = (s + 1) & mask;
+    }
+    return -1;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) v, lane);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) (v >> 32), lane);
+    return ((uint64_t) hi << 32) | lo;
+}
+
+__device__ __forceinline__ int lane_id() { return (int) __lane_id(); }
+
+__global__ void k_fill_u64(uint64_t * __restrict__ p, int64_t count, uint64_t value) {
+    const int64_t stride = (int64_t) gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+        p[i] = value;
+    }
+}
+
+__global__ void k_fill_i32(int32_t * __restrict__ p, int64_t count, int32_t value) {
+    const int64_t stride = (int64_t) gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+        p[i] = value;
+    }
+}
+
+// One lane per voxel.  Lanes of a wavefront first agree on one representative
+// per distinct brick (ballot/readlane, no memory traffic); representatives
+// then insert concurrently with a 64-bit CAS.  The lane that claims an empty
+// slot numbers the brick.
+__global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict__ coords, int64_t n,
+                                                         uint64_t * __restrict__ bkeys, int32_t * __restrict__ bidx,
+                                                         uint64_t mask, int32_t * __restrict__ counters) {
+    const int64_t i = (int64_t) blockIdx.x * kBlock + threadIdx.x;
+    const bool active = i < n;
+    uint64_t key = 0;
+    if (active) {
+        const int4 c = coords[i];
+        key = brick_key((uint32_t) c.x & 0xffffu, ((uint32_t) c.y & 0xffffu) >> 2, ((uint32_t) c.z & 0xffffu) >> 2,
+                        ((uint32_t) c.w & 0xffffu) >> 2);
+    }
+    const int lane = lane_id();
+    bool first = active;
+    uint64_t todo = __ballot(active);
+    while (todo != 0) {
+        const int leader = __builtin_ctzll(todo);
+        const uint64_t lk = readlane_u64(key, leader);
+        const uint64_t same = __ballot(active && key == lk);
+        if (lane != leader && ((same >> lane) & 1ull)) {
+            first = false;
+        }
+        todo &= ~same;
+    }
+    if (!first) {
+        return;
+    }
+    uint64_t s = mix64(key) & mask;
+    for (uint64_t step = 0; step <= mask; ++step) {
+        const uint64_t prev = atomicCAS((unsigned long long *) &bkeys[s], 0ull, (unsigned long long) key);
+        if (prev == 0) {
+            bidx[s] = atomicAdd(&counters[0], 1);
+            return;
+        }
+        if (prev == key) {
+            return;
+        }
+        s = (s + 1) & mask;
+    }
+    atomicOr(&counters[2], 1);  // table full; cannot happen with slots >= 2n
+}
+
+// Clears the pool cells of the bricks numbered so far (count read on device).
+__global__ void k_pool_init(int32_t * __restrict__ pool, const int32_t * __restrict__ counters, int64_t cap_cells) {
+    int64_t cells = (int64_t) counters[0] * kBrickCells;
+    if (cells > cap_cells) {
+        cells = cap_cells;
+    }
+    const int64_t stride = (int64_t) gridDim.x * blockDim.x * 4;
+    for (int64_t i = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) * 4; i < cells; i += stride) {
+        *(int4 *) (pool + i) = make_int4(-1, -1, -1, -1);
+    }
+}
+
+// One lane per voxel: record the row in its brick cell.  atomicMax makes the
+// highest row (the last duplicate in input order) win deterministically.
+__global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict__ coords, int64_t n,
+                                                         const uint64_t * __restrict__ bkeys,
+                                                         const int32_t * __restrict__ bidx, uint64_t mask,
+                                                         int32_t * __restrict__ pool, int32_t * __restrict__ counters) {
+    const int64_t i = (int64_t) blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) {
+        return;
+    }
+    const int4 c = coords[i];
+    const uint32_t x = (uint32_t) c.y & 0xffffu, y = (uint32_t) c.z & 0xffffu, z = (uint32_t) c.w & 0xffffu;
+    const int32_t b = brick_find(bkeys, bidx, mask, brick_key((uint32_t) c.x & 0xffffu, x >> 2, y >> 2, z >> 2));
+    if (b < 0) {
+        atomicOr(&counters[2], 2);  // unreachable: every voxel's brick was inserted
+        return;
+    }
+    const uint32_t cell = (x & 3u) | ((y & 3u) << 2) | ((z & 3u) << 4);
+    const int32_t old = atomicMax(&pool[(int64_t) b * kBrickCells + cell], (int32_t) i);
+    if (old >= 0) {
+        atomicOr(&counters[1], 1);
+    }
+}
+
+// Neighbour table + mask + per-tile per-offset counts.  One block = one
+// 256-row tile; the tile's [256][27] table is staged in LDS and written out
+// as one contiguous, 16-byte-vectorised block.
+__global__ void __launch_bounds__(kBlock) k_neighbors(const int4 * __restrict__ coords, int64_t n,
+                                                      const uint64_t * __restrict__ bkeys,
+                                                      const int32_t * __restrict__ bidx, uint64_t hmask,
+                                                      const int32_t * __restrict__ pool, int32_t * __restrict__ nbr,
+                                                      uint32_t * __restrict__ mask_out,
+                                                      int32_t * __restrict__ tile_counts) {
+    __shared__ int32_t s_nbr[kBlock * 27];
+    __shared__ int32_t s_cnt[27];
+    const int t = threadIdx.x;
+    const int64_t tile = blockIdx.x;
+    const int64_t row0 = tile * kBlock;
+    const int64_t i = row0 + t;
+    if (t < 27) {
+        s_cnt[t] = 0;
+    }
+    uint32_t m = 0;
+    if (i < n) {
+        const int4 c = coords[i];
+        const uint32_t b = (uint32_t) c.x & 0xffffu;
+        const uint32_t x = (uint32_t) c.y & 0xffffu, y = (uint32_t) c.z & 0xffffu, z = (uint32_t) c.w & 0xffffu;
+        const uint32_t bx = x >> 2, by = y >> 2, bz = z >> 2;
+        const int cx = (int) (x & 3u), cy = (int) (y & 3u), cz = (int) (z & 3u);
+        // Adjacent brick per axis: -1 when the cell is on the low face, +1 on the high face, 0 otherwise.
+        const int sx = cx == 0 ? -1 : (cx == 3 ? 1 : 0);
+        const int sy = cy == 0 ? -1 : (cy == 3 ? 1 : 0);
+        const int sz = cz == 0 ? -1 : (cz == 3 ? 1 : 0);
+        int32_t br[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int ax = q & 1, ay = (q >> 1) & 1, az = (q >> 2) & 1;
+            br[q] = -1;
+            if ((ax == 0 || sx != 0) && (ay == 0 || sy != 0) && (az == 0 || sz != 0)) {
+                const uint32_t nbx = (bx + (uint32_t) (ax * sx)) & 0x3fffu;
+                const uint32_t nby = (by + (uint32_t) (ay * sy)) & 0x3fffu;
+                const uint32_t nbz = (bz + (uint32_t) (az * sz)) & 0x3fffu;
+                br[q] = brick_find(bkeys, bidx, hmask, brick_key(b, nbx, nby, nbz));
+            }
+        }
+#pragma unroll
+        for (int kd = 0; kd < 3; ++kd) {
+            const int nx = cx + kd - 1;
+            const int ix = (nx < 0 || nx > 3) ? 1 : 0;
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+                const int ny = cy + kh - 1;
+                const int iy = (ny < 0 || ny > 3) ? 1 : 0;
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw) {
+                    const int nz = cz + kw - 1;
+                    const int iz = (nz < 0 || nz > 3) ? 1 : 0;
+                    const int q = ix | (iy << 1) | (iz << 2);
+                    int32_t brick = br[0];
+#pragma unroll
+                    for (int qq = 1; qq < 8; ++qq) {
+                        brick = q == qq ? br[qq] : brick;
+                    }
+                    const int cell = (nx & 3) | ((ny & 3) << 2) | ((nz & 3) << 4);
+                    const int32_t r = brick >= 0 ? pool[(int64_t) brick * kBrickCells + cell] : -1;
+                    const int k = kd * 9 + kh * 3 + kw;
+                    s_nbr[t * 27 + k] = r;
+                    m |= (r >= 0 ? 1u : 0u) << k;
+                }
+            }
+        }
+        mask_out[i] = m;
+    }
+    __syncthreads();
+    const int lane = lane_id();
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        const uint64_t bal = __ballot((m >> k) & 1u);
+        if (lane == 0 && bal != 0) {
+            atomicAdd(&s_cnt[k], __popcll(bal));
+        }
+    }
+    // Coalesced copy of the tile's table.
+    const int64_t rows = (n - row0) < kBlock ? (n - row0) : kBlock;
+    const int64_t words = rows * 27;
+    int32_t * dst = nbr + row0 * 27;
+    if ((words & 3) == 0) {
+        for (int64_t w = (int64_t) t * 4; w < words; w += kBlock * 4) {
+            *(int4 *) (dst + w) = *(const int4 *) (s_nbr + w);
+        }
+    } else {
+        for (int64_t w = t; w < words; w += kBlock) {
+            dst[w] = s_nbr[w];
+        }
+    }
+    __syncthreads();
+    if (t < 27) {
+        tile_counts[tile * 27 + t] = s_cnt[t];
+    }
+}
+
+// Exclusive prefix over tiles, one block per offset.
+__global__ void __launch_bounds__(1024) k_tile_scan(const int32_t * __restrict__ tile_counts, int64_t n_tiles,
+                                                    int32_t * __restrict__ tile_off, int32_t * __restrict__ k_count) {
+    __shared__ int32_t s_wave[16];
+    __shared__ int32_t s_carry;
+    const int k = blockIdx.x;
+    const int t = threadIdx.x;
+    const int lane = lane_id();
+    const int wave = t >> 6;
+    if (t == 0) {
+        s_carry = 0;
+    }
+    __syncthreads();
+    for (int64_t base = 0; base < n_tiles; base += 1024) {
+        const int64_t idx = base + t;
+        const int32_t v = idx < n_tiles ? tile_counts[idx * 27 + k] : 0;
+        // Inclusive scan within the wavefront.
+        int32_t incl = v;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int32_t o = __shfl_up(incl, d);
+            if (lane >= d) {
+                incl += o;
+            }
+        }
+        if (lane == 63) {
+            s_wave[wave] = incl;
+        }
+        __syncthreads();
+        int32_t wave_base = 0;
+        int32_t chunk = 0;
+        for (int w = 0; w < 16; ++w) {
+            const int32_t sw = s_wave[w];
+            wave_base += w < wave ? sw : 0;
+            chunk += sw;
+        }
+        const int32_t carry = s_carry;
+        if (idx < n_tiles) {
+            tile_off[idx * 27 + k] = carry + wave_base + incl - v;
+        }
+        __syncthreads();
+        if (t == 0) {
+            s_carry = carry + chunk;
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        k_count[k] = s_carry;
+    }
+}
+
+// Compacted pair lists, destination ascending within each offset.
+__global__ void __launch_bounds__(kBlock) k_fill_pairs(const int32_t * __restrict__ nbr,
+                                                       const uint32_t * __restrict__ mask, int64_t n,
+                                                       const int32_t * __restrict__ tile_off,
+                                                       int32_t * __restrict__ pair_src,
+                                                       int32_t * __restrict__ pair_dst) {
+    __shared__ int32_t s_wave_cnt[27][kBlock / 64];
+    const int t = threadIdx.x;
+    const int lane = lane_id();
+    const int wave = t >> 6;
+    const int64_t tile = blockIdx.x;
+    const int64_t i = tile * kBlock + t;
+    const uint32_t m = i < n ? mask[i] : 0u;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int32_t rank[27];
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        const uint64_t bal = __ballot((m >> k) & 1u);
+        rank[k] = __popcll(bal & lt);
+        if (lane == 0) {
+            s_wave_cnt[k][wave] = __popcll(bal);
+        }
+    }
+    __syncthreads();
+    if (i >= n || m == 0) {
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        if ((m >> k) & 1u) {
+            int32_t base = tile_off[tile * 27 + k];
+            for (int w = 0; w < wave; ++w) {
+                base += s_wave_cnt[k][w];
+            }
+            const int64_t pos = (int64_t) k * n + base + rank[k];
+            pair_src[pos] = nbr[i * 27 + k];
+            pair_dst[pos] = (int32_t) i;
+        }
+    }
+}
+
+int grid_for(int64_t count, int block, int cap = 65536) {
+    int64_t g = (count + block - 1) / block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (int) g;
+}
+
+}  // namespace
+
+hipError_t launch_fill_u64(uint64_t * p, int64_t count, uint64_t value, hipStream_t s) {
+    if (count <= 0) return hipSuccess;
+    k_fill_u64<<<grid_for(count, 256, 16384), 256, 0, s>>>(p, count, value);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_t s) {
+    if (count <= 0) return hipSuccess;
+    k_fill_i32<<<grid_for(count, 256, 16384), 256, 0, s>>>(p, count, value);
+    return hipGetLastError();
+}
+
+hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx, int64_t slots,
+                               int32_t * counters, hipStream_t s) {
+    const int64_t blocks = (n + kBlock - 1) / kBlock;
+    k_brick_insert<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
+                                                        (uint64_t) (slots - 1), counters);
+    return hipGetLastError();
+}
+
+hipError_t launch_pool_init(int32_t * pool, const int32_t * counters, int64_t cap_cells, hipStream_t s) {
+    k_pool_init<<<grid_for(cap_cells / 4, 256, 8192), 256, 0, s>>>(pool, counters, cap_cells);
+    return hipGetLastError();
+}
+
+hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
+                               int64_t slots, int32_t * pool, int32_t * counters, hipStream_t s) {
+    const int64_t blocks = (n + kBlock - 1) / kBlock;
+    k_voxel_insert<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
+                                                        (uint64_t) (slots - 1), pool, counters);
+    return hipGetLastError();
+}
+
+hipError_t launch_neighbors(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
+                            int64_t slots, const int32_t * pool, int32_t * nbr, uint32_t * mask,
+                            int32_t * tile_counts, hipStream_t s) {
+    const int64_t blocks = (n + kBlock - 1) / kBlock;
+    k_neighbors<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx, (uint64_t) (slots - 1),
+                                                     pool, nbr, mask, tile_counts);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_scan(const int32_t * tile_counts, int64_t n_tiles, int32_t * tile_off, int32_t * k_count,
+                            hipStream_t s) {
+    k_tile_scan<<<27, 1024, 0, s>>>(tile_counts, n_tiles, tile_off, k_count);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_pairs(const int32_t * nbr, const uint32_t * mask, int64_t n, const int32_t * tile_off,
+                             int32_t * pair_src, int32_t * pair_dst, hipStream_t s) {
+    const int64_t blocks = (n + kBlock - 1) / kBlock;
+    k_fill_pairs<<<(unsigned) blocks, kBlock, 0, s>>>(nbr, mask, n, tile_off, pair_src, pair_dst);
+    return hipGetLastError();
+}
+
+}  // namespace tsh

@@ -1,0 +1,160 @@
+// tsh_internal.h - internal declarations of the MI355X sparse-voxel backend.
+//
+// Not part of the C ABI.  Shared between the backend translation unit
+// (vtable, memory, caches) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "trellis_sparse_hip.h"
+
+namespace tsh {
+
+enum Dtype : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+inline size_t dtype_bytes(int dt) { return dt == kF32 ? 4u : 2u; }
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet), usable on host and device.
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return (uint16_t) ((u >> 16) | 0x40u);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t) (u >> 16);
+}
+__host__ __device__ inline float bf16_to_f32(uint16_t h) {
+    return __builtin_bit_cast(float, (uint32_t) h << 16);
+}
+
+// Storage-type load/store with fp32 arithmetic.
+template <int DT> struct Store;
+template <> struct Store<kF32> {
+    using T = float;
+    __device__ static float ld(const T * p, int64_t i) { return p[i]; }
+    __device__ static void st(T * p, int64_t i, float v) { p[i] = v; }
+};
+template <> struct Store<kF16> {
+    using T = _Float16;
+    __device__ static float ld(const T * p, int64_t i) { return (float) p[i]; }
+    __device__ static void st(T * p, int64_t i, float v) { p[i] = (_Float16) v; }
+};
+template <> struct Store<kBF16> {
+    using T = uint16_t;
+    __device__ static float ld(const T * p, int64_t i) { return bf16_to_f32(p[i]); }
+    __device__ static void st(T * p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+};
+
+// Work split of a rulebook build / conv: rows per tile of the kernel map.
+constexpr int kMapTile = 256;
+constexpr int kBrickCells = 64;  // 4x4x4 cells per brick
+
+struct Backend;
+
+// Device-side scratch handed out by the backend's pool.
+struct DevMem {
+    void * ptr = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace tsh
+
+// Opaque ABI types, defined here for the backend.
+struct trellis_sparse_buffer {
+    void * ptr;
+    size_t count;   // elements
+    size_t bytes;   // count * element size
+    size_t cap;     // bytes actually reserved (pool size class)
+    int dtype;      // tsh::Dtype of the storage, or -1 for raw int32
+};
+
+struct trellis_sparse_rulebook {
+    int64_t n;
+    int32_t * coords;        // device [n][4]
+    tsh::DevMem coords_mem;  // owned copy (empty when borrowed from a C2S map)
+    // Brick hash: open-addressed uint64 keys (b, x>>2, y>>2, z>>2)+1 -> brick index.
+    int64_t table_slots;
+    tsh::DevMem bkeys;       // uint64 [table_slots]
+    tsh::DevMem bidx;        // int32  [table_slots]
+    tsh::DevMem pool;        // int32  [cap_bricks][64] voxel rows, -1 = empty
+    tsh::DevMem counters;    // int32  [4]: bricks, duplicate flag, (reserved)
+    // Kernel map.
+    tsh::DevMem nbr;         // int32  [n][27]
+    tsh::DevMem mask;        // uint32 [n] bit k set when nbr[i][k] >= 0
+    int64_t n_tiles;         // ceil(n / kMapTile)
+    tsh::DevMem tile_counts; // int32  [n_tiles][27]
+    tsh::DevMem tile_off;    // int32  [n_tiles][27] exclusive prefix over tiles
+    tsh::DevMem k_count;     // int32  [27]
+    tsh::DevMem pair_src;    // int32  [27][n] (offset k occupies [k*n, k*n + k_count[k]))
+    tsh::DevMem pair_dst;    // int32  [27][n]
+};
+
+struct trellis_sparse_c2s_device_map {
+    int64_t n;
+    int64_t n_parent;    // rows of the parent level (0 for a coordinates-only map)
+    tsh::DevMem coords;  // int32 [n][4]
+    tsh::DevMem parent;  // int32 [n]
+    tsh::DevMem subidx;  // int32 [n]
+};
+
+namespace tsh {
+
+// ---------------------------------------------------------------------------
+// Kernel launchers (defined in the kernel translation units).  All enqueue on
+// `stream` and return hipSuccess or the launch error.
+// ---------------------------------------------------------------------------
+
+// Voxel hash + kernel map (kernels_map.hip).
+hipError_t launch_fill_u64(uint64_t * p, int64_t count, uint64_t value, hipStream_t s);
+hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_t s);
+hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx,
+                               int64_t slots, int32_t * counters, hipStream_t s);
+hipError_t launch_pool_init(int32_t * pool, const int32_t * counters, int64_t cap_cells, hipStream_t s);
+hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
+                               int64_t slots, int32_t * pool, int32_t * counters, hipStream_t s);
+hipError_t launch_neighbors(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
+                            int64_t slots, const int32_t * pool, int32_t * nbr, uint32_t * mask,
+                            int32_t * tile_counts, hipStream_t s);
+hipError_t launch_tile_scan(const int32_t * tile_counts, int64_t n_tiles, int32_t * tile_off, int32_t * k_count,
+                            hipStream_t s);
+hipError_t launch_fill_pairs(const int32_t * nbr, const uint32_t * mask, int64_t n, const int32_t * tile_off,
+                             int32_t * pair_src, int32_t * pair_dst, hipStream_t s);
+
+// Convolution (kernels_conv.hip).  Weight layouts are produced by the backend.
+//  generic: w32 fp32 [27][ci][co]
+//  mfma:    w16 storage-type [27][ci/8][co][8]
+hipError_t launch_conv_generic(int dtype, const void * x, const int32_t * nbr, const float * w32,
+                               const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s);
+bool conv_mfma_supported(int dtype, int ci, int co);
+hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nbr, const uint32_t * mask,
+                                   const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
+                                   hipStream_t s);
+
+// Everything else (kernels_misc.hip).
+hipError_t launch_convert_from_f32(int dtype, const float * src, void * dst, int64_t count, hipStream_t s);
+hipError_t launch_convert_to_f32(int dtype, const void * src, float * dst, int64_t count, hipStream_t s);
+hipError_t launch_silu(int dtype, void * x, int64_t count, hipStream_t s);
+hipError_t launch_add(int dtype, const void * a, const void * b, void * y, int64_t count, hipStream_t s);
+hipError_t launch_row_norm(int dtype, const void * x, const float * gamma, const float * beta, void * y,
+                           int64_t n, int c, float eps, int silu, hipStream_t s);
+hipError_t launch_linear(int dtype, const void * x, const float * wt, const float * bias, void * y, int64_t n,
+                         int ci, int co, int silu, hipStream_t s);
+hipError_t launch_c2s_count(int dtype, const void * logits, int64_t n, int32_t * counts, hipStream_t s);
+// Exclusive scan of n int32 values; total written to *total_dev.  tmp needs scan_tmp_bytes(n).
+size_t scan_tmp_bytes(int64_t n);
+hipError_t launch_scan_exclusive(const int32_t * in, int32_t * out, int64_t n, int32_t * total_dev, void * tmp,
+                                 hipStream_t s);
+hipError_t launch_c2s_fill(int dtype, const int32_t * coords, const void * logits, const int32_t * offsets,
+                           int64_t n, int32_t * out_coords, int32_t * parent, int32_t * subidx, hipStream_t s);
+hipError_t launch_c2s_gather(int dtype, const void * x, const int32_t * parent, const int32_t * subidx, void * y,
+                             int64_t n_out, int co, hipStream_t s);
+hipError_t launch_skip_repeat(int dtype, const void * x, const int32_t * parent, const int32_t * subidx, void * y,
+                              int64_t n_out, int ci, int co, hipStream_t s);
+
+}  // namespace tsh
