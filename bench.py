@@ -184,7 +184,24 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-stride", type=int, default=16)
     ap.add_argument("--conv-algo", type=int, default=sh.CONV_AUTO)
+    ap.add_argument("--calibrate", action="store_true",
+                    help="run one fp32 add over 2 x 64Mi-element inputs (512 MiB read, 256 MiB written) so PMC "
+                         "byte counters can be scaled against a streaming kernel of known traffic")
     args = ap.parse_args()
+    if args.calibrate:
+        if sh.device_count() < 1:
+            print("bench.py: no HIP device visible", file=sys.stderr)
+            sys.exit(1)
+        count = 64 * 1024 * 1024
+        be = sh.Backend(0, sh.F32)
+        a = be.upload(np.ones(count, np.float32))
+        b = be.upload(np.ones(count, np.float32))
+        y = be.alloc(count)
+        be.add(a, b, y, count)
+        be.synchronize()
+        print(json.dumps({"calibration": "k_add<0>", "read_bytes": 2 * count * 4, "write_bytes": count * 4}))
+        be.destroy()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the multi-GPU sharding design is described in DESIGN.md)", file=sys.stderr)
@@ -224,6 +241,17 @@ def main():
     achieved = per_launch_flops / (conv_avg * 1e-3) / 1e12 if conv_avg > 0 else 0.0
     hm_ms = (stages["hash"][0] + stages["map"][0]) / args.steps
     elem = 4 if spec["dtype"] == sh.F32 else 2
+    # HBM bytes per conv launch come from the committed, copy-calibrated
+    # rocprofv3 FETCH_SIZE / WRITE_SIZE summary for this workload and schedule.
+    algo_name = {sh.CONV_AUTO: "masked", sh.CONV_MASKED: "masked", sh.CONV_COMPACT: "compact"}.get(args.conv_algo)
+    traffic = None
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            entry = json.load(f).get(spec["name"], {}).get(algo_name)
+        if entry is not None:
+            traffic = round(entry["hbm_bytes_per_launch"])
+    except (OSError, ValueError):
+        traffic = None
     result = {
         "metric": METRIC,
         "value": round(flops / (ms_per_step * 1e-3) / 1e12, 3),
@@ -248,8 +276,9 @@ def main():
             "peak": PEAK_TFLOPS[spec["dtype"]],
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_TFLOPS[spec["dtype"]], 4),
-            "traffic": None,
+            "traffic": traffic,
             "algorithmic_bytes": wl.conv_bytes(job.m, job.ci, job.co, elem),
+            "schedule": algo_name,
             "avg_launch_ms": round(conv_avg, 4),
         },
         "timing": {"device_event_ms": round(dev_ms, 3), "wall_ms": round(wall, 3)},

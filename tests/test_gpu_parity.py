@@ -27,8 +27,9 @@ def say(msg):
 
 
 def max_rel_err(got, exp):
-    got = np.asarray(got, dtype=np.float64)
-    exp = np.asarray(exp, dtype=np.float64)
+    got = np.asarray(got, dtype=np.float64).ravel()
+    exp = np.asarray(exp, dtype=np.float64).ravel()
+    assert got.shape == exp.shape
     scale = np.maximum(1.0, np.maximum(np.abs(got), np.abs(exp)))
     return float(np.max(np.abs(got - exp) / scale)) if got.size else 0.0
 
@@ -162,10 +163,20 @@ def test_conv_fp32_config1_full(be32):
     assert np.array_equal(got, exp)
 
 
+@pytest.fixture(scope="module")
+def be_masked():
+    b = {sh.BF16: sh.Backend(0, sh.BF16, conv_algo=sh.CONV_MASKED),
+         sh.F16: sh.Backend(0, sh.F16, conv_algo=sh.CONV_MASKED)}
+    yield b
+    for v in b.values():
+        v.destroy()
+
+
+@pytest.mark.parametrize("algo", ["compact", "masked"])
 @pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])
-@pytest.mark.parametrize("ci,co", [(64, 64), (128, 128), (256, 128), (32, 192)])
-def test_conv_mfma_vs_oracle(be32, be16, bebf, dtype, ci, co):
-    be = backend_for(dtype, be32, be16, bebf)
+@pytest.mark.parametrize("ci,co", [(64, 64), (128, 128), (256, 128), (32, 192), (64, 512)])
+def test_conv_mfma_vs_oracle(be32, be16, bebf, be_masked, algo, dtype, ci, co):
+    be = backend_for(dtype, be32, be16, bebf) if algo == "compact" else be_masked[dtype]
     c = wl.make_coords(1)
     rng = np.random.default_rng(ci + co + dtype)
     x = sh.storage_round(rng.standard_normal((c.shape[0], ci)).astype(np.float32), dtype)
@@ -175,7 +186,7 @@ def test_conv_mfma_vs_oracle(be32, be16, bebf, dtype, ci, co):
     got = run_conv(be, c, x, w, bias, ci, co)
     exp = orc.Rulebook(c).conv(x, wr, bias, ci, co)
     err = max_rel_err(got, exp)
-    say(f"mfma dtype={dtype} ci={ci} co={co} max_rel_err={err:.3e}")
+    say(f"mfma {algo} dtype={dtype} ci={ci} co={co} max_rel_err={err:.3e}")
     assert err <= TOL[dtype]
 
 
@@ -370,7 +381,8 @@ def test_row_ops(be32, be16, bebf, dtype):
         exp = orc.linear(x, w, bias, n, c, 48, silu)
         got = be.download(y2)
         assert max_rel_err(got, exp) <= tol
-        if dtype == sh.F32:
+        if dtype == sh.F32 and not silu:
+            # Same operation order as the reference; SiLU's expf differs from libm by an ulp.
             assert np.array_equal(got.reshape(n, 48), exp)
 
 

@@ -602,10 +602,12 @@ trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_
     CallScope scope(be);
     const int dt = be->policy.compute_dtype;
     int algo = be->policy.conv_algo;
-    if (algo == TRELLIS_SPARSE_HIP_CONV_AUTO || algo == TRELLIS_SPARSE_HIP_CONV_COMPACT) {
-        algo = conv_mfma_supported(dt, ci, co) ? TRELLIS_SPARSE_HIP_CONV_MASKED : TRELLIS_SPARSE_HIP_CONV_GENERIC;
+    if (algo == TRELLIS_SPARSE_HIP_CONV_AUTO) {
+        // The masked schedule is the faster one on every measured workload so far.
+        algo = TRELLIS_SPARSE_HIP_CONV_MASKED;
     }
-    if (algo == TRELLIS_SPARSE_HIP_CONV_MASKED && !conv_mfma_supported(dt, ci, co)) {
+    if ((algo == TRELLIS_SPARSE_HIP_CONV_MASKED || algo == TRELLIS_SPARSE_HIP_CONV_COMPACT) &&
+        !conv_mfma_supported(dt, ci, co)) {
         algo = TRELLIS_SPARSE_HIP_CONV_GENERIC;
     }
     const void * bd = nullptr;
@@ -613,14 +615,14 @@ trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_
     if (st != TRELLIS_STATUS_OK) return st;
     const size_t wcount = (size_t) co * 27 * ci;
     hipError_t err;
-    if (algo == TRELLIS_SPARSE_HIP_CONV_MASKED) {
+    if (algo == TRELLIS_SPARSE_HIP_CONV_MASKED || algo == TRELLIS_SPARSE_HIP_CONV_COMPACT) {
         const void * w = nullptr;
         st = get_weight(be, weight, wcount, kLayoutConvMfma, ci, co, &w);
         if (st != TRELLIS_STATUS_OK) return st;
+        auto launch = algo == TRELLIS_SPARSE_HIP_CONV_COMPACT ? launch_conv_mfma_compact : launch_conv_mfma_masked;
         stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
-        err = launch_conv_mfma_masked(dt, feats->ptr, (const int32_t *) rulebook->nbr.ptr,
-                                      (const uint32_t *) rulebook->mask.ptr, w, (const float *) bd, out->ptr, n, ci,
-                                      co, be->stream);
+        err = launch(dt, feats->ptr, (const int32_t *) rulebook->nbr.ptr, (const uint32_t *) rulebook->mask.ptr, w,
+                     (const float *) bd, out->ptr, n, ci, co, be->stream);
         stage_end(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
     } else {
         const void * w = nullptr;

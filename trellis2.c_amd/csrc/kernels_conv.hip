@@ -251,6 +251,193 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
     }
 }
 
+// ---------------------------------------------------------------------------
+// Compacted MFMA kernel (bf16 / fp16 storage).
+//
+// A block owns TM output rows x BN output channels.  Their fp32 sums live in
+// LDS.  For each offset k the block compacts its rows that have a neighbour at
+// k into a (src, dst) list (wavefront ballots, destination ascending), so the
+// MFMA row dimension runs over valid pairs only: 16-pair row blocks are
+// gathered straight into A fragments, multiplied by the k-th weight slice
+// (staged through LDS and shared by the four wavefronts) and the 16 x BN
+// partial results are added into the LDS sums of their destination rows.
+// Within one offset a destination occurs at most once, so no two lanes touch
+// the same LDS word; offsets are applied in k order, so the result is
+// deterministic.  The tile's rows are written once at the end.
+//
+// Wavefront w covers channel half (w >> 1) and row blocks (w & 1), +2, +4, +6
+// of each pass of eight row blocks.
+// ---------------------------------------------------------------------------
+template <int DT, int BN, int TM>
+__global__ void __launch_bounds__(256) k_conv_mfma_compact(const typename Store<DT>::T * __restrict__ x,
+                                                           const int32_t * __restrict__ nbr,
+                                                           const uint32_t * __restrict__ mask,
+                                                           const typename Store<DT>::T * __restrict__ w16,
+                                                           const float * __restrict__ bias,
+                                                           typename Store<DT>::T * __restrict__ y, int64_t n,
+                                                           int ci, int co, int64_t n_col_tiles) {
+    using T = typename Store<DT>::T;
+    using V = typename Mfma<DT>::V;
+    constexpr int ACC_LD = BN + 4;   // padded fp32 row stride of the LDS sums
+    constexpr int BK = 32;           // input channels per K step
+    constexpr int WN = BN / 2;       // channels per wavefront
+    constexpr int NT = WN / 16;      // MFMA column tiles per wavefront
+    constexpr int QB = 4;            // row blocks per wavefront per pass
+    constexpr int ROWS_PER_THREAD = (TM + 255) / 256;
+    __shared__ float s_acc[TM * ACC_LD];
+    __shared__ int32_t s_src[TM];
+    __shared__ int32_t s_dst[TM];
+    __shared__ int32_t s_wcnt[4 * ROWS_PER_THREAD];
+    __shared__ uint32_t s_need;
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int rh = wave & 1, ch = wave >> 1;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int64_t logical = xcd_remap(blockIdx.x, (int64_t) gridDim.x);
+    const int64_t row0 = (logical / n_col_tiles) * TM;
+    const int col0 = (int) (logical % n_col_tiles) * BN;
+    const int ci8 = ci >> 3;
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+
+    for (int i = t; i < TM * ACC_LD; i += 256) s_acc[i] = 0.0f;
+    if (t == 0) s_need = 0u;
+    uint32_t m[ROWS_PER_THREAD];
+#pragma unroll
+    for (int q = 0; q < ROWS_PER_THREAD; ++q) {
+        const int local = q * 256 + t;
+        const int64_t row = row0 + local;
+        m[q] = (local < TM && row < n) ? mask[row] : 0u;
+    }
+    __syncthreads();
+    {
+        uint32_t any = 0;
+#pragma unroll
+        for (int q = 0; q < ROWS_PER_THREAD; ++q) any |= m[q];
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) any |= __shfl_xor(any, d);
+        if (lane == 0) atomicOr(&s_need, any);
+    }
+    __syncthreads();
+    const uint32_t need = s_need;
+
+    for (int k = 0; k < 27; ++k) {
+        if (((need >> k) & 1u) == 0) continue;
+        // Compact this offset's pairs: destination-ascending (src, dst) list.
+        int32_t rank[ROWS_PER_THREAD];
+#pragma unroll
+        for (int q = 0; q < ROWS_PER_THREAD; ++q) {
+            const uint64_t bal = __ballot((m[q] >> k) & 1u);
+            rank[q] = __popcll(bal & lt);
+            if (lane == 0) s_wcnt[q * 4 + wave] = __popcll(bal);
+        }
+        __syncthreads();
+        int c = 0;
+#pragma unroll
+        for (int q = 0; q < ROWS_PER_THREAD; ++q) {
+            int base = c;
+            for (int w = 0; w < 4; ++w) {
+                base += w < wave ? s_wcnt[q * 4 + w] : 0;
+                c += s_wcnt[q * 4 + w];
+            }
+            if ((m[q] >> k) & 1u) {
+                const int local = q * 256 + t;
+                s_src[base + rank[q]] = nbr[(row0 + local) * 27 + k];
+                s_dst[base + rank[q]] = local;
+            }
+        }
+        __syncthreads();
+        const int nb = (c + 15) >> 4;
+        const T * wk = w16 + (int64_t) k * ci8 * co * 8;
+        for (int pb = 0; pb < nb; pb += 2 * QB) {
+            f32x4 acc[QB][NT];
+            int32_t src[QB];
+            bool live[QB];
+#pragma unroll
+            for (int q = 0; q < QB; ++q) {
+                const int j = pb + rh + 2 * q;
+                live[q] = j < nb;
+                const int p = j * 16 + l16;
+                src[q] = (live[q] && p < c) ? s_src[p] : -1;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+            // Operand fragments for K step s, loaded one step ahead into two
+            // register sets that alternate (no copies, so a wait only ever
+            // covers older loads).  A: gathered source rows (padding slots read
+            // row 0; their products are never added).  B: this wavefront's
+            // weight columns, read from L2 (the packed weights are L2-resident).
+            int64_t abase[QB];
+#pragma unroll
+            for (int q = 0; q < QB; ++q) abase[q] = (int64_t) (src[q] >= 0 ? src[q] : 0) * ci + lg * 8;
+            const T * bbase = wk + ((int64_t) lg * co + col0 + ch * WN + l16) * 8;
+            auto load = [&](int s, V * a, V * b) {
+#pragma unroll
+                for (int q = 0; q < QB; ++q) a[q] = *(const V *) (x + abase[q] + s * BK);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) b[nt] = *(const V *) (bbase + ((int64_t) s * 4 * co + nt * 16) * 8);
+            };
+            const int ks = ci / BK;
+            auto step = [&](int s, const V * a, const V * b, V * an, V * bn) {
+                if (s + 1 < ks) load(s + 1, an, bn);
+#pragma unroll
+                for (int q = 0; q < QB; ++q) {
+                    if (!live[q]) continue;
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) acc[q][nt] = Mfma<DT>::mac(a[q], b[nt], acc[q][nt]);
+                }
+            };
+            V a0[QB], a1[QB], b0[NT], b1[NT];
+            load(0, a0, b0);
+            int s = 0;
+            for (; s + 1 < ks; s += 2) {
+                step(s, a0, b0, a1, b1);
+                step(s + 1, a1, b1, a0, b0);
+            }
+            if (s < ks) step(s, a0, b0, a1, b1);
+            // Add the partial products into the destination rows' sums.
+#pragma unroll
+            for (int q = 0; q < QB; ++q) {
+                if (!live[q]) continue;
+                const int j = pb + rh + 2 * q;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int p = j * 16 + lg * 4 + i;
+                    if (p < c) {
+                        float * dst = s_acc + s_dst[p] * ACC_LD + ch * WN + l16;
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt) atomicAdd(dst + nt * 16, acc[q][nt][i]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    // Epilogue: bias, round to the storage type, 16-byte coalesced stores.
+    constexpr int CHUNKS = BN / 8;
+    for (int e = t; e < TM * CHUNKS; e += 256) {
+        const int r = e / CHUNKS, cc = (e % CHUNKS) * 8;
+        const int64_t row = row0 + r;
+        if (row >= n) continue;
+        union {
+            int4 v;
+            T h[8];
+        } o;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float bv = bias != nullptr ? bias[col0 + cc + u] : 0.0f;
+            float v = s_acc[r * ACC_LD + cc + u] + bv;
+            if constexpr (DT == kBF16) {
+                o.h[u] = f32_to_bf16(v);
+            } else {
+                o.h[u] = (T) v;
+            }
+        }
+        *(int4 *) (y + row * co + col0 + cc) = o.v;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_conv_generic(int dtype, const void * x, const int32_t * nbr, const float * w32, const float * bias,
@@ -302,6 +489,54 @@ hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nb
         if (bn == 128) TSH_LAUNCH(kF16, _Float16, 128);
         else TSH_LAUNCH(kF16, _Float16, 64);
     }
+#undef TSH_LAUNCH
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_mfma_compact(int dtype, const void * x, const int32_t * nbr, const uint32_t * mask,
+                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
+                                    hipStream_t s) {
+    if (!conv_mfma_supported(dtype, ci, co)) {
+        return hipErrorInvalidValue;
+    }
+    // Tile shapes (rows x channels): the LDS sums take TM*(BN+4)*4 bytes, so
+    // 128x128 and 256x64 leave room for two blocks per CU, 256x128 and 512x64
+    // for one.  TRELLIS_HIP_CONV_TILE=1..4 pins a shape for tuning; the shape
+    // does not change the order of any sum.
+    static const int forced = [] {
+        const char * e = getenv("TRELLIS_HIP_CONV_TILE");
+        return e != nullptr ? atoi(e) : 0;
+    }();
+    int shape = forced;
+    if (shape < 1 || shape > 4 || ((shape == 1 || shape == 2) && co % 128 != 0)) {
+        shape = co % 128 == 0 ? 2 : 3;
+    }
+    static const int kTm[5] = {0, 256, 128, 256, 512};
+    static const int kBn[5] = {0, 128, 128, 64, 64};
+    const int tm = kTm[shape], bn = kBn[shape];
+    const int64_t row_tiles = (n + tm - 1) / tm;
+    const int64_t col_tiles = co / bn;
+    const int64_t grid = row_tiles * col_tiles;
+    if (grid > 0x7fffffffLL) {
+        return hipErrorInvalidValue;
+    }
+#define TSH_LAUNCH(DTV, TYPE, BNV, TMV)                                                                         \
+    k_conv_mfma_compact<DTV, BNV, TMV><<<(unsigned) grid, 256, 0, s>>>((const TYPE *) x, nbr, mask,            \
+                                                                        (const TYPE *) w16, bias, (TYPE *) y, n, \
+                                                                        ci, co, col_tiles)
+#define TSH_SHAPES(DTV, TYPE)                              \
+    switch (shape) {                                       \
+        case 1: TSH_LAUNCH(DTV, TYPE, 128, 256); break;    \
+        case 2: TSH_LAUNCH(DTV, TYPE, 128, 128); break;    \
+        case 3: TSH_LAUNCH(DTV, TYPE, 64, 256); break;     \
+        default: TSH_LAUNCH(DTV, TYPE, 64, 512); break;    \
+    }
+    if (dtype == kBF16) {
+        TSH_SHAPES(kBF16, uint16_t)
+    } else {
+        TSH_SHAPES(kF16, _Float16)
+    }
+#undef TSH_SHAPES
 #undef TSH_LAUNCH
     return hipGetLastError();
 }

@@ -100,22 +100,49 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
         }
         todo &= ~same;
     }
-    if (!first) {
-        return;
-    }
-    uint64_t s = mix64(key) & mask;
-    for (uint64_t step = 0; step <= mask; ++step) {
-        const uint64_t prev = atomicCAS((unsigned long long *) &bkeys[s], 0ull, (unsigned long long) key);
-        if (prev == 0) {
-            bidx[s] = atomicAdd(&counters[0], 1);
-            return;
+    // Representatives probe; a lane that claims an empty slot owns a new brick.
+    uint64_t s = 0;
+    bool won = false;
+    if (first) {
+        s = mix64(key) & mask;
+        uint64_t step = 0;
+        for (; step <= mask; ++step) {
+            const uint64_t prev = atomicCAS((unsigned long long *) &bkeys[s], 0ull, (unsigned long long) key);
+            if (prev == 0) {
+                won = true;
+                break;
+            }
+            if (prev == key) {
+                break;
+            }
+            s = (s + 1) & mask;
         }
-        if (prev == key) {
-            return;
+        if (step > mask) {
+            atomicOr(&counters[2], 1);  // table full; cannot happen with slots >= 2n
         }
-        s = (s + 1) & mask;
     }
-    atomicOr(&counters[2], 1);  // table full; cannot happen with slots >= 2n
+    // Number the new bricks with one global atomic per block: wave ballots give
+    // each winner its rank, LDS gives each wave its block offset.
+    __shared__ int32_t s_wave_new[kBlock / 64];
+    __shared__ int32_t s_base;
+    const int wave = threadIdx.x >> 6;
+    const uint64_t wins = __ballot(won);
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    if (lane == 0) {
+        s_wave_new[wave] = __popcll(wins);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t total = 0;
+        for (int w = 0; w < kBlock / 64; ++w) total += s_wave_new[w];
+        s_base = total > 0 ? atomicAdd(&counters[0], total) : 0;
+    }
+    __syncthreads();
+    if (won) {
+        int32_t idx = s_base + __popcll(wins & below);
+        for (int w = 0; w < wave; ++w) idx += s_wave_new[w];
+        bidx[s] = idx;
+    }
 }
 
 // Clears the pool cells of the bricks numbered so far (count read on device).

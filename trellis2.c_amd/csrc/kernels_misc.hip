@@ -294,11 +294,17 @@ __global__ void k_skip_repeat(const typename Store<DT>::T * __restrict__ x, cons
                 int4 v;
                 T e[kVec];
             } out;
+            // One division per chunk; step the quotient/remainder across it.
+            const int first = s * co + c0;
+            int from = first / repeat;
+            int rem = first - from * repeat;
 #pragma unroll
             for (int q = 0; q < kVec; ++q) {
-                int from = (s * co + c0 + q) / repeat;
-                from = from < ci - 1 ? from : ci - 1;
-                out.e[q] = xr[from];
+                out.e[q] = xr[from < ci - 1 ? from : ci - 1];
+                if (++rem == repeat) {
+                    rem = 0;
+                    ++from;
+                }
             }
             *(int4 *) (y + r * co + c0) = out.v;
         }

@@ -135,6 +135,9 @@ bool conv_mfma_supported(int dtype, int ci, int co);
 hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nbr, const uint32_t * mask,
                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
                                    hipStream_t s);
+hipError_t launch_conv_mfma_compact(int dtype, const void * x, const int32_t * nbr, const uint32_t * mask,
+                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
+                                    hipStream_t s);
 
 // Everything else (kernels_misc.hip).
 hipError_t launch_convert_from_f32(int dtype, const float * src, void * dst, int64_t count, hipStream_t s);
