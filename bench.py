@@ -134,6 +134,16 @@ class Cfg2(ConvOnly):
         return 2 * wl.conv_flops(self.pairs, self.ci, self.co)
 
 
+def conv_schedule(dtype, ci, co, algo):
+    """Name of the conv kernel the backend runs (its fallback rules)."""
+    mfma = dtype != sh.F32 and ci % 32 == 0 and co % 64 == 0
+    if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and ci % 64 == 0:
+        return "compact"
+    if algo in (sh.CONV_AUTO, sh.CONV_COMPACT, sh.CONV_MASKED) and mfma:
+        return "masked"
+    return "generic"
+
+
 def cpu_baseline(cfg, w, stride):
     """Single-threaded CPU oracle on a bounded sample of the same workload."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -243,7 +253,7 @@ def main():
     elem = 4 if spec["dtype"] == sh.F32 else 2
     # HBM bytes per conv launch come from the committed, copy-calibrated
     # rocprofv3 FETCH_SIZE / WRITE_SIZE summary for this workload and schedule.
-    algo_name = {sh.CONV_AUTO: "masked", sh.CONV_MASKED: "masked", sh.CONV_COMPACT: "compact"}.get(args.conv_algo)
+    algo_name = conv_schedule(spec["dtype"], job.ci, job.co, args.conv_algo)
     traffic = None
     try:
         with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:

@@ -163,10 +163,14 @@ def test_conv_fp32_config1_full(be32):
     assert np.array_equal(got, exp)
 
 
+SCHEDULES = {"masked": sh.CONV_MASKED, "compact": sh.CONV_COMPACT}
+
+
 @pytest.fixture(scope="module")
-def be_masked():
-    b = {sh.BF16: sh.Backend(0, sh.BF16, conv_algo=sh.CONV_MASKED),
-         sh.F16: sh.Backend(0, sh.F16, conv_algo=sh.CONV_MASKED)}
+def be_sched():
+    """One backend per (MFMA schedule, storage type)."""
+    b = {(name, dt): sh.Backend(0, dt, conv_algo=algo) for name, algo in SCHEDULES.items()
+         for dt in (sh.BF16, sh.F16)}
     yield b
     for v in b.values():
         v.destroy()
@@ -175,8 +179,8 @@ def be_masked():
 @pytest.mark.parametrize("algo", ["compact", "masked"])
 @pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])
 @pytest.mark.parametrize("ci,co", [(64, 64), (128, 128), (256, 128), (32, 192), (64, 512)])
-def test_conv_mfma_vs_oracle(be32, be16, bebf, be_masked, algo, dtype, ci, co):
-    be = backend_for(dtype, be32, be16, bebf) if algo == "compact" else be_masked[dtype]
+def test_conv_mfma_vs_oracle(be_sched, algo, dtype, ci, co):
+    be = be_sched[(algo, dtype)]
     c = wl.make_coords(1)
     rng = np.random.default_rng(ci + co + dtype)
     x = sh.storage_round(rng.standard_normal((c.shape[0], ci)).astype(np.float32), dtype)
@@ -190,16 +194,36 @@ def test_conv_mfma_vs_oracle(be32, be16, bebf, be_masked, algo, dtype, ci, co):
     assert err <= TOL[dtype]
 
 
-def test_conv_mfma_dense_block_vs_torch(bebf):
+@pytest.mark.parametrize("algo", ["compact", "masked"])
+def test_conv_mfma_dense_block_vs_torch(be_sched, algo):
+    """Fully occupied block: every interior row has all 27 neighbours, so a
+    256-row tile holds more than 128 pairs per offset (several units each)."""
     from test_oracle import dense_block, torch_dense_conv
 
     coords, feats, w, bias, side = dense_block(side=12, ci=64, co=64, seed=3)
     x = sh.bf16_round(feats)
     wr = sh.bf16_round(w)
-    got = run_conv(bebf, coords, x, w, bias, 64, 64)
+    got = run_conv(be_sched[(algo, sh.BF16)], coords, x, w, bias, 64, 64)
     exp = torch_dense_conv(x, wr, bias, side)
     err = max_rel_err(got, exp)
-    say(f"dense block bf16 vs torch conv3d max_rel_err={err:.3e}")
+    say(f"dense block bf16 {algo} vs torch conv3d max_rel_err={err:.3e}")
+    assert err <= 2e-2
+
+
+@pytest.mark.parametrize("algo", ["compact", "masked"])
+@pytest.mark.parametrize("n", [1, 37, 300, 777])
+def test_conv_mfma_ragged_rows(be_sched, algo, n):
+    """Row counts that leave the last 64/256-row tile partly empty."""
+    c = wl.make_coords(1)[:n]
+    ci, co = 128, 64
+    rng = np.random.default_rng(n)
+    x = sh.bf16_round(rng.standard_normal((n, ci)).astype(np.float32))
+    w = (rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci)).astype(np.float32)
+    bias = rng.standard_normal(co).astype(np.float32)
+    got = run_conv(be_sched[(algo, sh.BF16)], c, x, w, bias, ci, co)
+    exp = orc.Rulebook(c).conv(x, sh.bf16_round(w), bias, ci, co)
+    err = max_rel_err(got, exp)
+    say(f"ragged {algo} n={n} max_rel_err={err:.3e}")
     assert err <= 2e-2
 
 
@@ -213,13 +237,15 @@ def test_conv_generic_small_channels_all_dtypes(be32, be16, bebf):
         assert max_rel_err(got, exp) <= TOL[dtype]
 
 
-def test_conv_deterministic(bebf):
+@pytest.mark.parametrize("algo", ["compact", "masked"])
+def test_conv_deterministic(be_sched, algo):
+    be = be_sched[(algo, sh.BF16)]
     c = wl.make_coords(1)
     rng = np.random.default_rng(4)
     x = rng.standard_normal((c.shape[0], 128)).astype(np.float32)
     w = (rng.standard_normal((128, 27, 128)) * 0.02).astype(np.float32)
-    a = run_conv(bebf, c, x, w, None, 128, 128)
-    b = run_conv(bebf, c, x, w, None, 128, 128)
+    a = run_conv(be, c, x, w, None, 128, 128)
+    b = run_conv(be, c, x, w, None, 128, 128)
     assert np.array_equal(a, b)
 
 

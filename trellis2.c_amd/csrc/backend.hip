@@ -42,7 +42,8 @@ enum WeightLayout : int {
     kLayoutConvF32 = 1,   // fp32 [27][ci][co]
     kLayoutConvMfma = 2,  // storage type [27][ci/8][co][8]
     kLayoutLinearT = 3,   // fp32 [ci][co]
-    kLayoutVector = 4     // fp32 [count]
+    kLayoutVector = 4,    // fp32 [count]
+    kLayoutConvMfmaGrouped = 5  // kLayoutConvMfma with the streamed kernel's column grouping
 };
 
 struct StageMark {
@@ -247,12 +248,16 @@ trellis_status get_weight(Backend * be, const float * host, size_t count, int la
                         w[((size_t) k * ci + c) * co + o] = host[((size_t) o * 27 + k) * ci + c];
             break;
         }
-        case kLayoutConvMfma: {  // [co][27][ci] -> [27][ci/8][co][8] in the storage type
+        case kLayoutConvMfma:  // [co][27][ci] -> [27][ci/8][co][8] in the storage type
+        case kLayoutConvMfmaGrouped: {
             const size_t elems = (size_t) 27 * ci * co;
             staged.resize(elems * 2);
             uint16_t * w = (uint16_t *) staged.data();
             const int ci8 = ci / 8;
-            for (int o = 0; o < co; ++o)
+            const int g = conv_stream_group(co), wn = 16 * g;
+            for (int o = 0; o < co; ++o) {
+                // Packed column of channel o.
+                const int pos = layout == kLayoutConvMfma ? o : (o / wn) * wn + (o % g) * 16 + (o % wn) / g;
                 for (int k = 0; k < 27; ++k)
                     for (int c = 0; c < ci; ++c) {
                         const float v = host[((size_t) o * 27 + k) * ci + c];
@@ -263,8 +268,9 @@ trellis_status get_weight(Backend * be, const float * host, size_t count, int la
                             const _Float16 f = (_Float16) v;
                             memcpy(&h, &f, 2);
                         }
-                        w[((((size_t) k * ci8 + c / 8) * co + o) * 8) + (c & 7)] = h;
+                        w[((((size_t) k * ci8 + c / 8) * co + pos) * 8) + (c & 7)] = h;
                     }
+            }
             break;
         }
         case kLayoutLinearT: {  // [co][ci] -> [ci][co]
@@ -500,7 +506,7 @@ trellis_status op_add(trellis_sparse_backend * backend, const trellis_sparse_buf
 void rulebook_release(Backend * be, trellis_sparse_rulebook * r) {
     if (r == nullptr) return;
     DevMem * mems[] = {&r->coords_mem, &r->bkeys, &r->bidx, &r->pool, &r->counters, &r->nbr, &r->mask,
-                       &r->tile_counts, &r->tile_off, &r->k_count, &r->pair_src, &r->pair_dst};
+                       &r->tile_counts, &r->tile_off, &r->k_count, &r->scan_tmp, &r->pair_src, &r->pair_dst};
     for (DevMem * m : mems) dev_release(be, m);
     delete r;
 }
@@ -531,6 +537,7 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
         {&r->tile_counts, (size_t) r->n_tiles * 27 * 4},
         {&r->tile_off, (size_t) r->n_tiles * 27 * 4},
         {&r->k_count, 27 * 4},
+        {&r->scan_tmp, scan_tmp_bytes(r->n_tiles * 27)},
         {&r->pair_src, (size_t) n * 27 * 4},
         {&r->pair_dst, (size_t) n * 27 * 4},
     };
@@ -552,8 +559,11 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
     TSH_TRY(be, launch_neighbors(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
                                  r->table_slots, (const int32_t *) r->pool.ptr, (int32_t *) r->nbr.ptr,
                                  (uint32_t *) r->mask.ptr, (int32_t *) r->tile_counts.ptr, s));
-    TSH_TRY(be, launch_tile_scan((const int32_t *) r->tile_counts.ptr, r->n_tiles, (int32_t *) r->tile_off.ptr,
-                                 (int32_t *) r->k_count.ptr, s));
+    // Pairs are stored by tile, then offset: list starts = exclusive scan of
+    // the flattened [n_tiles][27] counts (total into counters[2]).
+    TSH_TRY(be, launch_scan_exclusive((const int32_t *) r->tile_counts.ptr, (int32_t *) r->tile_off.ptr,
+                                      r->n_tiles * 27, (int32_t *) r->counters.ptr + 2, r->scan_tmp.ptr, s));
+    TSH_TRY(be, launch_offset_totals((const int32_t *) r->tile_counts.ptr, r->n_tiles, (int32_t *) r->k_count.ptr, s));
     TSH_TRY(be, launch_fill_pairs((const int32_t *) r->nbr.ptr, (const uint32_t *) r->mask.ptr, n,
                                   (const int32_t *) r->tile_off.ptr, (int32_t *) r->pair_src.ptr,
                                   (int32_t *) r->pair_dst.ptr, s));
@@ -603,11 +613,14 @@ trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_
     const int dt = be->policy.compute_dtype;
     int algo = be->policy.conv_algo;
     if (algo == TRELLIS_SPARSE_HIP_CONV_AUTO) {
-        // The masked schedule is the faster one on every measured workload so far.
+        // The streamed compacted schedule multiplies valid pairs only; where it
+        // does not apply (Ci % 64 != 0) the masked one, then the VALU one.
+        algo = TRELLIS_SPARSE_HIP_CONV_COMPACT;
+    }
+    if (algo == TRELLIS_SPARSE_HIP_CONV_COMPACT && !conv_stream_supported(dt, ci, co)) {
         algo = TRELLIS_SPARSE_HIP_CONV_MASKED;
     }
-    if ((algo == TRELLIS_SPARSE_HIP_CONV_MASKED || algo == TRELLIS_SPARSE_HIP_CONV_COMPACT) &&
-        !conv_mfma_supported(dt, ci, co)) {
+    if (algo == TRELLIS_SPARSE_HIP_CONV_MASKED && !conv_mfma_supported(dt, ci, co)) {
         algo = TRELLIS_SPARSE_HIP_CONV_GENERIC;
     }
     const void * bd = nullptr;
@@ -617,12 +630,22 @@ trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_
     hipError_t err;
     if (algo == TRELLIS_SPARSE_HIP_CONV_MASKED || algo == TRELLIS_SPARSE_HIP_CONV_COMPACT) {
         const void * w = nullptr;
-        st = get_weight(be, weight, wcount, kLayoutConvMfma, ci, co, &w);
+        st = get_weight(be, weight, wcount,
+                        algo == TRELLIS_SPARSE_HIP_CONV_COMPACT ? kLayoutConvMfmaGrouped : kLayoutConvMfma, ci, co,
+                        &w);
         if (st != TRELLIS_STATUS_OK) return st;
-        auto launch = algo == TRELLIS_SPARSE_HIP_CONV_COMPACT ? launch_conv_mfma_compact : launch_conv_mfma_masked;
         stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
-        err = launch(dt, feats->ptr, (const int32_t *) rulebook->nbr.ptr, (const uint32_t *) rulebook->mask.ptr, w,
-                     (const float *) bd, out->ptr, n, ci, co, be->stream);
+        if (algo == TRELLIS_SPARSE_HIP_CONV_COMPACT) {
+            err = launch_conv_mfma_stream(dt, feats->ptr, (const int32_t *) rulebook->pair_src.ptr,
+                                          (const int32_t *) rulebook->pair_dst.ptr,
+                                          (const int32_t *) rulebook->tile_off.ptr,
+                                          (const int32_t *) rulebook->tile_counts.ptr, w, (const float *) bd,
+                                          out->ptr, n, ci, co, be->stream);
+        } else {
+            err = launch_conv_mfma_masked(dt, feats->ptr, (const int32_t *) rulebook->nbr.ptr,
+                                          (const uint32_t *) rulebook->mask.ptr, w, (const float *) bd, out->ptr, n,
+                                          ci, co, be->stream);
+        }
         stage_end(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
     } else {
         const void * w = nullptr;
@@ -1183,23 +1206,30 @@ trellis_status trellis_sparse_hip_download_pairs(trellis_sparse_backend * backen
     }
     if (src_out == nullptr && dst_out == nullptr) return TRELLIS_STATUS_OK;
     if (total > capacity) return tsh::fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "download_pairs: capacity too small");
-    int64_t at = 0;
-    const int64_t n = rulebook->n;
-    for (int k = 0; k < 27 && err == hipSuccess; ++k) {
-        const size_t bytes = (size_t) counts[k] * 4;
-        if (bytes == 0) continue;
-        if (src_out != nullptr) {
-            err = hipMemcpyAsync(src_out + at, (const int32_t *) rulebook->pair_src.ptr + (int64_t) k * n, bytes,
-                                 hipMemcpyDeviceToHost, be->stream);
-        }
-        if (err == hipSuccess && dst_out != nullptr) {
-            err = hipMemcpyAsync(dst_out + at, (const int32_t *) rulebook->pair_dst.ptr + (int64_t) k * n, bytes,
-                                 hipMemcpyDeviceToHost, be->stream);
-        }
-        at += counts[k];
-    }
+    // The device lists are tile-major; reorder them to the canonical
+    // offset-major order (destination ascending within an offset).
+    const int64_t tiles = rulebook->n_tiles;
+    std::vector<int32_t> off((size_t) tiles * 27), cnt((size_t) tiles * 27), hs((size_t) total), hd((size_t) total);
+    err = hipMemcpyAsync(off.data(), rulebook->tile_off.ptr, off.size() * 4, hipMemcpyDeviceToHost, be->stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(cnt.data(), rulebook->tile_counts.ptr, cnt.size() * 4, hipMemcpyDeviceToHost, be->stream);
+    if (err == hipSuccess && total > 0)
+        err = hipMemcpyAsync(hs.data(), rulebook->pair_src.ptr, (size_t) total * 4, hipMemcpyDeviceToHost, be->stream);
+    if (err == hipSuccess && total > 0)
+        err = hipMemcpyAsync(hd.data(), rulebook->pair_dst.ptr, (size_t) total * 4, hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
-    return tsh::hip_status(be, err, "download_pairs");
+    if (err != hipSuccess) return tsh::hip_status(be, err, "download_pairs");
+    int64_t at = 0;
+    for (int k = 0; k < 27; ++k) {
+        for (int64_t t = 0; t < tiles; ++t) {
+            const int64_t from = off[(size_t) t * 27 + k], c = cnt[(size_t) t * 27 + k];
+            if (c <= 0) continue;
+            if (src_out != nullptr) memcpy(src_out + at, hs.data() + from, (size_t) c * 4);
+            if (dst_out != nullptr) memcpy(dst_out + at, hd.data() + from, (size_t) c * 4);
+            at += c;
+        }
+    }
+    return TRELLIS_STATUS_OK;
 }
 
 trellis_status trellis_sparse_hip_upload_raw(trellis_sparse_backend * backend, const void * src, size_t count,

@@ -3,8 +3,7 @@
 // out[i][o] = bias[o] + sum_k sum_c x[nbr[i][k]][c] * W[o][k][c]
 // (src/ops/sparse/trellis_sparse_cpu.c:324-373; weight [Co][27][Ci], :361).
 //
-// Two output-stationary schedules, both writing every output row exactly once
-// (no scatter, no atomics, deterministic):
+// Three schedules, each deterministic:
 //
 //  * generic  - VALU, any channel counts, any storage type.  For each output
 //               it follows the reference's operation order exactly: start at
@@ -12,14 +11,19 @@
 //               rounded fp32 dot product (no fused multiply-add) added to the
 //               row.  With fp32 storage the result is bit-identical to the
 //               reference CPU backend.
-//  * mfma     - bf16/fp16 storage, Ci % 32 == 0, Co % 64 == 0.  Implicit GEMM
-//               on v_mfma_f32_16x16x32_{bf16,f16} with fp32 accumulation.  A
-//               block owns 64 output rows x 64/128 output channels; each
-//               wavefront owns 32 rows x 32/64 channels.  For each offset the
-//               lanes gather their source rows straight into MFMA A fragments
-//               (16 contiguous bytes per lane) and read pre-packed weight
-//               fragments; row groups of 16 with no valid neighbour skip the
-//               offset.
+//  * masked   - bf16/fp16 storage, Ci % 32 == 0, Co % 64 == 0.  Implicit GEMM
+//               on v_mfma_f32_16x16x32_{bf16,f16} with fp32 accumulation over
+//               the dense neighbour table.  A block owns 64 output rows x
+//               64/128 output channels; each wavefront owns 32 rows x 32/64
+//               channels.  For each offset the lanes gather their source rows
+//               straight into MFMA A fragments (16 contiguous bytes per lane)
+//               and read pre-packed weight fragments; row groups of 16 with no
+//               valid neighbour skip the offset, others multiply zeros for
+//               their missing neighbours.
+//  * compact  - bf16/fp16 storage, Ci % 64 == 0, Co % 64 == 0.  The same MFMA
+//               tiles driven by the kernel map's compacted per-tile pair
+//               lists, so the MFMA rows are valid (src, dst) pairs only; sums
+//               of a 256-row tile stay in LDS until one final store.
 #include "tsh_internal.h"
 
 namespace tsh {
@@ -33,6 +37,16 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t grid) {
     const int64_t q = grid / kXcd, r = grid % kXcd;
     const int64_t xcd = bid % kXcd, slot = bid / kXcd;
     return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+}
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also drains every
+// outstanding global load (vmcnt(0)), which would empty the register prefetch
+// ring of the streamed kernel at each barrier; its global loads only read
+// data that no block writes.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // ---------------------------------------------------------------------------
@@ -252,173 +266,202 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
 }
 
 // ---------------------------------------------------------------------------
-// Compacted MFMA kernel (bf16 / fp16 storage).
+// Compacted MFMA kernel (bf16 / fp16 storage), streamed.
 //
-// A block owns TM output rows x BN output channels.  Their fp32 sums live in
-// LDS.  For each offset k the block compacts its rows that have a neighbour at
-// k into a (src, dst) list (wavefront ballots, destination ascending), so the
-// MFMA row dimension runs over valid pairs only: 16-pair row blocks are
-// gathered straight into A fragments, multiplied by the k-th weight slice
-// (staged through LDS and shared by the four wavefronts) and the 16 x BN
-// partial results are added into the LDS sums of their destination rows.
-// Within one offset a destination occurs at most once, so no two lanes touch
-// the same LDS word; offsets are applied in k order, so the result is
-// deterministic.  The tile's rows are written once at the end.
+// A block owns one 256-row map tile x BN output channels; the fp32 sums of
+// those rows live in LDS.  The kernel map's tile-major pair lists give, for
+// each offset k, the tile's valid (src, dst) pairs in destination order.  The
+// block walks "units" (offset k, up to 128 of its pairs) in k order; each unit
+// is Ci/32 K steps of MFMA work over 16-pair row blocks, so the MFMA row
+// dimension runs over valid pairs only.  Wavefront w multiplies row blocks
+// (w & 1), +2, +4, +6 of the unit by channel half (w >> 1).
 //
-// Wavefront w covers channel half (w >> 1) and row blocks (w & 1), +2, +4, +6
-// of each pass of eight row blocks.
+// Weights use the grouped packing: packed column ch*WN + nt*16 + l16 holds
+// output channel ch*WN + l16*NT + nt, so each lane's MFMA results for a row
+// are NT adjacent channels and a unit's results reach the LDS sums as one
+// vector read-modify-write per row (LDS float atomics are far slower).
+//
+// Latency: operand fragments (gathered A rows from the pair list, weight
+// fragments from L2) are loaded DEPTH K steps ahead into a register ring that
+// runs across unit boundaries (Ci/32 is a multiple of DEPTH, so every unit
+// starts at ring slot 0); the next unit's src/dst lists are staged into an
+// LDS ring one unit ahead.  One barrier per unit, which orders LDS only, so
+// the register ring stays in flight across it.  At the end of a unit the
+// 16 x BN partial products are added into the destination rows' LDS sums;
+// within a unit a destination occurs at most once and units are applied in
+// order, so the result is deterministic.  The tile's rows are written once.
 // ---------------------------------------------------------------------------
-template <int DT, int BN, int TM>
-__global__ void __launch_bounds__(256) k_conv_mfma_compact(const typename Store<DT>::T * __restrict__ x,
-                                                           const int32_t * __restrict__ nbr,
-                                                           const uint32_t * __restrict__ mask,
-                                                           const typename Store<DT>::T * __restrict__ w16,
-                                                           const float * __restrict__ bias,
-                                                           typename Store<DT>::T * __restrict__ y, int64_t n,
-                                                           int ci, int co, int64_t n_col_tiles) {
+template <int DT, int BN, int DEPTH>
+__global__ void __launch_bounds__(256) k_conv_mfma_stream(const typename Store<DT>::T * __restrict__ x,
+                                                          const int32_t * __restrict__ pair_src,
+                                                          const int32_t * __restrict__ pair_dst,
+                                                          const int32_t * __restrict__ tile_off,
+                                                          const int32_t * __restrict__ tile_counts,
+                                                          const typename Store<DT>::T * __restrict__ w16,
+                                                          const float * __restrict__ bias,
+                                                          typename Store<DT>::T * __restrict__ y, int64_t n,
+                                                          int ci, int co, int64_t n_col_tiles) {
     using T = typename Store<DT>::T;
     using V = typename Mfma<DT>::V;
+    constexpr int TM = kMapTile;     // rows per block = rows per kernel-map tile
     constexpr int ACC_LD = BN + 4;   // padded fp32 row stride of the LDS sums
     constexpr int BK = 32;           // input channels per K step
     constexpr int WN = BN / 2;       // channels per wavefront
     constexpr int NT = WN / 16;      // MFMA column tiles per wavefront
-    constexpr int QB = 4;            // row blocks per wavefront per pass
-    constexpr int ROWS_PER_THREAD = (TM + 255) / 256;
+    constexpr int QB = 4;            // row blocks per wavefront per unit
+    constexpr int PASS = 128;        // pairs per unit
+    constexpr int MAX_UNITS = 27 * (TM / PASS);
     __shared__ float s_acc[TM * ACC_LD];
-    __shared__ int32_t s_src[TM];
-    __shared__ int32_t s_dst[TM];
-    __shared__ int32_t s_wcnt[4 * ROWS_PER_THREAD];
-    __shared__ uint32_t s_need;
+    __shared__ int32_t s_rsrc[4][PASS];
+    __shared__ uint8_t s_rdst[4][PASS];
+    __shared__ int32_t s_uk[MAX_UNITS], s_ustart[MAX_UNITS], s_ucnt[MAX_UNITS];
+    __shared__ int32_t s_cnt[27], s_start[27];
+    __shared__ int32_t s_units;
 
     const int t = threadIdx.x;
     const int lane = t & 63;
-    const int wave = t >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int rh = wave & 1, ch = wave >> 1;
     const int l16 = lane & 15, lg = lane >> 4;
     const int64_t logical = xcd_remap(blockIdx.x, (int64_t) gridDim.x);
-    const int64_t row0 = (logical / n_col_tiles) * TM;
+    const int64_t tile = logical / n_col_tiles;
+    const int64_t row0 = tile * TM;
     const int col0 = (int) (logical % n_col_tiles) * BN;
     const int ci8 = ci >> 3;
-    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const int KS = ci / BK;
 
     for (int i = t; i < TM * ACC_LD; i += 256) s_acc[i] = 0.0f;
-    if (t == 0) s_need = 0u;
-    uint32_t m[ROWS_PER_THREAD];
-#pragma unroll
-    for (int q = 0; q < ROWS_PER_THREAD; ++q) {
-        const int local = q * 256 + t;
-        const int64_t row = row0 + local;
-        m[q] = (local < TM && row < n) ? mask[row] : 0u;
+    if (t < 27) {
+        s_cnt[t] = tile_counts[tile * 27 + t];
+        s_start[t] = tile_off[tile * 27 + t];
     }
-    __syncthreads();
-    {
-        uint32_t any = 0;
-#pragma unroll
-        for (int q = 0; q < ROWS_PER_THREAD; ++q) any |= m[q];
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) any |= __shfl_xor(any, d);
-        if (lane == 0) atomicOr(&s_need, any);
+    lds_barrier();
+    // Unit table: offset k contributes ceil(count / PASS) units, in k order.
+    if (t < 27) {
+        int u = 0;
+#pragma unroll 1
+        for (int k = 0; k < t; ++k) u += (s_cnt[k] + PASS - 1) / PASS;
+        const int c = s_cnt[t];
+#pragma unroll 1
+        for (int p = 0; p < c; p += PASS, ++u) {
+            s_uk[u] = t;
+            s_ustart[u] = s_start[t] + p;
+            s_ucnt[u] = c - p < PASS ? c - p : PASS;
+        }
+        if (t == 26) s_units = u;
     }
-    __syncthreads();
-    const uint32_t need = s_need;
+    lds_barrier();
+    const int U = s_units;
+    if (U == 0) return;  // unreachable for a tile with rows: the centre offset pairs every row with itself
 
-    for (int k = 0; k < 27; ++k) {
-        if (((need >> k) & 1u) == 0) continue;
-        // Compact this offset's pairs: destination-ascending (src, dst) list.
-        int32_t rank[ROWS_PER_THREAD];
+    // Unit lists: threads 0..127 carry src entries, 128..255 dst entries.
+    // Padding entries repeat the unit's last pair, so every gather stays in
+    // range; past the last unit the last unit is loaded again (never used).
+    const int le = t & (PASS - 1);
+    const int32_t * list = t < PASS ? pair_src : pair_dst;
+    const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
+    auto list_load = [&](int u) -> int32_t {
+        const int lu = u < U ? u : U - 1;
+        const int c = s_ucnt[lu];
+        return list[s_ustart[lu] + (le < c ? le : c - 1)];
+    };
+    auto list_store = [&](int u, int32_t v) {
+        if (t < PASS) s_rsrc[u & 3][le] = v;
+        else s_rdst[u & 3][le] = (uint8_t) (v - list_bias);
+    };
+    list_store(0, list_load(0));
+    int32_t lv = list_load(1);
+    lds_barrier();
+
+    V ra[DEPTH][QB];
+    V rb[DEPTH][NT];
+    f32x4 acc[QB][NT];
 #pragma unroll
-        for (int q = 0; q < ROWS_PER_THREAD; ++q) {
-            const uint64_t bal = __ballot((m[q] >> k) & 1u);
-            rank[q] = __popcll(bal & lt);
-            if (lane == 0) s_wcnt[q * 4 + wave] = __popcll(bal);
+    for (int q = 0; q < QB; ++q)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Prefetch cursor (unit pu, K step ps).
+    int pu = 0, ps = 0;
+    const T * bcol = w16 + ((int64_t) lg * co + col0 + ch * WN + l16) * 8;
+    auto issue = [&](V * a, V * b) {
+        const int lu = pu < U ? pu : U - 1;
+        const int slot = lu & 3;
+        const int64_t koff = (int64_t) s_uk[lu] * ci8 * co * 8;
+#pragma unroll
+        for (int q = 0; q < QB; ++q) {
+            const int32_t src = s_rsrc[slot][(rh + 2 * q) * 16 + l16];
+            a[q] = *(const V *) (x + (int64_t) src * ci + ps * BK + lg * 8);
         }
-        __syncthreads();
-        int c = 0;
 #pragma unroll
-        for (int q = 0; q < ROWS_PER_THREAD; ++q) {
-            int base = c;
-            for (int w = 0; w < 4; ++w) {
-                base += w < wave ? s_wcnt[q * 4 + w] : 0;
-                c += s_wcnt[q * 4 + w];
-            }
-            if ((m[q] >> k) & 1u) {
-                const int local = q * 256 + t;
-                s_src[base + rank[q]] = nbr[(row0 + local) * 27 + k];
-                s_dst[base + rank[q]] = local;
-            }
+        for (int nt = 0; nt < NT; ++nt) b[nt] = *(const V *) (bcol + koff + ((int64_t) ps * 4 * co + nt * 16) * 8);
+        if (++ps == KS) {
+            ps = 0;
+            ++pu;
         }
-        __syncthreads();
-        const int nb = (c + 15) >> 4;
-        const T * wk = w16 + (int64_t) k * ci8 * co * 8;
-        for (int pb = 0; pb < nb; pb += 2 * QB) {
-            f32x4 acc[QB][NT];
-            int32_t src[QB];
-            bool live[QB];
+    };
 #pragma unroll
-            for (int q = 0; q < QB; ++q) {
-                const int j = pb + rh + 2 * q;
-                live[q] = j < nb;
-                const int p = j * 16 + l16;
-                src[q] = (live[q] && p < c) ? s_src[p] : -1;
+    for (int r = 0; r < DEPTH; ++r) {
+        issue(ra[r], rb[r]);
+        __builtin_amdgcn_sched_barrier(0);  // ring slots issue in ring order
+    }
+
+    for (int cu = 0; cu < U; ++cu) {
+        // The list of unit cu + 1 becomes visible to the prefetches of this unit.
+        list_store(cu + 1, lv);
+        lv = list_load(cu + 2);
+        lds_barrier();
+        const int c = s_ucnt[cu];
+        // Row blocks past the unit's count multiply padding (never flushed);
+        // keeping the MFMA stream branch-free lets every operand wait be a
+        // precise count of the loads issued after it.
+        int s0 = 0;
+        do {
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int r = 0; r < DEPTH; ++r) {
+#pragma unroll
+                for (int q = 0; q < QB; ++q)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) acc[q][nt] = Mfma<DT>::mac(ra[r][q], rb[r][nt], acc[q][nt]);
+                issue(ra[r], rb[r]);
+                // Keep each step's loads in its step: the scheduler would
+                // otherwise sink the whole ring's loads below the last MFMA.
+                __builtin_amdgcn_sched_barrier(0);
             }
-            // Operand fragments for K step s, loaded one step ahead into two
-            // register sets that alternate (no copies, so a wait only ever
-            // covers older loads).  A: gathered source rows (padding slots read
-            // row 0; their products are never added).  B: this wavefront's
-            // weight columns, read from L2 (the packed weights are L2-resident).
-            int64_t abase[QB];
+            s0 += DEPTH;
+        } while (s0 < KS);
+        const int slot = cu & 3;
 #pragma unroll
-            for (int q = 0; q < QB; ++q) abase[q] = (int64_t) (src[q] >= 0 ? src[q] : 0) * ci + lg * 8;
-            const T * bbase = wk + ((int64_t) lg * co + col0 + ch * WN + l16) * 8;
-            auto load = [&](int s, V * a, V * b) {
-#pragma unroll
-                for (int q = 0; q < QB; ++q) a[q] = *(const V *) (x + abase[q] + s * BK);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) b[nt] = *(const V *) (bbase + ((int64_t) s * 4 * co + nt * 16) * 8);
-            };
-            const int ks = ci / BK;
-            auto step = [&](int s, const V * a, const V * b, V * an, V * bn) {
-                if (s + 1 < ks) load(s + 1, an, bn);
-#pragma unroll
-                for (int q = 0; q < QB; ++q) {
-                    if (!live[q]) continue;
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) acc[q][nt] = Mfma<DT>::mac(a[q], b[nt], acc[q][nt]);
-                }
-            };
-            V a0[QB], a1[QB], b0[NT], b1[NT];
-            load(0, a0, b0);
-            int s = 0;
-            for (; s + 1 < ks; s += 2) {
-                step(s, a0, b0, a1, b1);
-                step(s + 1, a1, b1, a0, b0);
-            }
-            if (s < ks) step(s, a0, b0, a1, b1);
-            // Add the partial products into the destination rows' sums.
-#pragma unroll
-            for (int q = 0; q < QB; ++q) {
-                if (!live[q]) continue;
-                const int j = pb + rh + 2 * q;
+        for (int q = 0; q < QB; ++q) {
+            const int j = rh + 2 * q;
+            if (j * 16 < c) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int p = j * 16 + lg * 4 + i;
                     if (p < c) {
-                        float * dst = s_acc + s_dst[p] * ACC_LD + ch * WN + l16;
+                        // The lane's NT columns are adjacent (grouped weight
+                        // packing): one vector read-modify-write.  No other
+                        // lane touches them before the next barrier.
+                        using Row = float __attribute__((ext_vector_type(NT)));
+                        Row * dst = (Row *) (s_acc + s_rdst[slot][p] * ACC_LD + ch * WN + l16 * NT);
+                        Row v = *dst;
 #pragma unroll
-                        for (int nt = 0; nt < NT; ++nt) atomicAdd(dst + nt * 16, acc[q][nt][i]);
+                        for (int nt = 0; nt < NT; ++nt) v[nt] += acc[q][nt][i];
+                        *dst = v;
                     }
                 }
             }
+            // Row blocks past the count accumulated padding: clear them too.
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-        __syncthreads();
     }
+    lds_barrier();
     // Epilogue: bias, round to the storage type, 16-byte coalesced stores.
     constexpr int CHUNKS = BN / 8;
     for (int e = t; e < TM * CHUNKS; e += 256) {
-        const int r = e / CHUNKS, cc = (e % CHUNKS) * 8;
-        const int64_t row = row0 + r;
+        const int rr = e / CHUNKS, cc = (e % CHUNKS) * 8;
+        const int64_t row = row0 + rr;
         if (row >= n) continue;
         union {
             int4 v;
@@ -427,7 +470,7 @@ __global__ void __launch_bounds__(256) k_conv_mfma_compact(const typename Store<
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const float bv = bias != nullptr ? bias[col0 + cc + u] : 0.0f;
-            float v = s_acc[r * ACC_LD + cc + u] + bv;
+            const float v = s_acc[rr * ACC_LD + cc + u] + bv;
             if constexpr (DT == kBF16) {
                 o.h[u] = f32_to_bf16(v);
             } else {
@@ -493,52 +536,56 @@ hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nb
     return hipGetLastError();
 }
 
-hipError_t launch_conv_mfma_compact(int dtype, const void * x, const int32_t * nbr, const uint32_t * mask,
-                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
-                                    hipStream_t s) {
-    if (!conv_mfma_supported(dtype, ci, co)) {
-        return hipErrorInvalidValue;
-    }
-    // Tile shapes (rows x channels): the LDS sums take TM*(BN+4)*4 bytes, so
-    // 128x128 and 256x64 leave room for two blocks per CU, 256x128 and 512x64
-    // for one.  TRELLIS_HIP_CONV_TILE=1..4 pins a shape for tuning; the shape
-    // does not change the order of any sum.
-    static const int forced = [] {
-        const char * e = getenv("TRELLIS_HIP_CONV_TILE");
-        return e != nullptr ? atoi(e) : 0;
-    }();
-    int shape = forced;
-    if (shape < 1 || shape > 4 || ((shape == 1 || shape == 2) && co % 128 != 0)) {
-        shape = co % 128 == 0 ? 2 : 3;
-    }
-    static const int kTm[5] = {0, 256, 128, 256, 512};
-    static const int kBn[5] = {0, 128, 128, 64, 64};
-    const int tm = kTm[shape], bn = kBn[shape];
-    const int64_t row_tiles = (n + tm - 1) / tm;
-    const int64_t col_tiles = co / bn;
-    const int64_t grid = row_tiles * col_tiles;
+
+int conv_stream_group(int co) { return co % 128 == 0 ? 4 : 2; }
+
+bool conv_stream_supported(int dtype, int ci, int co) {
+    // Units must span a whole number of prefetch rings (Ci/32 steps, ring
+    // depth 2 or 4), so the prefetch never runs more than one unit ahead.
+    return conv_mfma_supported(dtype, ci, co) && ci % 64 == 0;
+}
+
+namespace {
+template <int DT, int BN, int DEPTH>
+hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
+                           const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
+                           const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
+    using T = typename Store<DT>::T;
+    const int64_t tiles = (n + kMapTile - 1) / kMapTile;
+    const int64_t col_tiles = co / BN;
+    const int64_t grid = tiles * col_tiles;
     if (grid > 0x7fffffffLL) {
         return hipErrorInvalidValue;
     }
-#define TSH_LAUNCH(DTV, TYPE, BNV, TMV)                                                                         \
-    k_conv_mfma_compact<DTV, BNV, TMV><<<(unsigned) grid, 256, 0, s>>>((const TYPE *) x, nbr, mask,            \
-                                                                        (const TYPE *) w16, bias, (TYPE *) y, n, \
-                                                                        ci, co, col_tiles)
-#define TSH_SHAPES(DTV, TYPE)                              \
-    switch (shape) {                                       \
-        case 1: TSH_LAUNCH(DTV, TYPE, 128, 256); break;    \
-        case 2: TSH_LAUNCH(DTV, TYPE, 128, 128); break;    \
-        case 3: TSH_LAUNCH(DTV, TYPE, 64, 256); break;     \
-        default: TSH_LAUNCH(DTV, TYPE, 64, 512); break;    \
+    k_conv_mfma_stream<DT, BN, DEPTH><<<(unsigned) grid, 256, 0, s>>>((const T *) x, pair_src, pair_dst, tile_off,
+                                                                      tile_counts, (const T *) w16, bias, (T *) y,
+                                                                      n, ci, co, col_tiles);
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
+                            const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
+                            const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
+    const bool wide = co % 128 == 0;
+    const bool deep = ci % 128 == 0;
+    if (wide && deep) return launch_stream_t<DT, 128, 4>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
+    if (wide) return launch_stream_t<DT, 128, 2>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
+    if (deep) return launch_stream_t<DT, 64, 4>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
+    return launch_stream_t<DT, 64, 2>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
+}
+}  // namespace
+
+hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const int32_t * pair_dst,
+                                   const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
+                                   const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
+    if (!conv_stream_supported(dtype, ci, co)) {
+        return hipErrorInvalidValue;
     }
     if (dtype == kBF16) {
-        TSH_SHAPES(kBF16, uint16_t)
-    } else {
-        TSH_SHAPES(kF16, _Float16)
+        return launch_stream_dt<kBF16>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
     }
-#undef TSH_SHAPES
-#undef TSH_LAUNCH
-    return hipGetLastError();
+    return launch_stream_dt<kF16>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
 }
 
 }  // namespace tsh

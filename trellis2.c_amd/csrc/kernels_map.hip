@@ -13,7 +13,8 @@
 //   nbr          int32 [n][27]
 //   mask         uint32 [n], bit k <=> nbr[i][k] >= 0
 //   tile_counts  int32 [n_tiles][27] valid pairs per 256-row tile and offset
-//   pairs        int32 src/dst [27][n], offset k in [k*n, k*n + count_k), dst ascending.
+//   pairs        int32 src/dst, tile-major: tile t's list for offset k starts at tile_off[t][k]
+//                (tiles ascending, offsets ascending within a tile, dst ascending within an offset).
 //
 // A voxel's 27 neighbours lie in at most 8 bricks (on average 3.4), so the
 // kernel map does a few hash probes per voxel plus 27 reads from 256-byte
@@ -278,58 +279,28 @@ __global__ void __launch_bounds__(kBlock) k_neighbors(const int4 * __restrict__ 
     }
 }
 
-// Exclusive prefix over tiles, one block per offset.
-__global__ void __launch_bounds__(1024) k_tile_scan(const int32_t * __restrict__ tile_counts, int64_t n_tiles,
-                                                    int32_t * __restrict__ tile_off, int32_t * __restrict__ k_count) {
-    __shared__ int32_t s_wave[16];
-    __shared__ int32_t s_carry;
+// Per-offset pair totals: block k sums column k of tile_counts [n_tiles][27].
+// (The list starts themselves are an exclusive scan of the flattened
+// tile_counts, since the pair arrays are ordered by tile, then offset.)
+__global__ void __launch_bounds__(kBlock) k_offset_totals(const int32_t * __restrict__ tile_counts, int64_t n_tiles,
+                                                          int32_t * __restrict__ k_count) {
+    __shared__ int32_t s_wave[kBlock / 64];
     const int k = blockIdx.x;
-    const int t = threadIdx.x;
-    const int lane = lane_id();
-    const int wave = t >> 6;
-    if (t == 0) {
-        s_carry = 0;
-    }
-    __syncthreads();
-    for (int64_t base = 0; base < n_tiles; base += 1024) {
-        const int64_t idx = base + t;
-        const int32_t v = idx < n_tiles ? tile_counts[idx * 27 + k] : 0;
-        // Inclusive scan within the wavefront.
-        int32_t incl = v;
+    int32_t v = 0;
+    for (int64_t t = threadIdx.x; t < n_tiles; t += kBlock) v += tile_counts[t * 27 + k];
 #pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int32_t o = __shfl_up(incl, d);
-            if (lane >= d) {
-                incl += o;
-            }
-        }
-        if (lane == 63) {
-            s_wave[wave] = incl;
-        }
-        __syncthreads();
-        int32_t wave_base = 0;
-        int32_t chunk = 0;
-        for (int w = 0; w < 16; ++w) {
-            const int32_t sw = s_wave[w];
-            wave_base += w < wave ? sw : 0;
-            chunk += sw;
-        }
-        const int32_t carry = s_carry;
-        if (idx < n_tiles) {
-            tile_off[idx * 27 + k] = carry + wave_base + incl - v;
-        }
-        __syncthreads();
-        if (t == 0) {
-            s_carry = carry + chunk;
-        }
-        __syncthreads();
-    }
-    if (t == 0) {
-        k_count[k] = s_carry;
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+    if (lane_id() == 0) s_wave[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t total = 0;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) total += s_wave[w];
+        k_count[k] = total;
     }
 }
 
-// Compacted pair lists, destination ascending within each offset.
+// Compacted pair lists in tile-major order, destination ascending within each (tile, offset).
 __global__ void __launch_bounds__(kBlock) k_fill_pairs(const int32_t * __restrict__ nbr,
                                                        const uint32_t * __restrict__ mask, int64_t n,
                                                        const int32_t * __restrict__ tile_off,
@@ -363,7 +334,7 @@ __global__ void __launch_bounds__(kBlock) k_fill_pairs(const int32_t * __restric
             for (int w = 0; w < wave; ++w) {
                 base += s_wave_cnt[k][w];
             }
-            const int64_t pos = (int64_t) k * n + base + rank[k];
+            const int64_t pos = (int64_t) base + rank[k];
             pair_src[pos] = nbr[i * 27 + k];
             pair_dst[pos] = (int32_t) i;
         }
@@ -421,9 +392,8 @@ hipError_t launch_neighbors(const int32_t * coords, int64_t n, const uint64_t * 
     return hipGetLastError();
 }
 
-hipError_t launch_tile_scan(const int32_t * tile_counts, int64_t n_tiles, int32_t * tile_off, int32_t * k_count,
-                            hipStream_t s) {
-    k_tile_scan<<<27, 1024, 0, s>>>(tile_counts, n_tiles, tile_off, k_count);
+hipError_t launch_offset_totals(const int32_t * tile_counts, int64_t n_tiles, int32_t * k_count, hipStream_t s) {
+    k_offset_totals<<<27, kBlock, 0, s>>>(tile_counts, n_tiles, k_count);
     return hipGetLastError();
 }
 

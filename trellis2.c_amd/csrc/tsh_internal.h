@@ -83,16 +83,17 @@ struct trellis_sparse_rulebook {
     tsh::DevMem bkeys;       // uint64 [table_slots]
     tsh::DevMem bidx;        // int32  [table_slots]
     tsh::DevMem pool;        // int32  [cap_bricks][64] voxel rows, -1 = empty
-    tsh::DevMem counters;    // int32  [4]: bricks, duplicate flag, (reserved)
+    tsh::DevMem counters;    // int32  [16]: bricks, duplicate flag, pair total, (reserved)
     // Kernel map.
     tsh::DevMem nbr;         // int32  [n][27]
     tsh::DevMem mask;        // uint32 [n] bit k set when nbr[i][k] >= 0
     int64_t n_tiles;         // ceil(n / kMapTile)
     tsh::DevMem tile_counts; // int32  [n_tiles][27]
-    tsh::DevMem tile_off;    // int32  [n_tiles][27] exclusive prefix over tiles
+    tsh::DevMem tile_off;    // int32  [n_tiles][27] start of (tile, k) in the pair arrays
     tsh::DevMem k_count;     // int32  [27]
-    tsh::DevMem pair_src;    // int32  [27][n] (offset k occupies [k*n, k*n + k_count[k]))
-    tsh::DevMem pair_dst;    // int32  [27][n]
+    tsh::DevMem scan_tmp;    // scratch of the tile_off scan
+    tsh::DevMem pair_src;    // int32  [P] tile-major: tiles ascending, then k, then dst ascending
+    tsh::DevMem pair_dst;    // int32  [P]
 };
 
 struct trellis_sparse_c2s_device_map {
@@ -121,8 +122,9 @@ hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t
 hipError_t launch_neighbors(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
                             int64_t slots, const int32_t * pool, int32_t * nbr, uint32_t * mask,
                             int32_t * tile_counts, hipStream_t s);
-hipError_t launch_tile_scan(const int32_t * tile_counts, int64_t n_tiles, int32_t * tile_off, int32_t * k_count,
-                            hipStream_t s);
+// Column sums of tile_counts [n_tiles][27] -> k_count[27].  (tile_off is the
+// exclusive scan of the flattened tile_counts: launch_scan_exclusive.)
+hipError_t launch_offset_totals(const int32_t * tile_counts, int64_t n_tiles, int32_t * k_count, hipStream_t s);
 hipError_t launch_fill_pairs(const int32_t * nbr, const uint32_t * mask, int64_t n, const int32_t * tile_off,
                              int32_t * pair_src, int32_t * pair_dst, hipStream_t s);
 
@@ -135,9 +137,14 @@ bool conv_mfma_supported(int dtype, int ci, int co);
 hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nbr, const uint32_t * mask,
                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
                                    hipStream_t s);
-hipError_t launch_conv_mfma_compact(int dtype, const void * x, const int32_t * nbr, const uint32_t * mask,
-                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
-                                    hipStream_t s);
+// Streamed compacted schedule over the tile-major pair lists (needs ci % 64 == 0).
+// Its weights use the grouped packing: [27][ci/8][co][8] whose packed column
+// b*16g + nt*16 + l holds channel b*16g + l*g + nt, g = conv_stream_group(co).
+int conv_stream_group(int co);
+bool conv_stream_supported(int dtype, int ci, int co);
+hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const int32_t * pair_dst,
+                                   const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
+                                   const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s);
 
 // Everything else (kernels_misc.hip).
 hipError_t launch_convert_from_f32(int dtype, const float * src, void * dst, int64_t count, hipStream_t s);
