@@ -273,26 +273,32 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
 // each offset k, the tile's valid (src, dst) pairs in destination order.  The
 // block walks "units" (offset k, up to 128 of its pairs) in k order; each unit
 // is Ci/32 K steps of MFMA work over 16-pair row blocks, so the MFMA row
-// dimension runs over valid pairs only.  Wavefront w multiplies row blocks
-// (w & 1), +2, +4, +6 of the unit by channel half (w >> 1).
+// dimension runs over valid pairs only.  With NW wavefronts (8: two per SIMD,
+// so one's VALU and LDS work overlaps the other's MFMAs) wavefront w
+// multiplies row blocks w % (NW/2) + (NW/2) q of the unit by channel half
+// w / (NW/2).
+//
+// Operands.  A (gathered feature rows) goes global -> registers through a
+// DEPTH-step ring that runs across unit boundaries (Ci/32 is a multiple of
+// DEPTH, so every unit starts at ring slot 0).  B (the unit's weight slice,
+// 32 channels x BN per step) is loaded once per block: the threads bring it
+// through a DEPTH-step register ring and store it into a 3-slot LDS ring two
+// steps ahead, and all wavefronts read their fragments from there one step
+// ahead, which halves the weight bytes through the vector memory path and
+// keeps LDS latency off the MFMA stream.  One barrier per step publishes the
+// weights; it orders LDS only, so both register rings stay in flight across
+// it.
 //
 // Weights use the grouped packing: packed column ch*WN + nt*16 + l16 holds
 // output channel ch*WN + l16*NT + nt, so each lane's MFMA results for a row
 // are NT adjacent channels and a unit's results reach the LDS sums as one
-// vector read-modify-write per row (LDS float atomics are far slower).
-//
-// Latency: operand fragments (gathered A rows from the pair list, weight
-// fragments from L2) are loaded DEPTH K steps ahead into a register ring that
-// runs across unit boundaries (Ci/32 is a multiple of DEPTH, so every unit
-// starts at ring slot 0); the next unit's src/dst lists are staged into an
-// LDS ring one unit ahead.  One barrier per unit, which orders LDS only, so
-// the register ring stays in flight across it.  At the end of a unit the
-// 16 x BN partial products are added into the destination rows' LDS sums;
-// within a unit a destination occurs at most once and units are applied in
-// order, so the result is deterministic.  The tile's rows are written once.
+// vector read-modify-write per row.  Padding rows of a unit (past its count)
+// multiply a repeated valid pair and are added into a spare row.  Within a
+// unit a destination occurs at most once and units are applied in order, so
+// the result is deterministic.  The tile's rows are written once at the end.
 // ---------------------------------------------------------------------------
-template <int DT, int BN, int DEPTH>
-__global__ void __launch_bounds__(256) k_conv_mfma_stream(const typename Store<DT>::T * __restrict__ x,
+template <int DT, int BN, int DEPTH, int NW>
+__global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Store<DT>::T * __restrict__ x,
                                                           const int32_t * __restrict__ pair_src,
                                                           const int32_t * __restrict__ pair_dst,
                                                           const int32_t * __restrict__ tile_off,
@@ -304,16 +310,23 @@ __global__ void __launch_bounds__(256) k_conv_mfma_stream(const typename Store<D
     using T = typename Store<DT>::T;
     using V = typename Mfma<DT>::V;
     constexpr int TM = kMapTile;     // rows per block = rows per kernel-map tile
-    constexpr int ACC_LD = BN + 4;   // padded fp32 row stride of the LDS sums
     constexpr int BK = 32;           // input channels per K step
+    constexpr int NTHR = 64 * NW;
     constexpr int WN = BN / 2;       // channels per wavefront
     constexpr int NT = WN / 16;      // MFMA column tiles per wavefront
-    constexpr int QB = 4;            // row blocks per wavefront per unit
+    constexpr int RG = NW / 2;       // row groups: wavefront w takes row blocks w % RG + RG * q
+    constexpr int QB = 8 / RG;       // row blocks per wavefront per unit
     constexpr int PASS = 128;        // pairs per unit
     constexpr int MAX_UNITS = 27 * (TM / PASS);
-    __shared__ float s_acc[TM * ACC_LD];
+    constexpr int BSLOT = 4 * BN * 8;      // weight elements per step: [4 channel groups][BN][8]
+    constexpr int BUNITS = 4 * BN;         // 16-byte pieces of a step's weights
+    constexpr int BLOADS = (BUNITS + NTHR - 1) / NTHR;  // pieces per thread
+    static_assert(NW == 4 || NW == 8, "4 or 8 wavefronts");
+    static_assert(BUNITS % NTHR == 0 || BUNITS < NTHR, "weight pieces split evenly or fit one round");
+    __shared__ float s_acc[(TM + 1) * BN];      // row TM absorbs padding rows
+    __shared__ __attribute__((aligned(16))) T s_b[3][BSLOT];
     __shared__ int32_t s_rsrc[4][PASS];
-    __shared__ uint8_t s_rdst[4][PASS];
+    __shared__ uint16_t s_rdst[4][PASS];        // tile-local dst row, TM for padding
     __shared__ int32_t s_uk[MAX_UNITS], s_ustart[MAX_UNITS], s_ucnt[MAX_UNITS];
     __shared__ int32_t s_cnt[27], s_start[27];
     __shared__ int32_t s_units;
@@ -321,7 +334,7 @@ __global__ void __launch_bounds__(256) k_conv_mfma_stream(const typename Store<D
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int rh = wave & 1, ch = wave >> 1;
+    const int rh = wave % RG, ch = wave / RG;
     const int l16 = lane & 15, lg = lane >> 4;
     const int64_t logical = xcd_remap(blockIdx.x, (int64_t) gridDim.x);
     const int64_t tile = logical / n_col_tiles;
@@ -330,7 +343,7 @@ __global__ void __launch_bounds__(256) k_conv_mfma_stream(const typename Store<D
     const int ci8 = ci >> 3;
     const int KS = ci / BK;
 
-    for (int i = t; i < TM * ACC_LD; i += 256) s_acc[i] = 0.0f;
+    for (int i = t; i < (TM + 1) * BN; i += NTHR) s_acc[i] = 0.0f;
     if (t < 27) {
         s_cnt[t] = tile_counts[tile * 27 + t];
         s_start[t] = tile_off[tile * 27 + t];
@@ -361,105 +374,172 @@ __global__ void __launch_bounds__(256) k_conv_mfma_stream(const typename Store<D
     const int32_t * list = t < PASS ? pair_src : pair_dst;
     const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
     auto list_load = [&](int u) -> int32_t {
+        if (t >= 2 * PASS) return 0;
         const int lu = u < U ? u : U - 1;
         const int c = s_ucnt[lu];
         return list[s_ustart[lu] + (le < c ? le : c - 1)];
     };
     auto list_store = [&](int u, int32_t v) {
-        if (t < PASS) s_rsrc[u & 3][le] = v;
-        else s_rdst[u & 3][le] = (uint8_t) (v - list_bias);
+        if (t < PASS) {
+            s_rsrc[u & 3][le] = v;
+        } else if (t < 2 * PASS) {
+            const int c = s_ucnt[u < U ? u : U - 1];
+            s_rdst[u & 3][le] = (uint16_t) (le < c ? v - list_bias : TM);
+        }
     };
     list_store(0, list_load(0));
     int32_t lv = list_load(1);
     lds_barrier();
 
     V ra[DEPTH][QB];
-    V rb[DEPTH][NT];
+    V rw[DEPTH][BLOADS];
     f32x4 acc[QB][NT];
 #pragma unroll
     for (int q = 0; q < QB; ++q)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Prefetch cursor (unit pu, K step ps).
-    int pu = 0, ps = 0;
-    const T * bcol = w16 + ((int64_t) lg * co + col0 + ch * WN + l16) * 8;
-    auto issue = [&](V * a, V * b) {
+    // A prefetch cursor (unit pu, K step ps) and weight prefetch cursor (bu, bps).
+    // Past the last unit both repeat the last unit (results never used).
+    int pu = 0, ps = 0, bu = 0, bps = 0;
+    auto issue_a = [&](V * a) {
         const int lu = pu < U ? pu : U - 1;
         const int slot = lu & 3;
-        const int64_t koff = (int64_t) s_uk[lu] * ci8 * co * 8;
 #pragma unroll
         for (int q = 0; q < QB; ++q) {
-            const int32_t src = s_rsrc[slot][(rh + 2 * q) * 16 + l16];
+            const int32_t src = s_rsrc[slot][(rh + RG * q) * 16 + l16];
             a[q] = *(const V *) (x + (int64_t) src * ci + ps * BK + lg * 8);
         }
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) b[nt] = *(const V *) (bcol + koff + ((int64_t) ps * 4 * co + nt * 16) * 8);
         if (++ps == KS) {
             ps = 0;
             ++pu;
         }
     };
+    // A step's weights are BUNITS 16-byte pieces, piece u = (channel group
+    // u / BN, column u % BN); thread t brings pieces t, t + NTHR, ...
+    constexpr bool B_ALL = BUNITS >= NTHR;  // every thread has a piece
+    auto issue_b = [&](V * b) {
+        const int lu = bu < U ? bu : U - 1;
+        const T * src = w16 + ((int64_t) (s_uk[lu] * ci8 + bps * 4) * co + col0) * 8;
+        if (B_ALL || t < BUNITS) {
+#pragma unroll
+            for (int h = 0; h < BLOADS; ++h) {
+                const int u = t + h * NTHR;
+                b[h] = *(const V *) (src + ((int64_t) (u / BN) * co + u % BN) * 8);
+            }
+        }
+        if (++bps == KS) {
+            bps = 0;
+            ++bu;
+        }
+    };
+    auto store_b = [&](int slot, const V * b) {
+        if (B_ALL || t < BUNITS) {
+#pragma unroll
+            for (int h = 0; h < BLOADS; ++h) *(V *) (&s_b[slot][(t + h * NTHR) * 8]) = b[h];
+        }
+    };
+    // Weights of steps 0 and 1 straight into LDS slots 0 and 1; then, in the
+    // order the loop issues them, weights of step r + 2 into ring slot
+    // (r + 2) % DEPTH and A of step r into ring slot r.
+    issue_b(rw[0]);
+    store_b(0, rw[0]);
+    issue_b(rw[1]);
+    store_b(1, rw[1]);
 #pragma unroll
     for (int r = 0; r < DEPTH; ++r) {
-        issue(ra[r], rb[r]);
+        issue_b(rw[(r + 2) % DEPTH]);
+        issue_a(ra[r]);
         __builtin_amdgcn_sched_barrier(0);  // ring slots issue in ring order
     }
+    // Fragments of the current step's weights (rf[g & 1] at step g).
+    V rf[2][NT];
+    lds_barrier();
+    {
+        const T * bs = &s_b[0][(lg * BN + ch * WN + l16) * 8];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) rf[0][nt] = *(const V *) (bs + nt * 16 * 8);
+    }
 
+    int bslot = 0;  // LDS slot of the current step's weights (step g: g % 3)
     for (int cu = 0; cu < U; ++cu) {
-        // The list of unit cu + 1 becomes visible to the prefetches of this unit.
+        // The list of unit cu + 1 becomes visible (at the next barrier) to the
+        // prefetches of this unit.
         list_store(cu + 1, lv);
         lv = list_load(cu + 2);
-        lds_barrier();
-        const int c = s_ucnt[cu];
-        // Row blocks past the unit's count multiply padding (never flushed);
-        // keeping the MFMA stream branch-free lets every operand wait be a
-        // precise count of the loads issued after it.
+        // Row blocks past the unit's count multiply padding (flushed into the
+        // spare row); keeping the MFMA stream branch-free lets every operand
+        // wait be a precise count of the loads issued after it.
         int s0 = 0;
         do {
 #pragma unroll
             for (int r = 0; r < DEPTH; ++r) {
+                // Publishes the next step's weights (stored during the previous
+                // step) and, at a unit's first step, the list ring.
+                lds_barrier();
+                const int next = bslot == 2 ? 0 : bslot + 1;
+                const int after = next == 2 ? 0 : next + 1;  // held step g-1, read before the last barrier
+                const T * bs = &s_b[next][(lg * BN + ch * WN + l16) * 8];
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) rf[(r + 1) & 1][nt] = *(const V *) (bs + nt * 16 * 8);
+                store_b(after, rw[(r + 2) % DEPTH]);
+                issue_b(rw[(r + 2) % DEPTH]);
 #pragma unroll
                 for (int q = 0; q < QB; ++q)
 #pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) acc[q][nt] = Mfma<DT>::mac(ra[r][q], rb[r][nt], acc[q][nt]);
-                issue(ra[r], rb[r]);
+                    for (int nt = 0; nt < NT; ++nt)
+                        acc[q][nt] = Mfma<DT>::mac(ra[r][q], rf[r & 1][nt], acc[q][nt]);
+                issue_a(ra[r]);
+                bslot = next;
                 // Keep each step's loads in its step: the scheduler would
                 // otherwise sink the whole ring's loads below the last MFMA.
                 __builtin_amdgcn_sched_barrier(0);
             }
             s0 += DEPTH;
         } while (s0 < KS);
+        // Flush: add the unit's products into the tile sums.  The lane's NT
+        // columns are adjacent (grouped weight packing), so each row is one
+        // vector read-modify-write; padding rows go to the spare row TM.
+        // Within a unit every valid destination occurs once, and no other
+        // wavefront touches these columns of these rows before the barrier.
+        // Rows are read in batches of eight before any is written back, so
+        // the LDS round trips overlap (the compiler cannot reorder a read
+        // past a write to a possibly equal row).
         const int slot = cu & 3;
+        using Row = float __attribute__((ext_vector_type(NT)));
 #pragma unroll
-        for (int q = 0; q < QB; ++q) {
-            const int j = rh + 2 * q;
-            if (j * 16 < c) {
+        for (int q0 = 0; q0 < QB; q0 += 2) {
+            Row * dst[2][4];
+            Row v[2][4];
+#pragma unroll
+            for (int qq = 0; qq < 2; ++qq) {
+                const ushort4 d = *(const ushort4 *) &s_rdst[slot][(rh + RG * (q0 + qq)) * 16 + lg * 4];
+                const int rows[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dst[qq][i] = (Row *) (s_acc + rows[i] * BN + ch * WN + l16 * NT);
+            }
+#pragma unroll
+            for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[qq][i] = *dst[qq][i];
+#pragma unroll
+            for (int qq = 0; qq < 2; ++qq)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int p = j * 16 + lg * 4 + i;
-                    if (p < c) {
-                        // The lane's NT columns are adjacent (grouped weight
-                        // packing): one vector read-modify-write.  No other
-                        // lane touches them before the next barrier.
-                        using Row = float __attribute__((ext_vector_type(NT)));
-                        Row * dst = (Row *) (s_acc + s_rdst[slot][p] * ACC_LD + ch * WN + l16 * NT);
-                        Row v = *dst;
 #pragma unroll
-                        for (int nt = 0; nt < NT; ++nt) v[nt] += acc[q][nt][i];
-                        *dst = v;
-                    }
+                    for (int nt = 0; nt < NT; ++nt) v[qq][i][nt] += acc[q0 + qq][nt][i];
+                    *dst[qq][i] = v[qq][i];
                 }
-            }
-            // Row blocks past the count accumulated padding: clear them too.
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[q0 + qq][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
     lds_barrier();
     // Epilogue: bias, round to the storage type, 16-byte coalesced stores.
     constexpr int CHUNKS = BN / 8;
-    for (int e = t; e < TM * CHUNKS; e += 256) {
+    for (int e = t; e < TM * CHUNKS; e += NTHR) {
         const int rr = e / CHUNKS, cc = (e % CHUNKS) * 8;
         const int64_t row = row0 + rr;
         if (row >= n) continue;
@@ -470,7 +550,7 @@ __global__ void __launch_bounds__(256) k_conv_mfma_stream(const typename Store<D
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const float bv = bias != nullptr ? bias[col0 + cc + u] : 0.0f;
-            const float v = s_acc[rr * ACC_LD + cc + u] + bv;
+            const float v = s_acc[rr * BN + cc + u] + bv;
             if constexpr (DT == kBF16) {
                 o.h[u] = f32_to_bf16(v);
             } else {
@@ -545,8 +625,12 @@ bool conv_stream_supported(int dtype, int ci, int co) {
     return conv_mfma_supported(dtype, ci, co) && ci % 64 == 0;
 }
 
+#ifndef TSH_STREAM_WAVES
+#define TSH_STREAM_WAVES 8
+#endif
+
 namespace {
-template <int DT, int BN, int DEPTH>
+template <int DT, int BN, int DEPTH, int NW>
 hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
                            const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
                            const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
@@ -557,9 +641,8 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32
     if (grid > 0x7fffffffLL) {
         return hipErrorInvalidValue;
     }
-    k_conv_mfma_stream<DT, BN, DEPTH><<<(unsigned) grid, 256, 0, s>>>((const T *) x, pair_src, pair_dst, tile_off,
-                                                                      tile_counts, (const T *) w16, bias, (T *) y,
-                                                                      n, ci, co, col_tiles);
+    k_conv_mfma_stream<DT, BN, DEPTH, NW><<<(unsigned) grid, 64 * NW, 0, s>>>(
+        (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co, col_tiles);
     return hipGetLastError();
 }
 
@@ -569,10 +652,13 @@ hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int3
                             const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
     const bool wide = co % 128 == 0;
     const bool deep = ci % 128 == 0;
-    if (wide && deep) return launch_stream_t<DT, 128, 4>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
-    if (wide) return launch_stream_t<DT, 128, 2>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
-    if (deep) return launch_stream_t<DT, 64, 4>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
-    return launch_stream_t<DT, 64, 2>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
+#define TSH_STREAM(BNV, DV) \
+    launch_stream_t<DT, BNV, DV, TSH_STREAM_WAVES>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s)
+    if (wide && deep) return TSH_STREAM(128, 4);
+    if (wide) return TSH_STREAM(128, 2);
+    if (deep) return TSH_STREAM(64, 4);
+    return TSH_STREAM(64, 2);
+#undef TSH_STREAM
 }
 }  // namespace
 
