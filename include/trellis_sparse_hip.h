@@ -172,13 +172,16 @@ typedef enum trellis_sparse_hip_dtype {
     TRELLIS_SPARSE_HIP_BF16 = 2
 } trellis_sparse_hip_dtype;
 
-/* Convolution schedule.  AUTO picks by channel counts and dtype.  The choice
- * never changes which pairs contribute, only the order of fp32 summation. */
+/* Convolution schedule.  AUTO picks by channel counts and dtype: COMPACT where
+ * it applies, else MASKED, else GENERIC; a schedule that does not apply falls
+ * back the same way.  The choice never changes which pairs contribute, only
+ * the order of fp32 summation. */
 typedef enum trellis_sparse_hip_conv_algo {
     TRELLIS_SPARSE_HIP_CONV_AUTO = 0,
-    TRELLIS_SPARSE_HIP_CONV_GENERIC = 1,   /* one lane per output element, any channels */
-    TRELLIS_SPARSE_HIP_CONV_MASKED = 2,    /* output-stationary implicit GEMM over the neighbour table */
-    TRELLIS_SPARSE_HIP_CONV_COMPACT = 3    /* output-stationary over compacted per-offset pair lists */
+    TRELLIS_SPARSE_HIP_CONV_GENERIC = 1,   /* one lane per output element, any channels and dtype */
+    TRELLIS_SPARSE_HIP_CONV_MASKED = 2,    /* MFMA over the neighbour table; F16/BF16, Ci % 32 == 0, Co % 64 == 0 */
+    TRELLIS_SPARSE_HIP_CONV_COMPACT = 3    /* MFMA over compacted per-tile pair lists; F16/BF16, Ci % 128 == 0,
+                                              Co % 64 == 0 */
 } trellis_sparse_hip_conv_algo;
 
 typedef struct trellis_sparse_hip_policy {

@@ -20,7 +20,7 @@
 //               and read pre-packed weight fragments; row groups of 16 with no
 //               valid neighbour skip the offset, others multiply zeros for
 //               their missing neighbours.
-//  * compact  - bf16/fp16 storage, Ci % 64 == 0, Co % 64 == 0.  The same MFMA
+//  * compact  - bf16/fp16 storage, Ci % 128 == 0, Co % 64 == 0.  The same MFMA
 //               tiles driven by the kernel map's compacted per-tile pair
 //               lists, so the MFMA rows are valid (src, dst) pairs only; sums
 //               of a 256-row tile stay in LDS until one final store.
@@ -278,16 +278,18 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
 // multiplies row blocks w % (NW/2) + (NW/2) q of the unit by channel half
 // w / (NW/2).
 //
-// Operands.  A (gathered feature rows) goes global -> registers through a
-// DEPTH-step ring that runs across unit boundaries (Ci/32 is a multiple of
-// DEPTH, so every unit starts at ring slot 0).  B (the unit's weight slice,
-// 32 channels x BN per step) is loaded once per block: the threads bring it
-// through a DEPTH-step register ring and store it into a 3-slot LDS ring two
-// steps ahead, and all wavefronts read their fragments from there one step
-// ahead, which halves the weight bytes through the vector memory path and
-// keeps LDS latency off the MFMA stream.  One barrier per step publishes the
-// weights; it orders LDS only, so both register rings stay in flight across
-// it.
+// Steps are processed in blocks of DEPTH (Ci/32 is a multiple of DEPTH, so a
+// block never straddles two units).  Operands are fetched one block ahead:
+//  * A (gathered feature rows) goes global -> registers; the row addresses of
+//    the target block are formed once per block from the unit's source list.
+//  * B (the unit's weight slice, 32 channels x BN per step) is fetched once
+//    per block into registers, stored into a 3-slot LDS ring two steps before
+//    use and read into fragments one step before use by every wavefront, which
+//    halves the weight bytes through the vector memory path and keeps LDS
+//    latency off the MFMA stream.
+// One barrier per step, after the step's MFMAs are issued, publishes the
+// weights stored during the step; it orders LDS only, so the register rings
+// stay in flight across it and the matrix cores run while wavefronts wait.
 //
 // Weights use the grouped packing: packed column ch*WN + nt*16 + l16 holds
 // output channel ch*WN + l16*NT + nt, so each lane's MFMA results for a row
@@ -297,16 +299,29 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
 // unit a destination occurs at most once and units are applied in order, so
 // the result is deterministic.  The tile's rows are written once at the end.
 // ---------------------------------------------------------------------------
+// Lane permute of a 16-byte fragment: lane l receives lane perm/4's value
+// (ds_bpermute per dword; the crossbar, no LDS storage).
+template <typename V> __device__ __forceinline__ V to_mfma_rows(V v, int perm) {
+    typedef int i4 __attribute__((ext_vector_type(4)));
+    const i4 u = __builtin_bit_cast(i4, v);
+    i4 r;
+    r.x = __builtin_amdgcn_ds_bpermute(perm, u.x);
+    r.y = __builtin_amdgcn_ds_bpermute(perm, u.y);
+    r.z = __builtin_amdgcn_ds_bpermute(perm, u.z);
+    r.w = __builtin_amdgcn_ds_bpermute(perm, u.w);
+    return __builtin_bit_cast(V, r);
+}
+
 template <int DT, int BN, int DEPTH, int NW>
 __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Store<DT>::T * __restrict__ x,
-                                                          const int32_t * __restrict__ pair_src,
-                                                          const int32_t * __restrict__ pair_dst,
-                                                          const int32_t * __restrict__ tile_off,
-                                                          const int32_t * __restrict__ tile_counts,
-                                                          const typename Store<DT>::T * __restrict__ w16,
-                                                          const float * __restrict__ bias,
-                                                          typename Store<DT>::T * __restrict__ y, int64_t n,
-                                                          int ci, int co, int64_t n_col_tiles) {
+                                                               const int32_t * __restrict__ pair_src,
+                                                               const int32_t * __restrict__ pair_dst,
+                                                               const int32_t * __restrict__ tile_off,
+                                                               const int32_t * __restrict__ tile_counts,
+                                                               const typename Store<DT>::T * __restrict__ w16,
+                                                               const float * __restrict__ bias,
+                                                               typename Store<DT>::T * __restrict__ y, int64_t n,
+                                                               int ci, int co, int64_t n_col_tiles) {
     using T = typename Store<DT>::T;
     using V = typename Mfma<DT>::V;
     constexpr int TM = kMapTile;     // rows per block = rows per kernel-map tile
@@ -322,6 +337,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     constexpr int BUNITS = 4 * BN;         // 16-byte pieces of a step's weights
     constexpr int BLOADS = (BUNITS + NTHR - 1) / NTHR;  // pieces per thread
     static_assert(NW == 4 || NW == 8, "4 or 8 wavefronts");
+    static_assert(DEPTH == 4 || DEPTH == 8, "block of 4 or 8 steps");
     static_assert(BUNITS % NTHR == 0 || BUNITS < NTHR, "weight pieces split evenly or fit one round");
     __shared__ float s_acc[(TM + 1) * BN];      // row TM absorbs padding rows
     __shared__ __attribute__((aligned(16))) T s_b[3][BSLOT];
@@ -367,9 +383,10 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     const int U = s_units;
     if (U == 0) return;  // unreachable for a tile with rows: the centre offset pairs every row with itself
 
-    // Unit lists: threads 0..127 carry src entries, 128..255 dst entries.
-    // Padding entries repeat the unit's last pair, so every gather stays in
-    // range; past the last unit the last unit is loaded again (never used).
+    // Unit lists, staged two units ahead: threads 0..127 carry src entries,
+    // 128..255 dst entries.  Padding entries repeat the unit's last pair, so
+    // every gather stays in range; past the last unit the last unit is loaded
+    // again (never used).
     const int le = t & (PASS - 1);
     const int32_t * list = t < PASS ? pair_src : pair_dst;
     const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
@@ -388,49 +405,47 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
         }
     };
     list_store(0, list_load(0));
-    int32_t lv = list_load(1);
+    list_store(1, list_load(1));
+    int32_t lv = list_load(2);
     lds_barrier();
 
-    V ra[DEPTH][QB];
-    V rw[DEPTH][BLOADS];
-    f32x4 acc[QB][NT];
+    // Operand addresses of one block of DEPTH steps: unit tu, first K step tps
+    // (past the last unit: the last unit again).  A row q of step tps + r is
+    // at pa[q] + r*BK; the thread's weight pieces of step tps + r at
+    // pb + r*bstep + piece offset.
+    const int64_t bstep = (int64_t) 4 * co * 8;  // elements between consecutive K steps' weights
+    int64_t boff[BLOADS];
 #pragma unroll
-    for (int q = 0; q < QB; ++q)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // A prefetch cursor (unit pu, K step ps) and weight prefetch cursor (bu, bps).
-    // Past the last unit both repeat the last unit (results never used).
-    int pu = 0, ps = 0, bu = 0, bps = 0;
-    auto issue_a = [&](V * a) {
-        const int lu = pu < U ? pu : U - 1;
-        const int slot = lu & 3;
+    for (int h = 0; h < BLOADS; ++h) {
+        const int u = t + h * NTHR;
+        boff[h] = ((int64_t) (u / BN) * co + u % BN) * 8;
+    }
+    const T * pa[QB];
+    const T * pb;
+    // A rows are fetched with the lane order of a coalesced load (lane
+    // 4*i + c reads 16 bytes c of row i of the row block: four neighbouring
+    // lanes read one 64-byte segment) and moved to the MFMA operand order
+    // (lane i + 16*c) with cross-lane permutes; an uncoalesced gather of
+    // 16-byte pieces costs the vector memory path four times as much.
+    auto target = [&](int tu, int tps) {
+        tu = tu < U ? tu : U - 1;
+        const int slot = tu & 3;
 #pragma unroll
         for (int q = 0; q < QB; ++q) {
-            const int32_t src = s_rsrc[slot][(rh + RG * q) * 16 + l16];
-            a[q] = *(const V *) (x + (int64_t) src * ci + ps * BK + lg * 8);
+            const int32_t src = s_rsrc[slot][(rh + RG * q) * 16 + (lane >> 2)];
+            pa[q] = x + (int64_t) src * ci + tps * BK + (lane & 3) * 8;
         }
-        if (++ps == KS) {
-            ps = 0;
-            ++pu;
-        }
+        pb = w16 + ((int64_t) (s_uk[tu] * ci8 + tps * 4) * co + col0) * 8;
     };
-    // A step's weights are BUNITS 16-byte pieces, piece u = (channel group
-    // u / BN, column u % BN); thread t brings pieces t, t + NTHR, ...
-    constexpr bool B_ALL = BUNITS >= NTHR;  // every thread has a piece
-    auto issue_b = [&](V * b) {
-        const int lu = bu < U ? bu : U - 1;
-        const T * src = w16 + ((int64_t) (s_uk[lu] * ci8 + bps * 4) * co + col0) * 8;
+    constexpr bool B_ALL = BUNITS >= NTHR;  // every thread has a weight piece
+    auto load_a = [&](V * a, int r) {
+#pragma unroll
+        for (int q = 0; q < QB; ++q) a[q] = *(const V *) (pa[q] + r * BK);
+    };
+    auto load_b = [&](V * b, int r) {
         if (B_ALL || t < BUNITS) {
 #pragma unroll
-            for (int h = 0; h < BLOADS; ++h) {
-                const int u = t + h * NTHR;
-                b[h] = *(const V *) (src + ((int64_t) (u / BN) * co + u % BN) * 8);
-            }
-        }
-        if (++bps == KS) {
-            bps = 0;
-            ++bu;
+            for (int h = 0; h < BLOADS; ++h) b[h] = *(const V *) (pb + r * bstep + boff[h]);
         }
     };
     auto store_b = [&](int slot, const V * b) {
@@ -439,21 +454,28 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
             for (int h = 0; h < BLOADS; ++h) *(V *) (&s_b[slot][(t + h * NTHR) * 8]) = b[h];
         }
     };
-    // Weights of steps 0 and 1 straight into LDS slots 0 and 1; then, in the
-    // order the loop issues them, weights of step r + 2 into ring slot
-    // (r + 2) % DEPTH and A of step r into ring slot r.
-    issue_b(rw[0]);
+
+    const int perm = (4 * l16 + lg) * 4;  // byte address of the source lane for to_mfma_rows
+    V ra[DEPTH][QB];  // A as loaded (coalesced lane order)
+    V rw[DEPTH][BLOADS];
+    V rf[2][NT];  // weight fragments of step g in rf[g & 1]
+    f32x4 acc[QB][NT];
+#pragma unroll
+    for (int q = 0; q < QB; ++q)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Block 0: weights of steps 0 and 1 straight into LDS slots 0 and 1,
+    // steps 2 .. DEPTH-1 into ring slots 2 .. DEPTH-1; A of steps 0 .. DEPTH-1.
+    target(0, 0);
+    load_b(rw[0], 0);
     store_b(0, rw[0]);
-    issue_b(rw[1]);
+    load_b(rw[1], 1);
     store_b(1, rw[1]);
 #pragma unroll
-    for (int r = 0; r < DEPTH; ++r) {
-        issue_b(rw[(r + 2) % DEPTH]);
-        issue_a(ra[r]);
-        __builtin_amdgcn_sched_barrier(0);  // ring slots issue in ring order
-    }
-    // Fragments of the current step's weights (rf[g & 1] at step g).
-    V rf[2][NT];
+    for (int r = 2; r < DEPTH; ++r) load_b(rw[r], r);
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) load_a(ra[r], r);
     lds_barrier();
     {
         const T * bs = &s_b[0][(lg * BN + ch * WN + l16) * 8];
@@ -463,34 +485,37 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
 
     int bslot = 0;  // LDS slot of the current step's weights (step g: g % 3)
     for (int cu = 0; cu < U; ++cu) {
-        // The list of unit cu + 1 becomes visible (at the next barrier) to the
-        // prefetches of this unit.
-        list_store(cu + 1, lv);
-        lv = list_load(cu + 2);
-        // Row blocks past the unit's count multiply padding (flushed into the
-        // spare row); keeping the MFMA stream branch-free lets every operand
-        // wait be a precise count of the loads issued after it.
+        // The lists of unit cu + 2 become visible at this step's barrier; the
+        // first reads of them are the target rows of unit cu + 1's last block.
+        list_store(cu + 2, lv);
+        lv = list_load(cu + 3);
         int s0 = 0;
         do {
+            // This block prefetches the next one: same unit unless s0 is the
+            // unit's last block.
+            const bool last = s0 + DEPTH >= KS;
+            target(last ? cu + 1 : cu, last ? 0 : s0 + DEPTH);
 #pragma unroll
             for (int r = 0; r < DEPTH; ++r) {
-                // Publishes the next step's weights (stored during the previous
-                // step) and, at a unit's first step, the list ring.
-                lds_barrier();
-                const int next = bslot == 2 ? 0 : bslot + 1;
-                const int after = next == 2 ? 0 : next + 1;  // held step g-1, read before the last barrier
-                const T * bs = &s_b[next][(lg * BN + ch * WN + l16) * 8];
+                const int s1 = bslot == 2 ? 0 : bslot + 1;  // next step's weights
+                const int s2 = s1 == 2 ? 0 : s1 + 1;        // step after: held step g-1
+                // Fragments of the next step (stored two steps ago, published
+                // by the previous step's barrier).
+                const T * bs = &s_b[s1][(lg * BN + ch * WN + l16) * 8];
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) rf[(r + 1) & 1][nt] = *(const V *) (bs + nt * 16 * 8);
-                store_b(after, rw[(r + 2) % DEPTH]);
-                issue_b(rw[(r + 2) % DEPTH]);
 #pragma unroll
                 for (int q = 0; q < QB; ++q)
 #pragma unroll
                     for (int nt = 0; nt < NT; ++nt)
-                        acc[q][nt] = Mfma<DT>::mac(ra[r][q], rf[r & 1][nt], acc[q][nt]);
-                issue_a(ra[r]);
-                bslot = next;
+                        acc[q][nt] = Mfma<DT>::mac(to_mfma_rows<V>(ra[r][q], perm), rf[r & 1][nt], acc[q][nt]);
+                // Weights of step g + 2 (fetched two steps ago) into the slot
+                // whose fragments every wavefront read before the last barrier.
+                store_b(s2, rw[(r + 2) % DEPTH]);
+                load_b(rw[r], r);
+                load_a(ra[r], r);
+                bslot = s1;
+                lds_barrier();
                 // Keep each step's loads in its step: the scheduler would
                 // otherwise sink the whole ring's loads below the last MFMA.
                 __builtin_amdgcn_sched_barrier(0);
@@ -501,10 +526,10 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
         // columns are adjacent (grouped weight packing), so each row is one
         // vector read-modify-write; padding rows go to the spare row TM.
         // Within a unit every valid destination occurs once, and no other
-        // wavefront touches these columns of these rows before the barrier.
-        // Rows are read in batches of eight before any is written back, so
-        // the LDS round trips overlap (the compiler cannot reorder a read
-        // past a write to a possibly equal row).
+        // wavefront touches these columns of these rows before the next
+        // barrier.  Rows are read in batches of eight before any is written
+        // back, so the LDS round trips overlap (the compiler cannot reorder a
+        // read past a write to a possibly equal row).
         const int slot = cu & 3;
         using Row = float __attribute__((ext_vector_type(NT)));
 #pragma unroll
@@ -620,9 +645,8 @@ hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nb
 int conv_stream_group(int co) { return co % 128 == 0 ? 4 : 2; }
 
 bool conv_stream_supported(int dtype, int ci, int co) {
-    // Units must span a whole number of prefetch rings (Ci/32 steps, ring
-    // depth 2 or 4), so the prefetch never runs more than one unit ahead.
-    return conv_mfma_supported(dtype, ci, co) && ci % 64 == 0;
+    // Units must span a whole number of 4-step blocks (Ci/32 steps).
+    return conv_mfma_supported(dtype, ci, co) && ci % 128 == 0;
 }
 
 #ifndef TSH_STREAM_WAVES
@@ -651,13 +675,10 @@ hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int3
                             const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
                             const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
     const bool wide = co % 128 == 0;
-    const bool deep = ci % 128 == 0;
 #define TSH_STREAM(BNV, DV) \
     launch_stream_t<DT, BNV, DV, TSH_STREAM_WAVES>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s)
-    if (wide && deep) return TSH_STREAM(128, 4);
-    if (wide) return TSH_STREAM(128, 2);
-    if (deep) return TSH_STREAM(64, 4);
-    return TSH_STREAM(64, 2);
+    if (wide) return TSH_STREAM(128, 4);
+    return TSH_STREAM(64, 4);
 #undef TSH_STREAM
 }
 }  // namespace
