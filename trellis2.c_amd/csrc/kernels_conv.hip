@@ -299,6 +299,15 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
 // unit a destination occurs at most once and units are applied in order, so
 // the result is deterministic.  The tile's rows are written once at the end.
 // ---------------------------------------------------------------------------
+// Shape of the streamed schedule: wavefronts per block, and row groups among
+// them (the rest split the block's channels).
+#ifndef TSH_STREAM_WAVES
+#define TSH_STREAM_WAVES 8
+#endif
+#ifndef TSH_STREAM_ROW_GROUPS
+#define TSH_STREAM_ROW_GROUPS 4
+#endif
+
 // Lane permute of a 16-byte fragment: lane l receives lane perm/4's value
 // (ds_bpermute per dword; the crossbar, no LDS storage).
 template <typename V> __device__ __forceinline__ V to_mfma_rows(V v, int perm) {
@@ -312,7 +321,7 @@ template <typename V> __device__ __forceinline__ V to_mfma_rows(V v, int perm) {
     return __builtin_bit_cast(V, r);
 }
 
-template <int DT, int BN, int DEPTH, int NW>
+template <int DT, int BN, int DEPTH, int NW, int RG>
 __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Store<DT>::T * __restrict__ x,
                                                                const int32_t * __restrict__ pair_src,
                                                                const int32_t * __restrict__ pair_dst,
@@ -327,9 +336,11 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     constexpr int TM = kMapTile;     // rows per block = rows per kernel-map tile
     constexpr int BK = 32;           // input channels per K step
     constexpr int NTHR = 64 * NW;
-    constexpr int WN = BN / 2;       // channels per wavefront
+    // Row groups RG: wavefront w takes row blocks w % RG + RG * q of a unit
+    // and channel group w / RG.
+    constexpr int CG = NW / RG;      // channel groups
+    constexpr int WN = BN / CG;      // channels per wavefront
     constexpr int NT = WN / 16;      // MFMA column tiles per wavefront
-    constexpr int RG = NW / 2;       // row groups: wavefront w takes row blocks w % RG + RG * q
     constexpr int QB = 8 / RG;       // row blocks per wavefront per unit
     constexpr int PASS = 128;        // pairs per unit
     constexpr int MAX_UNITS = 27 * (TM / PASS);
@@ -337,6 +348,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     constexpr int BUNITS = 4 * BN;         // 16-byte pieces of a step's weights
     constexpr int BLOADS = (BUNITS + NTHR - 1) / NTHR;  // pieces per thread
     static_assert(NW == 4 || NW == 8, "4 or 8 wavefronts");
+    static_assert((RG == 2 || RG == 4) && NW % RG == 0 && NT >= 1, "row groups");
     static_assert(DEPTH == 4 || DEPTH == 8, "block of 4 or 8 steps");
     static_assert(BUNITS % NTHR == 0 || BUNITS < NTHR, "weight pieces split evenly or fit one round");
     __shared__ float s_acc[(TM + 1) * BN];      // row TM absorbs padding rows
@@ -642,19 +654,18 @@ hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nb
 }
 
 
-int conv_stream_group(int co) { return co % 128 == 0 ? 4 : 2; }
+int conv_stream_group(int co) {
+    const int bn = co % 128 == 0 ? 128 : 64;
+    return bn / (TSH_STREAM_WAVES / TSH_STREAM_ROW_GROUPS) / 16;
+}
 
 bool conv_stream_supported(int dtype, int ci, int co) {
     // Units must span a whole number of 4-step blocks (Ci/32 steps).
     return conv_mfma_supported(dtype, ci, co) && ci % 128 == 0;
 }
 
-#ifndef TSH_STREAM_WAVES
-#define TSH_STREAM_WAVES 8
-#endif
-
 namespace {
-template <int DT, int BN, int DEPTH, int NW>
+template <int DT, int BN, int DEPTH, int NW, int RG>
 hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
                            const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
                            const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
@@ -665,7 +676,7 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32
     if (grid > 0x7fffffffLL) {
         return hipErrorInvalidValue;
     }
-    k_conv_mfma_stream<DT, BN, DEPTH, NW><<<(unsigned) grid, 64 * NW, 0, s>>>(
+    k_conv_mfma_stream<DT, BN, DEPTH, NW, RG><<<(unsigned) grid, 64 * NW, 0, s>>>(
         (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co, col_tiles);
     return hipGetLastError();
 }
@@ -676,7 +687,8 @@ hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int3
                             const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
     const bool wide = co % 128 == 0;
 #define TSH_STREAM(BNV, DV) \
-    launch_stream_t<DT, BNV, DV, TSH_STREAM_WAVES>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s)
+    launch_stream_t<DT, BNV, DV, TSH_STREAM_WAVES, TSH_STREAM_ROW_GROUPS>(x, pair_src, pair_dst, tile_off, tile_counts, \
+                                                                       w16, bias, y, n, ci, co, s)
     if (wide) return TSH_STREAM(128, 4);
     return TSH_STREAM(64, 4);
 #undef TSH_STREAM

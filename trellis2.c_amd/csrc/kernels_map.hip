@@ -307,12 +307,25 @@ __global__ void __launch_bounds__(kBlock) k_fill_pairs(const int32_t * __restric
                                                        int32_t * __restrict__ pair_src,
                                                        int32_t * __restrict__ pair_dst) {
     __shared__ int32_t s_wave_cnt[27][kBlock / 64];
+    __shared__ __attribute__((aligned(16))) int32_t s_nbr[kBlock * 27];
     const int t = threadIdx.x;
     const int lane = lane_id();
     const int wave = t >> 6;
     const int64_t tile = blockIdx.x;
     const int64_t i = tile * kBlock + t;
     const uint32_t m = i < n ? mask[i] : 0u;
+    // The tile's neighbour rows are contiguous: stage them with coalesced
+    // 16-byte loads (a thread's own row is 108 bytes, so direct per-offset
+    // reads would stride across the wavefront).
+    {
+        const int64_t first = tile * kBlock * 27;
+        const int64_t end = n * 27;
+        const int count = (int) ((end - first) < kBlock * 27 ? (end - first) : kBlock * 27);
+        const int32_t * src = nbr + first;
+        const int vec = count / 4;  // first is a multiple of 4 (kBlock * 27 is)
+        for (int v = t; v < vec; v += kBlock) *(int4 *) &s_nbr[v * 4] = *(const int4 *) (src + v * 4);
+        for (int e = vec * 4 + t; e < count; e += kBlock) s_nbr[e] = src[e];
+    }
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     int32_t rank[27];
 #pragma unroll
@@ -335,7 +348,7 @@ __global__ void __launch_bounds__(kBlock) k_fill_pairs(const int32_t * __restric
                 base += s_wave_cnt[k][w];
             }
             const int64_t pos = (int64_t) base + rank[k];
-            pair_src[pos] = nbr[i * 27 + k];
+            pair_src[pos] = s_nbr[t * 27 + k];
             pair_dst[pos] = (int32_t) i;
         }
     }

@@ -277,25 +277,67 @@ __global__ void k_c2s_gather(const typename Store<DT>::T * __restrict__ x, const
     }
 }
 
+// 16-byte chunks with 32-bit indexing, as k_skip_repeat_vec.
+template <int DT>
+__global__ void __launch_bounds__(256) k_c2s_gather_vec(const typename Store<DT>::T * __restrict__ x,
+                                                        const int32_t * __restrict__ parent,
+                                                        const int32_t * __restrict__ subidx,
+                                                        typename Store<DT>::T * __restrict__ y, int n_out, int co,
+                                                        int vpr, int vshift) {
+    constexpr int kVec = 16 / (int) sizeof(typename Store<DT>::T);
+    const int total = n_out * vpr;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        const int r = vshift >= 0 ? e >> vshift : e / vpr;
+        const int c0 = (e - r * vpr) * kVec;
+        const int64_t from = ((int64_t) parent[r] * 8 + subidx[r]) * co + c0;
+        *(int4 *) (y + (int64_t) r * co + c0) = *(const int4 *) (x + from);
+    }
+}
+
 template <int DT>
 __global__ void k_skip_repeat(const typename Store<DT>::T * __restrict__ x, const int32_t * __restrict__ parent,
                               const int32_t * __restrict__ subidx, typename Store<DT>::T * __restrict__ y,
                               int64_t n_out, int ci, int co, int repeat) {
+    TSH_GRID_STRIDE(e, n_out * co) {
+        const int64_t r = e / co;
+        const int c = (int) (e % co);
+        int from = (subidx[r] * co + c) / repeat;
+        from = from < ci - 1 ? from : ci - 1;
+        y[e] = x[(int64_t) parent[r] * ci + from];
+    }
+}
+
+// 16-byte output chunks, 32-bit indexing (n_out * co / kVec < 2^31).  The
+// chunks of a row are consecutive threads: row = e >> vshift when the chunk
+// count per row is a power of two (vshift >= 0), else e / vpr.  kSingle: the
+// repeat count is a multiple of the chunk width, so one source element fills
+// the whole chunk (repeat-interleave of 8 or more).
+template <int DT, bool kSingle>
+__global__ void __launch_bounds__(256) k_skip_repeat_vec(const typename Store<DT>::T * __restrict__ x,
+                                                         const int32_t * __restrict__ parent,
+                                                         const int32_t * __restrict__ subidx,
+                                                         typename Store<DT>::T * __restrict__ y, int n_out, int ci,
+                                                         int co, int repeat, int vpr, int vshift) {
     using T = typename Store<DT>::T;
     constexpr int kVec = 16 / (int) sizeof(T);
-    if (co % kVec == 0) {
-        const int vpr = co / kVec;
-        TSH_GRID_STRIDE(e, n_out * vpr) {
-            const int64_t r = e / vpr;
-            const int c0 = (int) (e % vpr) * kVec;
-            const T * xr = x + (int64_t) parent[r] * ci;
-            const int s = subidx[r];
-            union {
-                int4 v;
-                T e[kVec];
-            } out;
+    const int total = n_out * vpr;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        const int r = vshift >= 0 ? e >> vshift : e / vpr;
+        const int c0 = (e - r * vpr) * kVec;
+        const T * xr = x + (int64_t) parent[r] * ci;
+        const int first = subidx[r] * co + c0;
+        union {
+            int4 v;
+            T e[kVec];
+        } out;
+        if constexpr (kSingle) {
+            int from = first / repeat;
+            from = from < ci - 1 ? from : ci - 1;
+            const T v = xr[from];
+#pragma unroll
+            for (int q = 0; q < kVec; ++q) out.e[q] = v;
+        } else {
             // One division per chunk; step the quotient/remainder across it.
-            const int first = s * co + c0;
             int from = first / repeat;
             int rem = first - from * repeat;
 #pragma unroll
@@ -306,16 +348,8 @@ __global__ void k_skip_repeat(const typename Store<DT>::T * __restrict__ x, cons
                     ++from;
                 }
             }
-            *(int4 *) (y + r * co + c0) = out.v;
         }
-    } else {
-        TSH_GRID_STRIDE(e, n_out * co) {
-            const int64_t r = e / co;
-            const int c = (int) (e % co);
-            int from = (subidx[r] * co + c) / repeat;
-            from = from < ci - 1 ? from : ci - 1;
-            y[e] = x[(int64_t) parent[r] * ci + from];
-        }
+        *(int4 *) (y + (int64_t) r * co + c0) = out.v;
     }
 }
 
@@ -456,6 +490,31 @@ hipError_t launch_c2s_fill(int dtype, const int32_t * coords, const void * logit
 
 hipError_t launch_c2s_gather(int dtype, const void * x, const int32_t * parent, const int32_t * subidx, void * y,
                              int64_t n_out, int co, hipStream_t s) {
+    const int kvec = 16 / (int) dtype_bytes(dtype);
+    if (co % kvec == 0 && n_out * (co / kvec) < (int64_t) INT32_MAX - 65536 * 256) {
+        const int vpr = co / kvec;
+        int vshift = -1;
+        for (int b = 0; b < 30; ++b) {
+            if ((1 << b) == vpr) vshift = b;
+        }
+        const int gv = blocks_for(n_out * vpr, 256, 65536);
+        switch (dtype) {
+            case kF32:
+                k_c2s_gather_vec<kF32><<<gv, 256, 0, s>>>((const float *) x, parent, subidx, (float *) y, (int) n_out,
+                                                          co, vpr, vshift);
+                break;
+            case kF16:
+                k_c2s_gather_vec<kF16><<<gv, 256, 0, s>>>((const _Float16 *) x, parent, subidx, (_Float16 *) y,
+                                                          (int) n_out, co, vpr, vshift);
+                break;
+            case kBF16:
+                k_c2s_gather_vec<kBF16><<<gv, 256, 0, s>>>((const uint16_t *) x, parent, subidx, (uint16_t *) y,
+                                                           (int) n_out, co, vpr, vshift);
+                break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     const int g = blocks_for(n_out * co / 4 + 1, 256, 32768);
     switch (dtype) {
         case kF32: k_c2s_gather<kF32><<<g, 256, 0, s>>>((const float *) x, parent, subidx, (float *) y, n_out, co); break;
@@ -473,7 +532,35 @@ hipError_t launch_c2s_gather(int dtype, const void * x, const int32_t * parent, 
 hipError_t launch_skip_repeat(int dtype, const void * x, const int32_t * parent, const int32_t * subidx, void * y,
                               int64_t n_out, int ci, int co, hipStream_t s) {
     const int repeat = (8 * co + ci - 1) / ci;
-    const int g = blocks_for(n_out * co / 4 + 1, 256, 32768);
+    const int kvec = 16 / (int) dtype_bytes(dtype);
+    if (co % kvec == 0 && n_out * (co / kvec) < (int64_t) INT32_MAX - 65536 * 256) {
+        const int vpr = co / kvec;
+        int vshift = -1;
+        for (int b = 0; b < 30; ++b) {
+            if ((1 << b) == vpr) vshift = b;
+        }
+        const int g = blocks_for(n_out * vpr, 256, 65536);
+        const bool single = repeat % kvec == 0;
+#define TSH_SR(DTV, TYPE)                                                                                       \
+    do {                                                                                                        \
+        if (single) {                                                                                           \
+            k_skip_repeat_vec<DTV, true><<<g, 256, 0, s>>>((const TYPE *) x, parent, subidx, (TYPE *) y,         \
+                                                           (int) n_out, ci, co, repeat, vpr, vshift);            \
+        } else {                                                                                                \
+            k_skip_repeat_vec<DTV, false><<<g, 256, 0, s>>>((const TYPE *) x, parent, subidx, (TYPE *) y,        \
+                                                            (int) n_out, ci, co, repeat, vpr, vshift);           \
+        }                                                                                                       \
+    } while (0)
+        switch (dtype) {
+            case kF32: TSH_SR(kF32, float); break;
+            case kF16: TSH_SR(kF16, _Float16); break;
+            case kBF16: TSH_SR(kBF16, uint16_t); break;
+            default: return hipErrorInvalidValue;
+        }
+#undef TSH_SR
+        return hipGetLastError();
+    }
+    const int g = blocks_for(n_out * co, 256, 32768);
     switch (dtype) {
         case kF32:
             k_skip_repeat<kF32><<<g, 256, 0, s>>>((const float *) x, parent, subidx, (float *) y, n_out, ci, co, repeat);
