@@ -273,10 +273,12 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
 // each offset k, the tile's valid (src, dst) pairs in destination order.  The
 // block walks "units" (offset k, up to 128 of its pairs) in k order; each unit
 // is Ci/32 K steps of MFMA work over 16-pair row blocks, so the MFMA row
-// dimension runs over valid pairs only.  With NW wavefronts (8: two per SIMD,
-// so one's VALU and LDS work overlaps the other's MFMAs) wavefront w
-// multiplies row blocks w % (NW/2) + (NW/2) q of the unit by channel half
-// w / (NW/2).
+// dimension runs over valid pairs only.  NW wavefronts (8: two per SIMD, so
+// one's VALU and LDS work overlaps the other's MFMAs) are split into RG row
+// groups and NW/RG channel groups; wavefront w multiplies row blocks
+// w % RG + RG q of the unit by channel group w / RG.  The default, RG = 8,
+// gives each wavefront one row block and all BN channels, so no feature row
+// is fetched twice.
 //
 // Steps are processed in blocks of DEPTH (Ci/32 is a multiple of DEPTH, so a
 // block never straddles two units).  Operands are fetched one block ahead:
@@ -305,7 +307,7 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
 #define TSH_STREAM_WAVES 8
 #endif
 #ifndef TSH_STREAM_ROW_GROUPS
-#define TSH_STREAM_ROW_GROUPS 4
+#define TSH_STREAM_ROW_GROUPS 8
 #endif
 
 // Lane permute of a 16-byte fragment: lane l receives lane perm/4's value
@@ -348,7 +350,8 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     constexpr int BUNITS = 4 * BN;         // 16-byte pieces of a step's weights
     constexpr int BLOADS = (BUNITS + NTHR - 1) / NTHR;  // pieces per thread
     static_assert(NW == 4 || NW == 8, "4 or 8 wavefronts");
-    static_assert((RG == 2 || RG == 4) && NW % RG == 0 && NT >= 1, "row groups");
+    static_assert((RG == 2 || RG == 4 || RG == 8) && NW % RG == 0 && NT >= 1, "row groups");
+    constexpr int QF = QB < 2 ? QB : 2;  // row blocks per flush batch
     static_assert(DEPTH == 4 || DEPTH == 8, "block of 4 or 8 steps");
     static_assert(BUNITS % NTHR == 0 || BUNITS < NTHR, "weight pieces split evenly or fit one round");
     __shared__ float s_acc[(TM + 1) * BN];      // row TM absorbs padding rows
@@ -545,22 +548,22 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
         const int slot = cu & 3;
         using Row = float __attribute__((ext_vector_type(NT)));
 #pragma unroll
-        for (int q0 = 0; q0 < QB; q0 += 2) {
-            Row * dst[2][4];
-            Row v[2][4];
+        for (int q0 = 0; q0 < QB; q0 += QF) {
+            Row * dst[QF][4];
+            Row v[QF][4];
 #pragma unroll
-            for (int qq = 0; qq < 2; ++qq) {
+            for (int qq = 0; qq < QF; ++qq) {
                 const ushort4 d = *(const ushort4 *) &s_rdst[slot][(rh + RG * (q0 + qq)) * 16 + lg * 4];
                 const int rows[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) dst[qq][i] = (Row *) (s_acc + rows[i] * BN + ch * WN + l16 * NT);
             }
 #pragma unroll
-            for (int qq = 0; qq < 2; ++qq)
+            for (int qq = 0; qq < QF; ++qq)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[qq][i] = *dst[qq][i];
 #pragma unroll
-            for (int qq = 0; qq < 2; ++qq)
+            for (int qq = 0; qq < QF; ++qq)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -568,7 +571,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
                     *dst[qq][i] = v[qq][i];
                 }
 #pragma unroll
-            for (int qq = 0; qq < 2; ++qq)
+            for (int qq = 0; qq < QF; ++qq)
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) acc[q0 + qq][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
