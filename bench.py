@@ -251,6 +251,16 @@ def main():
     achieved = per_launch_flops / (conv_avg * 1e-3) / 1e12 if conv_avg > 0 else 0.0
     hm_ms = (stages["hash"][0] + stages["map"][0]) / args.steps
     elem = 4 if spec["dtype"] == sh.F32 else 2
+    # The conv's binding roofline: compute (2 P Ci Co at the dtype's MFMA or
+    # fp32 peak) or HBM (compulsory bytes at 8 TB/s), whichever takes longer.
+    conv_bytes = wl.conv_bytes(job.m, job.ci, job.co, elem)
+    peak_flops = PEAK_TFLOPS[spec["dtype"]]
+    hbm_bound = conv_bytes / (PEAK_HBM_GBS * 1e9) > per_launch_flops / (peak_flops * 1e12)
+    if hbm_bound:
+        roof_achieved = conv_bytes / (conv_avg * 1e-3) / 1e9 if conv_avg > 0 else 0.0
+        roof_peak, roof_unit, roof_bound = PEAK_HBM_GBS, "GB/s", "hbm"
+    else:
+        roof_achieved, roof_peak, roof_unit, roof_bound = achieved, peak_flops, "TFLOP/s", "mfma"
     # HBM bytes per conv launch come from the committed, copy-calibrated
     # rocprofv3 FETCH_SIZE / WRITE_SIZE summary for this workload and schedule.
     algo_name = conv_schedule(spec["dtype"], job.ci, job.co, args.conv_algo)
@@ -280,14 +290,15 @@ def main():
         "conv_kernel_tflops": round(achieved, 2),
         "stage_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in stages.items()},
         "roofline": {
-            "bound": "mfma",
+            "bound": roof_bound,
             "kernel": "sparse_conv3d",
-            "achieved": round(achieved, 2),
-            "peak": PEAK_TFLOPS[spec["dtype"]],
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_TFLOPS[spec["dtype"]], 4),
+            "achieved": round(roof_achieved, 2),
+            "peak": roof_peak,
+            "unit": roof_unit,
+            "frac": round(roof_achieved / roof_peak, 4),
             "traffic": traffic,
-            "algorithmic_bytes": wl.conv_bytes(job.m, job.ci, job.co, elem),
+            "algorithmic_bytes": conv_bytes,
+            "algorithmic_flops": per_launch_flops,
             "schedule": algo_name,
             "avg_launch_ms": round(conv_avg, 4),
         },
