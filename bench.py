@@ -137,7 +137,7 @@ class Cfg2(ConvOnly):
 def conv_schedule(dtype, ci, co, algo):
     """Name of the conv kernel the backend runs (its fallback rules)."""
     mfma = dtype != sh.F32 and ci % 32 == 0 and co % 64 == 0
-    if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and ci % 128 == 0:
+    if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and (ci % 128 == 0 or ci == 64):
         return "compact"
     if algo in (sh.CONV_AUTO, sh.CONV_COMPACT, sh.CONV_MASKED) and mfma:
         return "masked"

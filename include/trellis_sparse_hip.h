@@ -180,8 +180,8 @@ typedef enum trellis_sparse_hip_conv_algo {
     TRELLIS_SPARSE_HIP_CONV_AUTO = 0,
     TRELLIS_SPARSE_HIP_CONV_GENERIC = 1,   /* one lane per output element, any channels and dtype */
     TRELLIS_SPARSE_HIP_CONV_MASKED = 2,    /* MFMA over the neighbour table; F16/BF16, Ci % 32 == 0, Co % 64 == 0 */
-    TRELLIS_SPARSE_HIP_CONV_COMPACT = 3    /* MFMA over compacted per-tile pair lists; F16/BF16, Ci % 128 == 0,
-                                              Co % 64 == 0 */
+    TRELLIS_SPARSE_HIP_CONV_COMPACT = 3    /* MFMA over compacted per-tile pair lists; F16/BF16, Ci == 64 or
+                                              Ci % 128 == 0, Co % 64 == 0 */
 } trellis_sparse_hip_conv_algo;
 
 typedef struct trellis_sparse_hip_policy {

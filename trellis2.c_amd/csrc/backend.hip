@@ -614,7 +614,7 @@ trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_
     int algo = be->policy.conv_algo;
     if (algo == TRELLIS_SPARSE_HIP_CONV_AUTO) {
         // The streamed compacted schedule multiplies valid pairs only; where it
-        // does not apply (Ci % 128 != 0) the masked one, then the VALU one.
+        // does not apply (Ci not 64 or a multiple of 128) the masked one, then the VALU one.
         algo = TRELLIS_SPARSE_HIP_CONV_COMPACT;
     }
     if (algo == TRELLIS_SPARSE_HIP_CONV_COMPACT && !conv_stream_supported(dt, ci, co)) {

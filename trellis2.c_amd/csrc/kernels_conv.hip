@@ -20,7 +20,7 @@
 //               and read pre-packed weight fragments; row groups of 16 with no
 //               valid neighbour skip the offset, others multiply zeros for
 //               their missing neighbours.
-//  * compact  - bf16/fp16 storage, Ci % 128 == 0, Co % 64 == 0.  The same MFMA
+//  * compact  - bf16/fp16 storage, Ci = 64 or Ci % 128 == 0, Co % 64 == 0.  The same MFMA
 //               tiles driven by the kernel map's compacted per-tile pair
 //               lists, so the MFMA rows are valid (src, dst) pairs only; sums
 //               of a 256-row tile stay in LDS until one final store.
@@ -323,7 +323,7 @@ template <typename V> __device__ __forceinline__ V to_mfma_rows(V v, int perm) {
     return __builtin_bit_cast(V, r);
 }
 
-template <int DT, int BN, int DEPTH, int NW, int RG>
+template <int DT, int BN, int DEPTH, int NW, int RG, int UPB>
 __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Store<DT>::T * __restrict__ x,
                                                                const int32_t * __restrict__ pair_src,
                                                                const int32_t * __restrict__ pair_dst,
@@ -353,11 +353,13 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     static_assert((RG == 2 || RG == 4 || RG == 8) && NW % RG == 0 && NT >= 1, "row groups");
     constexpr int QF = QB < 2 ? QB : 2;  // row blocks per flush batch
     static_assert(DEPTH == 4 || DEPTH == 8, "block of 4 or 8 steps");
+    static_assert(UPB == 1 || UPB == 2, "units per block");
+    constexpr int RING = UPB == 1 ? 4 : 8;  // unit-list slots: the current block's units and two blocks ahead
     static_assert(BUNITS % NTHR == 0 || BUNITS < NTHR, "weight pieces split evenly or fit one round");
     __shared__ float s_acc[(TM + 1) * BN];      // row TM absorbs padding rows
     __shared__ __attribute__((aligned(16))) T s_b[3][BSLOT];
-    __shared__ int32_t s_rsrc[4][PASS];
-    __shared__ uint16_t s_rdst[4][PASS];        // tile-local dst row, TM for padding
+    __shared__ int32_t s_rsrc[RING][PASS];
+    __shared__ uint16_t s_rdst[RING][PASS];     // tile-local dst row, TM for padding
     __shared__ int32_t s_uk[MAX_UNITS], s_ustart[MAX_UNITS], s_ucnt[MAX_UNITS];
     __shared__ int32_t s_cnt[27], s_start[27];
     __shared__ int32_t s_units;
@@ -398,10 +400,10 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     const int U = s_units;
     if (U == 0) return;  // unreachable for a tile with rows: the centre offset pairs every row with itself
 
-    // Unit lists, staged two units ahead: threads 0..127 carry src entries,
-    // 128..255 dst entries.  Padding entries repeat the unit's last pair, so
-    // every gather stays in range; past the last unit the last unit is loaded
-    // again (never used).
+    // Unit lists, staged two blocks ahead in a ring of RING slots: threads
+    // 0..127 carry src entries, 128..255 dst entries.  Padding entries
+    // repeat the unit's last pair, so every gather stays in range; past the
+    // last unit the last unit is loaded again (never used).
     const int le = t & (PASS - 1);
     const int32_t * list = t < PASS ? pair_src : pair_dst;
     const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
@@ -413,21 +415,26 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     };
     auto list_store = [&](int u, int32_t v) {
         if (t < PASS) {
-            s_rsrc[u & 3][le] = v;
+            s_rsrc[u & (RING - 1)][le] = v;
         } else if (t < 2 * PASS) {
             const int c = s_ucnt[u < U ? u : U - 1];
-            s_rdst[u & 3][le] = (uint16_t) (le < c ? v - list_bias : TM);
+            s_rdst[u & (RING - 1)][le] = (uint16_t) (le < c ? v - list_bias : TM);
         }
     };
-    list_store(0, list_load(0));
-    list_store(1, list_load(1));
-    int32_t lv = list_load(2);
+#pragma unroll
+    for (int j = 0; j < 2 * UPB; ++j) list_store(j, list_load(j));
+    int32_t lv[UPB];
+#pragma unroll
+    for (int j = 0; j < UPB; ++j) lv[j] = list_load(2 * UPB + j);
     lds_barrier();
 
-    // Operand addresses of one block of DEPTH steps: unit tu, first K step tps
-    // (past the last unit: the last unit again).  A row q of step tps + r is
-    // at pa[q] + r*BK; the thread's weight pieces of step tps + r at
-    // pb + r*bstep + piece offset.
+    // Operand addresses of one block of DEPTH steps, which covers UPB units
+    // of SPU steps each (UPB > 1 only when a unit is shorter than a block):
+    // unit tu + r / SPU, K step tps + r % SPU for step r (past the last unit:
+    // the last unit again).  A row q of step r is at pa[r/SPU][q] +
+    // (r%SPU)*BK; the thread's weight pieces at pb[r/SPU] + (r%SPU)*bstep +
+    // piece offset.
+    constexpr int SPU = DEPTH / UPB;
     const int64_t bstep = (int64_t) 4 * co * 8;  // elements between consecutive K steps' weights
     int64_t boff[BLOADS];
 #pragma unroll
@@ -435,32 +442,35 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
         const int u = t + h * NTHR;
         boff[h] = ((int64_t) (u / BN) * co + u % BN) * 8;
     }
-    const T * pa[QB];
-    const T * pb;
+    const T * pa[UPB][QB];
+    const T * pb[UPB];
     // A rows are fetched with the lane order of a coalesced load (lane
     // 4*i + c reads 16 bytes c of row i of the row block: four neighbouring
     // lanes read one 64-byte segment) and moved to the MFMA operand order
     // (lane i + 16*c) with cross-lane permutes; an uncoalesced gather of
     // 16-byte pieces costs the vector memory path four times as much.
-    auto target = [&](int tu, int tps) {
-        tu = tu < U ? tu : U - 1;
-        const int slot = tu & 3;
+    auto target = [&](int tu0, int tps) {
 #pragma unroll
-        for (int q = 0; q < QB; ++q) {
-            const int32_t src = s_rsrc[slot][(rh + RG * q) * 16 + (lane >> 2)];
-            pa[q] = x + (int64_t) src * ci + tps * BK + (lane & 3) * 8;
+        for (int uo = 0; uo < UPB; ++uo) {
+            const int tu = tu0 + uo < U ? tu0 + uo : U - 1;
+            const int slot = tu & (RING - 1);
+#pragma unroll
+            for (int q = 0; q < QB; ++q) {
+                const int32_t src = s_rsrc[slot][(rh + RG * q) * 16 + (lane >> 2)];
+                pa[uo][q] = x + (int64_t) src * ci + tps * BK + (lane & 3) * 8;
+            }
+            pb[uo] = w16 + ((int64_t) (s_uk[tu] * ci8 + tps * 4) * co + col0) * 8;
         }
-        pb = w16 + ((int64_t) (s_uk[tu] * ci8 + tps * 4) * co + col0) * 8;
     };
     constexpr bool B_ALL = BUNITS >= NTHR;  // every thread has a weight piece
     auto load_a = [&](V * a, int r) {
 #pragma unroll
-        for (int q = 0; q < QB; ++q) a[q] = *(const V *) (pa[q] + r * BK);
+        for (int q = 0; q < QB; ++q) a[q] = *(const V *) (pa[r / SPU][q] + (r % SPU) * BK);
     };
     auto load_b = [&](V * b, int r) {
         if (B_ALL || t < BUNITS) {
 #pragma unroll
-            for (int h = 0; h < BLOADS; ++h) b[h] = *(const V *) (pb + r * bstep + boff[h]);
+            for (int h = 0; h < BLOADS; ++h) b[h] = *(const V *) (pb[r / SPU] + (r % SPU) * bstep + boff[h]);
         }
     };
     auto store_b = [&](int slot, const V * b) {
@@ -480,72 +490,16 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Block 0: weights of steps 0 and 1 straight into LDS slots 0 and 1,
-    // steps 2 .. DEPTH-1 into ring slots 2 .. DEPTH-1; A of steps 0 .. DEPTH-1.
-    target(0, 0);
-    load_b(rw[0], 0);
-    store_b(0, rw[0]);
-    load_b(rw[1], 1);
-    store_b(1, rw[1]);
-#pragma unroll
-    for (int r = 2; r < DEPTH; ++r) load_b(rw[r], r);
-#pragma unroll
-    for (int r = 0; r < DEPTH; ++r) load_a(ra[r], r);
-    lds_barrier();
-    {
-        const T * bs = &s_b[0][(lg * BN + ch * WN + l16) * 8];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) rf[0][nt] = *(const V *) (bs + nt * 16 * 8);
-    }
-
-    int bslot = 0;  // LDS slot of the current step's weights (step g: g % 3)
-    for (int cu = 0; cu < U; ++cu) {
-        // The lists of unit cu + 2 become visible at this step's barrier; the
-        // first reads of them are the target rows of unit cu + 1's last block.
-        list_store(cu + 2, lv);
-        lv = list_load(cu + 3);
-        int s0 = 0;
-        do {
-            // This block prefetches the next one: same unit unless s0 is the
-            // unit's last block.
-            const bool last = s0 + DEPTH >= KS;
-            target(last ? cu + 1 : cu, last ? 0 : s0 + DEPTH);
-#pragma unroll
-            for (int r = 0; r < DEPTH; ++r) {
-                const int s1 = bslot == 2 ? 0 : bslot + 1;  // next step's weights
-                const int s2 = s1 == 2 ? 0 : s1 + 1;        // step after: held step g-1
-                // Fragments of the next step (stored two steps ago, published
-                // by the previous step's barrier).
-                const T * bs = &s_b[s1][(lg * BN + ch * WN + l16) * 8];
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) rf[(r + 1) & 1][nt] = *(const V *) (bs + nt * 16 * 8);
-#pragma unroll
-                for (int q = 0; q < QB; ++q)
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt)
-                        acc[q][nt] = Mfma<DT>::mac(to_mfma_rows<V>(ra[r][q], perm), rf[r & 1][nt], acc[q][nt]);
-                // Weights of step g + 2 (fetched two steps ago) into the slot
-                // whose fragments every wavefront read before the last barrier.
-                store_b(s2, rw[(r + 2) % DEPTH]);
-                load_b(rw[r], r);
-                load_a(ra[r], r);
-                bslot = s1;
-                lds_barrier();
-                // Keep each step's loads in its step: the scheduler would
-                // otherwise sink the whole ring's loads below the last MFMA.
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            s0 += DEPTH;
-        } while (s0 < KS);
-        // Flush: add the unit's products into the tile sums.  The lane's NT
-        // columns are adjacent (grouped weight packing), so each row is one
-        // vector read-modify-write; padding rows go to the spare row TM.
-        // Within a unit every valid destination occurs once, and no other
-        // wavefront touches these columns of these rows before the next
-        // barrier.  Rows are read in batches of eight before any is written
-        // back, so the LDS round trips overlap (the compiler cannot reorder a
-        // read past a write to a possibly equal row).
-        const int slot = cu & 3;
+    // Flush: add a unit's products into the tile sums.  The lane's NT
+    // columns are adjacent (grouped weight packing), so each row is one
+    // vector read-modify-write; padding rows go to the spare row TM.  Within
+    // a unit every valid destination occurs once, and no other wavefront
+    // touches these columns of these rows before the next barrier.  Rows are
+    // read in batches before any is written back, so the LDS round trips
+    // overlap (the compiler cannot reorder a read past a write to a possibly
+    // equal row).
+    auto flush = [&](int unit) {
+        const int slot = unit & (RING - 1);
         using Row = float __attribute__((ext_vector_type(NT)));
 #pragma unroll
         for (int q0 = 0; q0 < QB; q0 += QF) {
@@ -575,6 +529,85 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) acc[q0 + qq][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
+    };
+
+    // Block 0: weights of steps 0 and 1 straight into LDS slots 0 and 1,
+    // steps 2 .. DEPTH-1 into ring slots 2 .. DEPTH-1; A of steps 0 .. DEPTH-1.
+    target(0, 0);
+    load_b(rw[0], 0);
+    store_b(0, rw[0]);
+    load_b(rw[1], 1);
+    store_b(1, rw[1]);
+#pragma unroll
+    for (int r = 2; r < DEPTH; ++r) load_b(rw[r], r);
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) load_a(ra[r], r);
+    lds_barrier();
+    {
+        const T * bs = &s_b[0][(lg * BN + ch * WN + l16) * 8];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) rf[0][nt] = *(const V *) (bs + nt * 16 * 8);
+    }
+
+    int bslot = 0;  // LDS slot of the current step's weights (step g: g % 3)
+    for (int cb = 0; cb < U; cb += UPB) {
+        // The lists of the units two blocks ahead become visible at this
+        // block's first barrier; their first readers are the next block's
+        // target computation.
+#pragma unroll
+        for (int j = 0; j < UPB; ++j) {
+            list_store(cb + 2 * UPB + j, lv[j]);
+            lv[j] = list_load(cb + 3 * UPB + j);
+        }
+        int s0 = 0;
+        do {
+            // This block prefetches the next one: same unit unless s0 is the
+            // unit's last block (always the next units when UPB > 1).
+            if constexpr (UPB == 1) {
+                const bool last = s0 + DEPTH >= KS;
+                target(last ? cb + 1 : cb, last ? 0 : s0 + DEPTH);
+            } else {
+                target(cb + UPB, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < DEPTH; ++r) {
+                const int s1 = bslot == 2 ? 0 : bslot + 1;  // next step's weights
+                const int s2 = s1 == 2 ? 0 : s1 + 1;        // step after: held step g-1
+                // Fragments of the next step (stored two steps ago, published
+                // by the previous step's barrier).
+                const T * bs = &s_b[s1][(lg * BN + ch * WN + l16) * 8];
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) rf[(r + 1) & 1][nt] = *(const V *) (bs + nt * 16 * 8);
+#pragma unroll
+                for (int q = 0; q < QB; ++q)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        acc[q][nt] = Mfma<DT>::mac(to_mfma_rows<V>(ra[r][q], perm), rf[r & 1][nt], acc[q][nt]);
+                // Weights of step g + 2 (fetched two steps ago) into the slot
+                // whose fragments every wavefront read before the last barrier.
+                store_b(s2, rw[(r + 2) % DEPTH]);
+                load_b(rw[r], r);
+                load_a(ra[r], r);
+                bslot = s1;
+                lds_barrier();
+                // Keep each step's loads in its step: the scheduler would
+                // otherwise sink the whole ring's loads below the last MFMA.
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (UPB > 1) {
+                    // A unit ends inside the block; a unit past the last one
+                    // (odd unit count) multiplied repeated data and is dropped.
+                    if (r % SPU == SPU - 1 && cb + r / SPU < U) flush(cb + r / SPU);
+                    if (r % SPU == SPU - 1) {
+#pragma unroll
+                        for (int q = 0; q < QB; ++q)
+#pragma unroll
+                            for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+                }
+            }
+            s0 += DEPTH;
+        } while (s0 < KS);
+        if constexpr (UPB == 1) flush(cb);
     }
     lds_barrier();
     // Epilogue: bias, round to the storage type, 16-byte coalesced stores.
@@ -663,12 +696,13 @@ int conv_stream_group(int co) {
 }
 
 bool conv_stream_supported(int dtype, int ci, int co) {
-    // Units must span a whole number of 4-step blocks (Ci/32 steps).
-    return conv_mfma_supported(dtype, ci, co) && ci % 128 == 0;
+    // A unit (Ci/32 K steps) spans a whole number of 4-step blocks, or two
+    // units (Ci = 64) make one block.
+    return conv_mfma_supported(dtype, ci, co) && (ci % 128 == 0 || ci == 64);
 }
 
 namespace {
-template <int DT, int BN, int DEPTH, int NW, int RG>
+template <int DT, int BN, int DEPTH, int NW, int RG, int UPB>
 hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
                            const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
                            const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
@@ -679,7 +713,7 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32
     if (grid > 0x7fffffffLL) {
         return hipErrorInvalidValue;
     }
-    k_conv_mfma_stream<DT, BN, DEPTH, NW, RG><<<(unsigned) grid, 64 * NW, 0, s>>>(
+    k_conv_mfma_stream<DT, BN, DEPTH, NW, RG, UPB><<<(unsigned) grid, 64 * NW, 0, s>>>(
         (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co, col_tiles);
     return hipGetLastError();
 }
@@ -689,11 +723,12 @@ hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int3
                             const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
                             const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
     const bool wide = co % 128 == 0;
-#define TSH_STREAM(BNV, DV) \
-    launch_stream_t<DT, BNV, DV, TSH_STREAM_WAVES, TSH_STREAM_ROW_GROUPS>(x, pair_src, pair_dst, tile_off, tile_counts, \
-                                                                       w16, bias, y, n, ci, co, s)
-    if (wide) return TSH_STREAM(128, 4);
-    return TSH_STREAM(64, 4);
+    const bool pair = ci == 64;  // two 2-step units per 4-step block
+#define TSH_STREAM(BNV, UV)                                                                                       \
+    launch_stream_t<DT, BNV, 4, TSH_STREAM_WAVES, TSH_STREAM_ROW_GROUPS, UV>(x, pair_src, pair_dst, tile_off,      \
+                                                                           tile_counts, w16, bias, y, n, ci, co, s)
+    if (wide) return pair ? TSH_STREAM(128, 2) : TSH_STREAM(128, 1);
+    return pair ? TSH_STREAM(64, 2) : TSH_STREAM(64, 1);
 #undef TSH_STREAM
 }
 }  // namespace

@@ -137,7 +137,7 @@ bool conv_mfma_supported(int dtype, int ci, int co);
 hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nbr, const uint32_t * mask,
                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
                                    hipStream_t s);
-// Streamed compacted schedule over the tile-major pair lists (needs ci % 128 == 0).
+// Streamed compacted schedule over the tile-major pair lists (needs ci == 64 or ci % 128 == 0).
 // Its weights use the grouped packing: [27][ci/8][co][8] whose packed column
 // b*16g + nt*16 + l holds channel b*16g + l*g + nt, g = conv_stream_group(co).
 int conv_stream_group(int co);
