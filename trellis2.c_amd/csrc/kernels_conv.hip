@@ -23,7 +23,10 @@
 //  * compact  - bf16/fp16 storage, Ci = 64 or Ci % 128 == 0, Co % 64 == 0.  The same MFMA
 //               tiles driven by the kernel map's compacted per-tile pair
 //               lists, so the MFMA rows are valid (src, dst) pairs only; sums
-//               of a 256-row tile stay in LDS until one final store.
+//               of a 256-row tile stay in LDS until one final store.  Blocks
+//               of 128 output channels run k_conv_mfma_wreg (weights in
+//               registers, feature rows shared through LDS), blocks of 64
+//               k_conv_mfma_stream (weights shared through LDS).
 #include "tsh_internal.h"
 
 namespace tsh {
@@ -634,6 +637,316 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     }
 }
 
+// ---------------------------------------------------------------------------
+// Compacted MFMA kernel with the weights in registers.
+//
+// Same units, tile sums in LDS, flush and epilogue as k_conv_mfma_stream, with
+// the two operands' staging paths exchanged:
+//  * A (the unit's gathered feature rows: 128 rows x 32 channels per step,
+//    8 KB) is fetched once per step by the whole block, one 16-byte piece per
+//    thread with four neighbouring lanes reading one row's 64 bytes, and
+//    stored into a 3-slot LDS ring two steps before use; each wavefront reads
+//    its row blocks' MFMA fragments one step before use.  The ring's layout
+//    (a_granule) keeps both the coalesced store and the fragment reads free
+//    of bank conflicts, and no lane transpose is needed.
+//  * B (the weights) never passes through LDS: each wavefront fetches its own
+//    channels' fragments straight into registers one block of DEPTH steps
+//    ahead and multiplies them there.
+// With RG row groups a step reads 64/RG KB of A fragments from LDS and fetches
+// RG x 8 KB of weights (each row group fetches all BN channels); RG = 2 (each
+// wavefront: 4 row blocks x 32 channels) balances the two.  Blocks of DEPTH =
+// 8 steps (when a unit is a whole number of them) give the gathers six steps
+// between fetch and use.
+// ---------------------------------------------------------------------------
+
+// LDS layout of one 16-row block of A (64 granules of 16 bytes: 16 rows x 4
+// chunks).  ds_read_b128 / ds_write_b128 serve 16 lanes per cycle from the 64
+// banks without conflict when lanes 0-7 of each 16-lane group touch granules
+// 0-7 (mod 16) and lanes 8-15 granules 8-15, each once.  Row i, chunk c sits at
+//   16 * (i1 + 2 i2) + 8 i3 + 4 (c1 ^ i2) + 2 (c0 ^ i1) + i0     (bits of i, c),
+// which meets that for the fragment reads (lane i + 16 c reads row i, chunk c)
+// and, with quad j fetching row a_quad_row(j) (bits 1 and 3 of j exchanged),
+// for the stores (lane 4 j + c stores row a_quad_row(j), chunk c).
+__device__ __forceinline__ int a_granule(int i, int c) {
+    const int i0 = i & 1, i1 = (i >> 1) & 1, i2 = (i >> 2) & 1, i3 = (i >> 3) & 1;
+    return 16 * (i1 + 2 * i2) + 8 * i3 + 4 * (((c >> 1) & 1) ^ i2) + 2 * ((c & 1) ^ i1) + i0;
+}
+__device__ __forceinline__ int a_quad_row(int j) { return (j & 5) | (((j >> 1) & 1) << 3) | (((j >> 3) & 1) << 1); }
+
+template <int DT, int BN, int RG, int UPB, int DEPTH>
+__global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,
+                                                        const int32_t * __restrict__ pair_src,
+                                                        const int32_t * __restrict__ pair_dst,
+                                                        const int32_t * __restrict__ tile_off,
+                                                        const int32_t * __restrict__ tile_counts,
+                                                        const typename Store<DT>::T * __restrict__ w16,
+                                                        const float * __restrict__ bias,
+                                                        typename Store<DT>::T * __restrict__ y, int64_t n, int ci,
+                                                        int co, int64_t n_col_tiles) {
+    using T = typename Store<DT>::T;
+    using V = typename Mfma<DT>::V;
+    constexpr int NW = 8;            // wavefronts
+    constexpr int NTHR = 64 * NW;
+    constexpr int TM = kMapTile;     // rows per block = rows per kernel-map tile
+    constexpr int BK = 32;           // input channels per K step
+    constexpr int CG = NW / RG;      // channel groups
+    constexpr int WN = BN / CG;      // channels per wavefront
+    constexpr int NT = WN / 16;      // MFMA column tiles per wavefront
+    constexpr int QB = 8 / RG;       // row blocks per wavefront per unit
+    constexpr int PASS = 128;        // pairs per unit
+    constexpr int MAX_UNITS = 27 * (TM / PASS);
+    constexpr int QF = QB < 2 ? QB : 2;  // row blocks per flush batch
+    constexpr int RING = UPB == 1 ? 4 : 8;
+    constexpr int SPU = DEPTH / UPB;
+    static_assert((RG == 1 || RG == 2 || RG == 4) && NT >= 1 && WN % 16 == 0, "row groups");
+    static_assert(PASS * 4 == NTHR, "one 16-byte A piece per thread and step");
+    static_assert(UPB == 1 || UPB == 2, "units per block");
+    static_assert(DEPTH == 4 || DEPTH == 8, "block of 4 or 8 steps");
+    __shared__ float s_acc[(TM + 1) * BN];      // row TM absorbs padding rows
+    __shared__ __attribute__((aligned(16))) T s_a[3][PASS * BK];
+    __shared__ int32_t s_rsrc[RING][PASS];
+    __shared__ uint16_t s_rdst[RING][PASS];     // tile-local dst row, TM for padding
+    __shared__ int32_t s_uk[MAX_UNITS], s_ustart[MAX_UNITS], s_ucnt[MAX_UNITS];
+    __shared__ int32_t s_cnt[27], s_start[27];
+    __shared__ int32_t s_units;
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int rh = wave % RG, ch = wave / RG;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int64_t logical = xcd_remap(blockIdx.x, (int64_t) gridDim.x);
+    const int64_t tile = logical / n_col_tiles;
+    const int64_t row0 = tile * TM;
+    const int col0 = (int) (logical % n_col_tiles) * BN;
+    const int ci8 = ci >> 3;
+    const int KS = ci / BK;
+
+    for (int i = t; i < (TM + 1) * BN; i += NTHR) s_acc[i] = 0.0f;
+    if (t < 27) {
+        s_cnt[t] = tile_counts[tile * 27 + t];
+        s_start[t] = tile_off[tile * 27 + t];
+    }
+    lds_barrier();
+    // Unit table: offset k contributes ceil(count / PASS) units, in k order.
+    if (t < 27) {
+        int u = 0;
+#pragma unroll 1
+        for (int k = 0; k < t; ++k) u += (s_cnt[k] + PASS - 1) / PASS;
+        const int c = s_cnt[t];
+#pragma unroll 1
+        for (int p = 0; p < c; p += PASS, ++u) {
+            s_uk[u] = t;
+            s_ustart[u] = s_start[t] + p;
+            s_ucnt[u] = c - p < PASS ? c - p : PASS;
+        }
+        if (t == 26) s_units = u;
+    }
+    lds_barrier();
+    const int U = s_units;
+    if (U == 0) return;  // unreachable for a tile with rows: the centre offset pairs every row with itself
+
+    // Unit lists, staged two blocks ahead in a ring of RING slots (threads
+    // 0..127 carry src entries, 128..255 dst entries).  Padding entries
+    // repeat the unit's last pair, so every gather stays in range; past the
+    // last unit the last unit is loaded again (never used).
+    const int le = t & (PASS - 1);
+    const int32_t * list = t < PASS ? pair_src : pair_dst;
+    const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
+    auto list_load = [&](int u) -> int32_t {
+        if (t >= 2 * PASS) return 0;
+        const int lu = u < U ? u : U - 1;
+        const int c = s_ucnt[lu];
+        return list[s_ustart[lu] + (le < c ? le : c - 1)];
+    };
+    auto list_store = [&](int u, int32_t v) {
+        if (t < PASS) {
+            s_rsrc[u & (RING - 1)][le] = v;
+        } else if (t < 2 * PASS) {
+            const int c = s_ucnt[u < U ? u : U - 1];
+            s_rdst[u & (RING - 1)][le] = (uint16_t) (le < c ? v - list_bias : TM);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < 2 * UPB; ++j) list_store(j, list_load(j));
+    int32_t lv[UPB];
+#pragma unroll
+    for (int j = 0; j < UPB; ++j) lv[j] = list_load(2 * UPB + j);
+    lds_barrier();
+
+    // This thread's A piece: wavefront w fetches and stores row block w of the
+    // unit; quad j of the wavefront (lanes 4j .. 4j+3) fetches row
+    // a_quad_row(j) of the block, lane 4j + c its chunk c.  Fragment q of
+    // this lane: chunk lg of row l16 of row block rh + RG q.
+    const int arow = (t >> 6) * 16 + a_quad_row((t >> 2) & 15), achunk = t & 3;
+    const int a_st = ((t >> 6) * 64 + a_granule(arow & 15, achunk)) * 8;
+    const int a_ld = (rh * 64 + a_granule(l16, lg)) * 8;
+    constexpr int A_QSTRIDE = RG * 64 * 8;
+
+    // Operand addresses of the next block of DEPTH steps, which covers UPB
+    // units of SPU steps each: unit tu + r / SPU, K step tps + r % SPU for
+    // step r (past the last unit: the last unit again).
+    const int64_t bstep = (int64_t) 4 * co * 8;  // elements between consecutive K steps' weights
+    const int64_t blane = ((int64_t) lg * co + ch * WN + l16) * 8;
+    const T * pa[UPB];
+    const T * pb[UPB];
+    auto target = [&](int tu0, int tps) {
+#pragma unroll
+        for (int uo = 0; uo < UPB; ++uo) {
+            const int tu = tu0 + uo < U ? tu0 + uo : U - 1;
+            const int32_t src = s_rsrc[tu & (RING - 1)][arow];
+            pa[uo] = x + (int64_t) src * ci + tps * BK + achunk * 8;
+            pb[uo] = w16 + ((int64_t) (s_uk[tu] * ci8 + tps * 4) * co + col0) * 8 + blane;
+        }
+    };
+    auto load_a = [&](V & a, int r) { a = *(const V *) (pa[r / SPU] + (r % SPU) * BK); };
+    auto load_b = [&](V * b, int r) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) b[nt] = *(const V *) (pb[r / SPU] + (r % SPU) * bstep + nt * 16 * 8);
+    };
+    auto store_a = [&](int slot, const V & a) { *(V *) (&s_a[slot][a_st]) = a; };
+    auto read_a = [&](V * f, int slot) {
+#pragma unroll
+        for (int q = 0; q < QB; ++q) f[q] = *(const V *) (&s_a[slot][a_ld + q * A_QSTRIDE]);
+    };
+
+    V ra[DEPTH];      // A pieces in flight
+    V rb[DEPTH][NT];  // weights of the block's steps (refilled with the next block's)
+    V af[2][QB];      // A fragments of step g in af[g & 1]
+    f32x4 acc[QB][NT];
+#pragma unroll
+    for (int q = 0; q < QB; ++q)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Flush: add a unit's products into the tile sums (as in
+    // k_conv_mfma_stream: one vector read-modify-write per row, padding rows
+    // into the spare row TM, reads batched ahead of the writes).
+    auto flush = [&](int unit) {
+        const int slot = unit & (RING - 1);
+        using Row = float __attribute__((ext_vector_type(NT)));
+#pragma unroll
+        for (int q0 = 0; q0 < QB; q0 += QF) {
+            Row * dst[QF][4];
+            Row v[QF][4];
+#pragma unroll
+            for (int qq = 0; qq < QF; ++qq) {
+                const ushort4 d = *(const ushort4 *) &s_rdst[slot][(rh + RG * (q0 + qq)) * 16 + lg * 4];
+                const int rows[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dst[qq][i] = (Row *) (s_acc + rows[i] * BN + ch * WN + l16 * NT);
+            }
+#pragma unroll
+            for (int qq = 0; qq < QF; ++qq)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[qq][i] = *dst[qq][i];
+#pragma unroll
+            for (int qq = 0; qq < QF; ++qq)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) v[qq][i][nt] += acc[q0 + qq][nt][i];
+                    *dst[qq][i] = v[qq][i];
+                }
+#pragma unroll
+            for (int qq = 0; qq < QF; ++qq)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[q0 + qq][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+
+    // Block 0: A of steps 0 and 1 straight into LDS slots 0 and 1, steps 2 ..
+    // DEPTH-1 into ring slots 2 .. DEPTH-1; weights of steps 0 .. DEPTH-1.
+    target(0, 0);
+    load_a(ra[0], 0);
+    store_a(0, ra[0]);
+    load_a(ra[1], 1);
+    store_a(1, ra[1]);
+#pragma unroll
+    for (int r = 2; r < DEPTH; ++r) load_a(ra[r], r);
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) load_b(rb[r], r);
+    lds_barrier();
+    read_a(af[0], 0);
+
+    int aslot = 0;  // LDS slot of the current step's A (step g: g % 3)
+    for (int cb = 0; cb < U; cb += UPB) {
+#pragma unroll
+        for (int j = 0; j < UPB; ++j) {
+            list_store(cb + 2 * UPB + j, lv[j]);
+            lv[j] = list_load(cb + 3 * UPB + j);
+        }
+        int s0 = 0;
+        do {
+            if constexpr (UPB == 1) {
+                const bool last = s0 + DEPTH >= KS;
+                target(last ? cb + 1 : cb, last ? 0 : s0 + DEPTH);
+            } else {
+                target(cb + UPB, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < DEPTH; ++r) {
+                const int s1 = aslot == 2 ? 0 : aslot + 1;  // next step's A
+                const int s2 = s1 == 2 ? 0 : s1 + 1;        // step after: held step g-1
+                // Fragments of the next step (stored two steps ago, published
+                // by the previous step's barrier).
+                read_a(af[(r + 1) & 1], s1);
+                // A of step g + 2 (fetched DEPTH - 2 steps ago) into the slot
+                // whose fragments every wavefront read before the last
+                // barrier.  Both LDS operations are issued ahead of the MFMAs
+                // so that they run under them.
+                store_a(s2, ra[(r + 2) % DEPTH]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int q = 0; q < QB; ++q)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        acc[q][nt] = Mfma<DT>::mac(af[r & 1][q], rb[r][nt], acc[q][nt]);
+                // Refill: A of step g + DEPTH, and the next block's weights in
+                // place of the ones just used.
+                load_a(ra[r], r);
+                load_b(rb[r], r);
+                aslot = s1;
+                lds_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (UPB > 1) {
+                    if (r % SPU == SPU - 1 && cb + r / SPU < U) flush(cb + r / SPU);
+                    if (r % SPU == SPU - 1) {
+#pragma unroll
+                        for (int q = 0; q < QB; ++q)
+#pragma unroll
+                            for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+                }
+            }
+            s0 += DEPTH;
+        } while (s0 < KS);
+        if constexpr (UPB == 1) flush(cb);
+    }
+    lds_barrier();
+    constexpr int CHUNKS = BN / 8;
+    for (int e = t; e < TM * CHUNKS; e += NTHR) {
+        const int rr = e / CHUNKS, cc = (e % CHUNKS) * 8;
+        const int64_t row = row0 + rr;
+        if (row >= n) continue;
+        union {
+            int4 v;
+            T h[8];
+        } o;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float bv = bias != nullptr ? bias[col0 + cc + u] : 0.0f;
+            const float v = s_acc[rr * BN + cc + u] + bv;
+            if constexpr (DT == kBF16) {
+                o.h[u] = f32_to_bf16(v);
+            } else {
+                o.h[u] = (T) v;
+            }
+        }
+        *(int4 *) (y + row * co + col0 + cc) = o.v;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_conv_generic(int dtype, const void * x, const int32_t * nbr, const float * w32, const float * bias,
@@ -691,8 +1004,10 @@ hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nb
 
 
 int conv_stream_group(int co) {
-    const int bn = co % 128 == 0 ? 128 : 64;
-    return bn / (TSH_STREAM_WAVES / TSH_STREAM_ROW_GROUPS) / 16;
+    // 128-channel blocks run k_conv_mfma_wreg (2 row groups x 4 channel
+    // groups of 32), 64-channel blocks k_conv_mfma_stream.
+    if (co % 128 == 0) return 128 / 4 / 16;
+    return 64 / (TSH_STREAM_WAVES / TSH_STREAM_ROW_GROUPS) / 16;
 }
 
 bool conv_stream_supported(int dtype, int ci, int co) {
@@ -713,8 +1028,23 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32
     if (grid > 0x7fffffffLL) {
         return hipErrorInvalidValue;
     }
-    k_conv_mfma_stream<DT, BN, DEPTH, NW, RG, UPB><<<(unsigned) grid, 64 * NW, 0, s>>>(
-        (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co, col_tiles);
+    if constexpr (BN == 128) {
+        // Weights in registers; blocks of 8 steps when a unit is a whole
+        // number of them (Ci % 256 == 0), else 4.
+        if (UPB == 1 && ci % 256 == 0) {
+            k_conv_mfma_wreg<DT, BN, 2, UPB, UPB == 1 ? 8 : 4><<<(unsigned) grid, 512, 0, s>>>(
+                (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co,
+                col_tiles);
+        } else {
+            k_conv_mfma_wreg<DT, BN, 2, UPB, 4><<<(unsigned) grid, 512, 0, s>>>(
+                (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co,
+                col_tiles);
+        }
+    } else {
+        k_conv_mfma_stream<DT, BN, DEPTH, NW, RG, UPB><<<(unsigned) grid, 64 * NW, 0, s>>>(
+            (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co,
+            col_tiles);
+    }
     return hipGetLastError();
 }
 
