@@ -412,6 +412,50 @@ def test_row_ops(be32, be16, bebf, dtype):
             assert np.array_equal(got.reshape(n, 48), exp)
 
 
+# Shapes of the MFMA linear: 64- and 128-channel column tiles, Ci = 64 (two
+# tiles per 4-step block) and Ci % 128 == 0, ragged row counts, and enough
+# tiles that every block walks several of them.
+LINEAR_MFMA_CASES = [
+    (64, 64, 1), (64, 256, 37), (128, 512, 1000), (512, 128, 777), (256, 192, 300), (128, 128, 40000),
+    (1024, 256, 2049),
+]
+
+
+@pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
+@pytest.mark.parametrize("ci,co,n", LINEAR_MFMA_CASES)
+def test_linear_mfma_vs_oracle(be16, bebf, dtype, ci, co, n):
+    be = backend_for(dtype, None, be16, bebf)
+    say(f"linear mfma dtype={dtype} ci={ci} co={co} n={n}")
+    rng = np.random.default_rng(ci * 7 + co + n)
+    x = sh.storage_round(rng.standard_normal((n, ci)), dtype)
+    w = sh.storage_round(rng.standard_normal((co, ci)) / math.sqrt(ci), dtype)
+    bias = rng.standard_normal(co).astype(np.float32)
+    xb = be.upload(x)
+    yb = be.alloc(n * co)
+    for silu in (False, True):
+        for bb in (bias, None):
+            be.linear(xb, w, bb, yb, n, ci, co, silu=silu)
+            exp = orc.linear(x, w, bb, n, ci, co, silu)
+            assert max_rel_err(be.download(yb), exp) <= TOL[dtype]
+
+
+def test_linear_mfma_rows_independent(bebf):
+    """Each row depends on its own input row only (no stale tile state)."""
+    ci, co, n = 128, 256, 3000
+    rng = np.random.default_rng(5)
+    x = sh.storage_round(rng.standard_normal((n, ci)), sh.BF16)
+    w = sh.storage_round(rng.standard_normal((co, ci)) / math.sqrt(ci), sh.BF16)
+    xb = bebf.upload(x)
+    yb = bebf.alloc(n * co)
+    bebf.linear(xb, w, None, yb, n, ci, co)
+    full = bebf.download(yb).reshape(n, co)
+    sub = x[1234:1234 + 129]
+    sb = bebf.upload(np.ascontiguousarray(sub))
+    ys = bebf.alloc(129 * co)
+    bebf.linear(sb, w, None, ys, 129, ci, co)
+    assert np.array_equal(bebf.download(ys).reshape(129, co), full[1234:1234 + 129])
+
+
 def test_trim_releases_and_weights_reload(be32):
     coords, feats, w, bias, ci, co = small_conv_cases()["direct"]
     a = run_conv(be32, coords, feats, w, bias, ci, co)

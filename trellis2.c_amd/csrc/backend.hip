@@ -43,7 +43,8 @@ enum WeightLayout : int {
     kLayoutConvMfma = 2,  // storage type [27][ci/8][co][8]
     kLayoutLinearT = 3,   // fp32 [ci][co]
     kLayoutVector = 4,    // fp32 [count]
-    kLayoutConvMfmaGrouped = 5  // kLayoutConvMfma with the streamed kernel's column grouping
+    kLayoutConvMfmaGrouped = 5,  // kLayoutConvMfma with the compacted kernels' column grouping
+    kLayoutLinearMfma = 6        // storage type [ci/8][co][8], linear_mfma_group column grouping
 };
 
 struct StageMark {
@@ -54,6 +55,7 @@ struct StageMark {
 struct Backend {
     trellis_sparse_backend base;
     int device = 0;
+    int cus = 0;  // compute units of the device
     hipStream_t stream = nullptr;
     trellis_sparse_hip_policy policy{};
     std::string last_error;
@@ -273,6 +275,26 @@ trellis_status get_weight(Backend * be, const float * host, size_t count, int la
             }
             break;
         }
+        case kLayoutLinearMfma: {  // [co][ci] -> [ci/8][co][8] in the storage type, grouped columns
+            staged.resize((size_t) ci * co * 2);
+            uint16_t * w = (uint16_t *) staged.data();
+            const int g = linear_mfma_group(co), wn = 16 * g;
+            for (int o = 0; o < co; ++o) {
+                const int pos = (o / wn) * wn + (o % g) * 16 + (o % wn) / g;
+                for (int c = 0; c < ci; ++c) {
+                    const float v = host[(size_t) o * ci + c];
+                    uint16_t h;
+                    if (dt == kBF16) {
+                        h = f32_to_bf16(v);
+                    } else {
+                        const _Float16 f = (_Float16) v;
+                        memcpy(&h, &f, 2);
+                    }
+                    w[(((size_t) (c / 8) * co + pos) * 8) + (c & 7)] = h;
+                }
+            }
+            break;
+        }
         case kLayoutLinearT: {  // [co][ci] -> [ci][co]
             staged.resize((size_t) ci * co * sizeof(float));
             float * w = (float *) staged.data();
@@ -425,12 +447,19 @@ trellis_status linear_impl(trellis_sparse_backend * backend, const trellis_spars
     CallScope scope(be);
     const void * wt = nullptr;
     const void * bd = nullptr;
-    trellis_status st = get_weight(be, weight, (size_t) ci * co, kLayoutLinearT, ci, co, &wt);
+    const int dt = be->policy.compute_dtype;
+    // bf16/fp16 with Ci = 64 or Ci % 128 == 0 and Co % 64 == 0: MFMA kernel;
+    // otherwise (and always for fp32) the reference-order VALU kernel.
+    const bool mfma = linear_mfma_supported(dt, ci, co);
+    trellis_status st =
+        get_weight(be, weight, (size_t) ci * co, mfma ? kLayoutLinearMfma : kLayoutLinearT, ci, co, &wt);
     if (st == TRELLIS_STATUS_OK) st = get_weight(be, bias, (size_t) co, kLayoutVector, 0, co, &bd);
     if (st != TRELLIS_STATUS_OK) return st;
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
-    const hipError_t err = launch_linear(be->policy.compute_dtype, x->ptr, (const float *) wt, (const float *) bd,
-                                         y->ptr, n, ci, co, silu, be->stream);
+    const hipError_t err =
+        mfma ? launch_linear_mfma(dt, x->ptr, wt, (const float *) bd, y->ptr, n, ci, co, silu, be->cus, be->stream)
+             : launch_linear(dt, x->ptr, (const float *) wt, (const float *) bd, y->ptr, n, ci, co, silu,
+                             be->stream);
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
     return hip_status(be, err, "linear");
 }
@@ -1123,8 +1152,14 @@ trellis_status trellis_sparse_hip_backend_create_ex(int device, const trellis_sp
         (void) hipGetLastError();
         return TRELLIS_STATUS_CUDA_UNAVAILABLE;
     }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) {
+        (void) hipGetLastError();
+        return TRELLIS_STATUS_CUDA_UNAVAILABLE;
+    }
     auto * be = new (std::nothrow) Backend();
     if (be == nullptr) return TRELLIS_STATUS_OUT_OF_MEMORY;
+    be->cus = cus;
     if (hipStreamCreateWithFlags(&be->stream, hipStreamNonBlocking) != hipSuccess) {
         (void) hipGetLastError();
         delete be;

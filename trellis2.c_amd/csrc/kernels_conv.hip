@@ -28,29 +28,10 @@
 //               registers, feature rows shared through LDS), blocks of 64
 //               k_conv_mfma_stream (weights shared through LDS).
 #include "tsh_internal.h"
+#include "mfma_common.h"
 
 namespace tsh {
 namespace {
-
-// Maps a linear block id onto a logical tile so that each of the 8 XCDs
-// (which receive block ids round-robin) works on one contiguous range of
-// tiles and its L2 sees neighbouring gathers.
-__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t grid) {
-    constexpr int64_t kXcd = 8;
-    const int64_t q = grid / kXcd, r = grid % kXcd;
-    const int64_t xcd = bid % kXcd, slot = bid / kXcd;
-    return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
-}
-
-// Workgroup barrier that orders LDS only.  __syncthreads() also drains every
-// outstanding global load (vmcnt(0)), which would empty the register prefetch
-// ring of the streamed kernel at each barrier; its global loads only read
-// data that no block writes.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // ---------------------------------------------------------------------------
 // Generic VALU kernel: 32 rows x 64 channels per 256-lane block.
@@ -157,25 +138,6 @@ __global__ void __launch_bounds__(256) k_conv_generic(const typename Store<DT>::
 // ---------------------------------------------------------------------------
 // MFMA kernel (bf16 / fp16 storage).
 // ---------------------------------------------------------------------------
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-template <int DT> struct Mfma;
-template <> struct Mfma<kBF16> {
-    typedef bf16x8 V;
-    __device__ static f32x4 mac(V a, V b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
-};
-template <> struct Mfma<kF16> {
-    typedef f16x8 V;
-    __device__ static f32x4 mac(V a, V b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-};
-
-// Lane layout of v_mfma_f32_16x16x32 (64 lanes): A fragment = row (lane%16),
-// 8 consecutive K values starting at 8*(lane/16); B fragment = column
-// (lane%16), the same 8 K values; D = rows 4*(lane/16)+i, column lane%16.
-// Any consistent K permutation of A and B gives the same product, so only
-// the row/column mapping matters for correctness.
 template <int DT, int BN>
 __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<DT>::T * __restrict__ x,
                                                           const int32_t * __restrict__ nbr,
@@ -659,19 +621,6 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
 // between fetch and use.
 // ---------------------------------------------------------------------------
 
-// LDS layout of one 16-row block of A (64 granules of 16 bytes: 16 rows x 4
-// chunks).  ds_read_b128 / ds_write_b128 serve 16 lanes per cycle from the 64
-// banks without conflict when lanes 0-7 of each 16-lane group touch granules
-// 0-7 (mod 16) and lanes 8-15 granules 8-15, each once.  Row i, chunk c sits at
-//   16 * (i1 + 2 i2) + 8 i3 + 4 (c1 ^ i2) + 2 (c0 ^ i1) + i0     (bits of i, c),
-// which meets that for the fragment reads (lane i + 16 c reads row i, chunk c)
-// and, with quad j fetching row a_quad_row(j) (bits 1 and 3 of j exchanged),
-// for the stores (lane 4 j + c stores row a_quad_row(j), chunk c).
-__device__ __forceinline__ int a_granule(int i, int c) {
-    const int i0 = i & 1, i1 = (i >> 1) & 1, i2 = (i >> 2) & 1, i3 = (i >> 3) & 1;
-    return 16 * (i1 + 2 * i2) + 8 * i3 + 4 * (((c >> 1) & 1) ^ i2) + 2 * ((c & 1) ^ i1) + i0;
-}
-__device__ __forceinline__ int a_quad_row(int j) { return (j & 5) | (((j >> 1) & 1) << 3) | (((j >> 3) & 1) << 1); }
 
 template <int DT, int BN, int RG, int UPB, int DEPTH>
 __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,

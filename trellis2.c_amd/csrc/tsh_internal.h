@@ -155,6 +155,14 @@ hipError_t launch_row_norm(int dtype, const void * x, const float * gamma, const
                            int64_t n, int c, float eps, int silu, hipStream_t s);
 hipError_t launch_linear(int dtype, const void * x, const float * wt, const float * bias, void * y, int64_t n,
                          int ci, int co, int silu, hipStream_t s);
+// MFMA linear (bf16/fp16; Ci = 64 or Ci % 128 == 0, Co % 64 == 0).  Weights
+// [ci/8][co][8] in the storage type; packed column g*16j + nt*16 + l (within
+// each group of 16j columns, j = linear_mfma_group(co)) holds channel
+// g*16j + l*j + nt.  cus = the device's compute units (one block each).
+int linear_mfma_group(int co);
+bool linear_mfma_supported(int dtype, int ci, int co);
+hipError_t launch_linear_mfma(int dtype, const void * x, const void * w16, const float * bias, void * y, int64_t n,
+                              int ci, int co, int silu, int cus, hipStream_t s);
 hipError_t launch_c2s_count(int dtype, const void * logits, int64_t n, int32_t * counts, hipStream_t s);
 // Exclusive scan of n int32 values; total written to *total_dev.  tmp needs scan_tmp_bytes(n).
 size_t scan_tmp_bytes(int64_t n);
