@@ -134,6 +134,155 @@ class Cfg2(ConvOnly):
         return 2 * wl.conv_flops(self.pairs, self.ci, self.co)
 
 
+class Block:
+    """Decoder blocks composed from the backend's slots, at config-3 scale (bf16).
+
+    convnext: on the ~1.26M config-3 children, C = 128:
+      conv(128->128) -> row_norm -> linear_silu(128->512) -> linear(512->128) -> add
+      (src/architectures/sparse_unet_decoder/executor.c:176-255).
+    c2s: the C2S up-block on the ~0.32M config-3 parents, Ci = 256 -> Co = 128:
+      linear(256->8) logits -> build_c2s_map_device -> build_rulebook_for_c2s_map;
+      row_norm_silu -> conv(256->1024) on the parents -> c2s_gather_device;
+      skip_repeat_device; row_norm_silu -> conv(128->128) on the children -> add
+      (executor.c:257-554).
+    Slot times come from HIP events on the backend stream between slots.
+    """
+
+    def __init__(self, be, kind):
+        self.be, self.kind = be, kind
+        w = wl.workload(3)
+        rng = np.random.default_rng(11)
+        f32 = lambda a: np.ascontiguousarray(a, np.float32)
+        if kind == "convnext":
+            c = 128
+            pmap = be.upload_coords(w["parent_coords"])
+            dm = be.build_c2s_map_device(be.upload(w["logits"]), w["parent_coords"].shape[0], coords_map=pmap)
+            self.cmap, self.n, self.c = dm, dm.n, c
+            self.h = be.upload(rng.standard_normal((self.n, c)).astype(np.float32))
+            self.conv_w = be.keep(f32(rng.standard_normal((c, 27, c)) / np.sqrt(27 * c)))
+            self.conv_b = be.keep(f32(0.1 * rng.standard_normal(c)))
+            self.gamma = be.keep(f32(1 + 0.1 * rng.standard_normal(c)))
+            self.beta = be.keep(f32(0.1 * rng.standard_normal(c)))
+            self.w0 = be.keep(f32(rng.standard_normal((4 * c, c)) / np.sqrt(c)))
+            self.b0 = be.keep(f32(0.1 * rng.standard_normal(4 * c)))
+            self.w2 = be.keep(f32(rng.standard_normal((c, 4 * c)) / np.sqrt(4 * c)))
+            self.b2 = be.keep(f32(0.1 * rng.standard_normal(c)))
+            self.rb = be.build_rulebook_for_c2s_map(self.cmap)
+            self.pairs = be.rulebook_stats(self.rb)["pairs"]
+            self.bufs = [be.alloc(self.n * c), be.alloc(self.n * c), be.alloc(self.n * 4 * c),
+                         be.alloc(self.n * c), be.alloc(self.n * c)]
+            self.slots = ["sparse_conv3d", "row_norm", "linear_silu", "linear", "add"]
+        else:
+            ci, co = 256, 128
+            self.ci, self.co = ci, co
+            self.n = w["parent_coords"].shape[0]
+            self.pmap = be.upload_coords(w["parent_coords"])
+            self.prb = be.build_rulebook_for_c2s_map(self.pmap)
+            self.ppairs = be.rulebook_stats(self.prb)["pairs"]
+            self.h = be.upload(w["parent_feats"])
+            self.ws = be.keep(f32(rng.standard_normal((8, ci)) / np.sqrt(ci)))
+            self.bs = be.keep(f32(0.1 * rng.standard_normal(8)))
+            self.g1 = be.keep(f32(1 + 0.1 * rng.standard_normal(ci)))
+            self.b1 = be.keep(f32(0.1 * rng.standard_normal(ci)))
+            self.w1 = be.keep(f32(rng.standard_normal((8 * co, 27, ci)) / np.sqrt(27 * ci)))
+            self.c1b = be.keep(f32(0.1 * rng.standard_normal(8 * co)))
+            self.w2 = be.keep(f32(rng.standard_normal((co, 27, co)) / np.sqrt(27 * co)))
+            self.c2b = be.keep(f32(0.1 * rng.standard_normal(co)))
+            self.subdiv = be.alloc(self.n * 8)
+            self.norm1 = be.alloc(self.n * ci)
+            self.conv1 = be.alloc(self.n * 8 * co)
+            be.linear(self.h, self.ws, self.bs, self.subdiv, self.n, ci, 8)
+            dm = be.build_c2s_map_device(self.subdiv, self.n, coords_map=self.pmap)
+            self.m = dm.n
+            rb = be.build_rulebook_for_c2s_map(dm)
+            self.pairs = be.rulebook_stats(rb)["pairs"]
+            rb.free()
+            be.free_map(dm)
+            self.bufs = [be.alloc(self.m * co) for _ in range(5)]
+            self.slots = ["linear_subdiv", "build_c2s_map_device", "build_rulebook_for_c2s_map", "row_norm_silu_pre",
+                          "sparse_conv3d_pre", "c2s_gather_device", "skip_repeat_device", "row_norm_silu_post",
+                          "sparse_conv3d_post", "add"]
+
+    def step(self):
+        be = self.be
+        ev = iter(range(1, 16))
+        be.event(0)
+        if self.kind == "convnext":
+            n, c = self.n, self.c
+            conv, norm, mlp1, mlp2, out = self.bufs
+            be.conv(self.rb, self.h, self.conv_w, self.conv_b, conv, c, c)
+            be.event(next(ev))
+            be.row_norm(conv, self.gamma, self.beta, norm, n, c, 1e-6)
+            be.event(next(ev))
+            be.linear(norm, self.w0, self.b0, mlp1, n, c, 4 * c, silu=True)
+            be.event(next(ev))
+            be.linear(mlp1, self.w2, self.b2, mlp2, n, 4 * c, c)
+            be.event(next(ev))
+            be.add(self.h, mlp2, out, n * c)
+            be.event(next(ev))
+            return
+        n, ci, co = self.n, self.ci, self.co
+        be.linear(self.h, self.ws, self.bs, self.subdiv, n, ci, 8)
+        be.event(next(ev))
+        dm = be.build_c2s_map_device(self.subdiv, n, coords_map=self.pmap)
+        be.event(next(ev))
+        rb = be.build_rulebook_for_c2s_map(dm)
+        be.event(next(ev))
+        be.row_norm(self.h, self.g1, self.b1, self.norm1, n, ci, 1e-6, silu=True)
+        be.event(next(ev))
+        be.conv(self.prb, self.norm1, self.w1, self.c1b, self.conv1, ci, 8 * co)
+        be.event(next(ev))
+        h_up, skip, norm2, conv2, out = self.bufs
+        be.c2s_gather_device(self.conv1, dm, h_up, co)
+        be.event(next(ev))
+        be.skip_repeat_device(self.h, dm, skip, ci, co)
+        be.event(next(ev))
+        be.row_norm(h_up, None, None, norm2, self.m, co, 1e-6, silu=True)
+        be.event(next(ev))
+        be.conv(rb, norm2, self.w2, self.c2b, conv2, co, co)
+        be.event(next(ev))
+        be.add(conv2, skip, out, self.m * co)
+        be.event(next(ev))
+        rb.free()
+        be.free_map(dm)
+
+    def flops(self):
+        if self.kind == "convnext":
+            n, c = self.n, self.c
+            return wl.conv_flops(self.pairs, c, c) + 2 * (2 * n * c * 4 * c)
+        return (wl.conv_flops(self.ppairs, self.ci, 8 * self.co) + wl.conv_flops(self.pairs, self.co, self.co)
+                + 2 * self.n * self.ci * 8)
+
+
+def run_block(args):
+    be = sh.Backend(0, sh.BF16)
+    job = Block(be, args.block)
+    for _ in range(args.warmup):
+        job.step()
+    be.synchronize()
+    slot_ms = [0.0] * len(job.slots)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        job.step()
+        be.synchronize()
+        for i in range(len(job.slots)):
+            slot_ms[i] += be.elapsed(i, i + 1)
+    wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    slots = {name: round(ms / args.steps, 4) for name, ms in zip(job.slots, slot_ms)}
+    dev = sum(slots.values())
+    out = {"block": args.block, "dtype": "bf16", "data": "synthetic (config-3 voxel sets, seeded random weights)",
+           "steps": args.steps, "warmup": args.warmup, "ms_per_block": round(dev, 4),
+           "wall_ms_per_block": round(wall, 4), "effective_tflops": round(job.flops() / (dev * 1e-3) / 1e12, 2),
+           "slot_ms": slots}
+    if args.block == "convnext":
+        out.update({"voxels": int(job.n), "pairs": int(job.pairs), "channels": job.c})
+    else:
+        out.update({"parents": int(job.n), "children": int(job.m), "parent_pairs": int(job.ppairs),
+                    "child_pairs": int(job.pairs), "ci": job.ci, "co": job.co})
+    print(json.dumps(out))
+    be.destroy()
+
+
 def conv_schedule(dtype, ci, co, algo):
     """Name of the conv kernel the backend runs (its fallback rules)."""
     mfma = dtype != sh.F32 and ci % 32 == 0 and co % 64 == 0
@@ -194,6 +343,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-stride", type=int, default=16)
     ap.add_argument("--conv-algo", type=int, default=sh.CONV_AUTO)
+    ap.add_argument("--block", choices=["convnext", "c2s"],
+                    help="instead of the configuration step, time one decoder block composed from the backend's "
+                         "slots at config-3 scale and print its own JSON line")
     ap.add_argument("--calibrate", action="store_true",
                     help="run one fp32 add over 2 x 64Mi-element inputs (512 MiB read, 256 MiB written) so PMC "
                          "byte counters can be scaled against a streaming kernel of known traffic")
@@ -219,6 +371,9 @@ def main():
     if sh.device_count() < 1:
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
+    if args.block is not None:
+        run_block(args)
+        return
 
     cfg = args.config
     spec = wl.CONFIGS[cfg]

@@ -1,0 +1,187 @@
+"""GPU parity of the decoder blocks the backend's slots compose into.
+
+The reference decoder builds its blocks from the vtable slots:
+- ConvNeXt block (src/architectures/sparse_unet_decoder/executor.c:176-255):
+  conv(C->C) -> row_norm(gamma, beta, 1e-6) -> linear_silu(C->4C)
+  -> linear(4C->C) -> add(h, .).
+- C2S up-block, device-map path (executor.c:257-554): linear(Ci->8) logits
+  -> build_c2s_map_device -> build_rulebook_for_c2s_map;
+  row_norm_silu(h) -> conv(Ci->8Co) on the parent rulebook
+  -> c2s_gather_device; skip_repeat_device(h);
+  row_norm_silu(h_up, no affine) -> conv(Co->Co) on the child rulebook
+  -> add(conv2, skip).
+Here the same sequences run through the C ABI and are compared with the
+oracle's restatement of each slot, chained with the storage rounding the
+backend applies between slots.  Maps stay bit-exact; values meet the
+per-dtype tolerance of check_close (tests/test_sparse_decoder_backend.c:16-24).
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+import sparse_hip as sh
+import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+TOL = {sh.F32: 1e-5, sh.F16: 2e-2, sh.BF16: 2e-2}
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def max_rel_err(got, exp):
+    got = np.asarray(got, dtype=np.float64).ravel()
+    exp = np.asarray(exp, dtype=np.float64).ravel()
+    assert got.shape == exp.shape
+    scale = np.maximum(1.0, np.maximum(np.abs(got), np.abs(exp)))
+    return float(np.max(np.abs(got - exp) / scale)) if got.size else 0.0
+
+
+@pytest.fixture(scope="module")
+def backends():
+    bes = {dt: sh.Backend(0, dt) for dt in (sh.F32, sh.F16, sh.BF16)}
+    yield bes
+    for b in bes.values():
+        b.destroy()
+
+
+def shell_coords(n_max):
+    """Config-1 sphere shell (batch 0), first n_max voxels in generator order."""
+    return np.ascontiguousarray(wl.make_coords(1)[:n_max])
+
+
+def weights(rng, co, k, ci, dtype):
+    return sh.storage_round(rng.standard_normal((co, k, ci)) / math.sqrt(k * ci), dtype)
+
+
+@pytest.mark.parametrize("dtype", [sh.F32, sh.F16, sh.BF16])
+@pytest.mark.parametrize("c", [64, 128])
+def test_convnext_block_vs_oracle(backends, dtype, c):
+    be = backends[dtype]
+    rnd = lambda a: sh.storage_round(a, dtype)
+    rng = np.random.default_rng(c + dtype)
+    coords = shell_coords(6000)
+    n = coords.shape[0]
+    say(f"convnext dtype={dtype} c={c} n={n}")
+    h = rnd(rng.standard_normal((n, c)))
+    conv_w = weights(rng, c, 27, c, dtype)
+    conv_b = rng.standard_normal(c).astype(np.float32) * 0.1
+    gamma = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    w0 = rnd(rng.standard_normal((4 * c, c)) / math.sqrt(c))
+    b0 = (0.1 * rng.standard_normal(4 * c)).astype(np.float32)
+    w2 = rnd(rng.standard_normal((c, 4 * c)) / math.sqrt(4 * c))
+    b2 = (0.1 * rng.standard_normal(c)).astype(np.float32)
+
+    rb = be.build_rulebook(coords)
+    hb = be.upload(h)
+    conv = be.alloc(n * c)
+    norm = be.alloc(n * c)
+    mlp1 = be.alloc(n * 4 * c)
+    mlp2 = be.alloc(n * c)
+    out = be.alloc(n * c)
+    be.conv(rb, hb, conv_w, conv_b, conv, c, c)
+    be.row_norm(conv, gamma, beta, norm, n, c, 1e-6)
+    be.linear(norm, w0, b0, mlp1, n, c, 4 * c, silu=True)
+    be.linear(mlp1, w2, b2, mlp2, n, 4 * c, c)
+    be.add(hb, mlp2, out, n * c)
+    got = be.download(out).reshape(n, c)
+
+    # Oracle chain on the values the backend holds after each slot: the conv
+    # is compared first, then each later slot runs on the backend's own input
+    # so the tolerance applies per slot, not compounded.
+    e_conv = rnd(orc.Rulebook(coords).conv(h, conv_w, conv_b, c, c))
+    g_conv = be.download(conv).reshape(n, c)
+    assert max_rel_err(g_conv, e_conv) <= TOL[dtype]
+    g_norm = be.download(norm).reshape(n, c)
+    assert max_rel_err(g_norm, rnd(orc.row_norm(g_conv, gamma, beta, n, c, 1e-6))) <= TOL[dtype]
+    g_mlp1 = be.download(mlp1).reshape(n, 4 * c)
+    assert max_rel_err(g_mlp1, rnd(orc.linear(g_norm, w0, b0, n, c, 4 * c, silu=True))) <= TOL[dtype]
+    g_mlp2 = be.download(mlp2).reshape(n, c)
+    assert max_rel_err(g_mlp2, rnd(orc.linear(g_mlp1, w2, b2, n, 4 * c, c))) <= TOL[dtype]
+    assert max_rel_err(got, rnd(orc.add(h, g_mlp2))) <= TOL[dtype]
+    # End to end against the oracle chain from the block input alone.
+    e = rnd(orc.row_norm(e_conv, gamma, beta, n, c, 1e-6))
+    e = rnd(orc.linear(e, w0, b0, n, c, 4 * c, silu=True))
+    e = rnd(orc.linear(e, w2, b2, n, 4 * c, c))
+    e = rnd(orc.add(h, e))
+    err = max_rel_err(got, e)
+    say(f"convnext dtype={dtype} c={c} end-to-end max_rel_err={err:.3e}")
+    assert err <= (TOL[dtype] if dtype == sh.F32 else 5e-2)
+    rb.free()
+
+
+@pytest.mark.parametrize("dtype", [sh.F32, sh.BF16])
+def test_c2s_upblock_vs_oracle(backends, dtype):
+    be = backends[dtype]
+    rnd = lambda a: sh.storage_round(a, dtype)
+    ci, co = 64, 32
+    rng = np.random.default_rng(77 + dtype)
+    coords = shell_coords(3000)
+    n = coords.shape[0]
+    say(f"c2s up-block dtype={dtype} parents={n} {ci}->{co}")
+    h = rnd(rng.standard_normal((n, ci)))
+    ws = (rng.standard_normal((8, ci)) / math.sqrt(ci)).astype(np.float32)
+    bs = (0.1 * rng.standard_normal(8)).astype(np.float32)
+    g1 = (1 + 0.1 * rng.standard_normal(ci)).astype(np.float32)
+    b1 = (0.1 * rng.standard_normal(ci)).astype(np.float32)
+    w1 = weights(rng, 8 * co, 27, ci, dtype)
+    c1b = (0.1 * rng.standard_normal(8 * co)).astype(np.float32)
+    w2 = weights(rng, co, 27, co, dtype)
+    c2b = (0.1 * rng.standard_normal(co)).astype(np.float32)
+
+    pmap = be.upload_coords(coords)
+    rb = be.build_rulebook_for_c2s_map(pmap)
+    hb = be.upload(h)
+    subdiv = be.alloc(n * 8)
+    be.linear(hb, ws, bs, subdiv, n, ci, 8)
+    logits = be.download(subdiv).reshape(n, 8)
+    assert max_rel_err(logits, rnd(orc.linear(h, ws, bs, n, ci, 8))) <= TOL[dtype]
+    dm = be.build_c2s_map_device(subdiv, n, coords_map=pmap)
+    rc, ec, ep, es = orc.c2s_map(coords, logits)
+    assert rc == 0
+    c2, p2, s2 = be.download_c2s_map(dm)
+    assert np.array_equal(c2, ec) and np.array_equal(p2, ep) and np.array_equal(s2, es)
+    m = dm.n
+    nrb = be.build_rulebook_for_c2s_map(dm)
+    assert np.array_equal(be.neighbors(nrb), orc.Rulebook(ec).neighbors())
+
+    norm1 = be.alloc(n * ci)
+    be.row_norm(hb, g1, b1, norm1, n, ci, 1e-6, silu=True)
+    conv1 = be.alloc(n * 8 * co)
+    be.conv(rb, norm1, w1, c1b, conv1, ci, 8 * co)
+    h_up = be.alloc(m * co)
+    be.c2s_gather_device(conv1, dm, h_up, co)
+    skip = be.alloc(m * co)
+    be.skip_repeat_device(hb, dm, skip, ci, co)
+    norm2 = be.alloc(m * co)
+    be.row_norm(h_up, None, None, norm2, m, co, 1e-6, silu=True)
+    conv2 = be.alloc(m * co)
+    be.conv(nrb, norm2, w2, c2b, conv2, co, co)
+    out = be.alloc(m * co)
+    be.add(conv2, skip, out, m * co)
+
+    # Per slot, each on the backend's own input (see the ConvNeXt test).
+    g_n1 = be.download(norm1).reshape(n, ci)
+    assert max_rel_err(g_n1, rnd(orc.row_norm(h, g1, b1, n, ci, 1e-6, silu=True))) <= TOL[dtype]
+    g_c1 = be.download(conv1).reshape(n, 8 * co)
+    assert max_rel_err(g_c1, rnd(orc.Rulebook(coords).conv(g_n1, w1, c1b, ci, 8 * co))) <= TOL[dtype]
+    g_up = be.download(h_up).reshape(m, co)
+    assert np.array_equal(g_up, orc.c2s_gather(g_c1, ep, es, co))
+    g_skip = be.download(skip).reshape(m, co)
+    assert np.array_equal(g_skip, orc.skip_repeat(h, ep, es, ci, co))
+    g_n2 = be.download(norm2).reshape(m, co)
+    assert max_rel_err(g_n2, rnd(orc.row_norm(g_up, None, None, m, co, 1e-6, silu=True))) <= TOL[dtype]
+    g_c2 = be.download(conv2).reshape(m, co)
+    assert max_rel_err(g_c2, rnd(orc.Rulebook(ec).conv(g_n2, w2, c2b, co, co))) <= TOL[dtype]
+    got = be.download(out).reshape(m, co)
+    assert max_rel_err(got, rnd(orc.add(g_c2, g_skip))) <= TOL[dtype]
+    say(f"c2s up-block dtype={dtype} children={m}")
+    rb.free()
+    nrb.free()

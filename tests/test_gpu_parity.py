@@ -412,6 +412,23 @@ def test_row_ops(be32, be16, bebf, dtype):
             assert np.array_equal(got.reshape(n, 48), exp)
 
 
+@pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
+@pytest.mark.parametrize("c,n", [(64, 33), (128, 1031), (256, 7), (512, 300), (1024, 65), (2048, 3), (96, 50)])
+def test_row_norm_widths(be16, bebf, dtype, c, n):
+    """Vectorised rows (power-of-two widths) and the general kernel (c = 96)."""
+    be = backend_for(dtype, None, be16, bebf)
+    rng = np.random.default_rng(c + n)
+    x = sh.storage_round(rng.standard_normal((n, c)) * 3 - 1, dtype)
+    g = rng.standard_normal(c).astype(np.float32)
+    b = rng.standard_normal(c).astype(np.float32)
+    xb = be.upload(x)
+    yb = be.alloc(n * c)
+    for silu in (False, True):
+        for gg, bb in ((g, b), (None, None), (g, None)):
+            be.row_norm(xb, gg, bb, yb, n, c, 1e-6, silu=silu)
+            assert max_rel_err(be.download(yb), orc.row_norm(x, gg, bb, n, c, 1e-6, silu)) <= TOL[dtype]
+
+
 # Shapes of the MFMA linear: 64- and 128-channel column tiles, Ci = 64 (two
 # tiles per 4-step block) and Ci % 128 == 0, ragged row counts, and enough
 # tiles that every block walks several of them.

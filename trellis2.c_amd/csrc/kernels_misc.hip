@@ -407,8 +407,112 @@ hipError_t launch_add(int dtype, const void * a, const void * b, void * y, int64
     return hipGetLastError();
 }
 
+namespace {
+// 16-bit storage, C = 8 * LPR * CPL: LPR lanes per row, each holding CPL
+// 16-byte chunks, so a row is read once into registers, reduced with
+// shuffles inside its lane segment (mean, then squared deviations), and
+// written back in 16-byte chunks; 64 / LPR rows per wavefront.  SiLU uses the
+// hardware exp2 / reciprocal (about 1 ulp each, far inside the 16-bit
+// rounding).
+template <int DT, int LPR, int CPL>
+__global__ void __launch_bounds__(256) k_row_norm_vec(const typename Store<DT>::T * __restrict__ x,
+                                                      const float * __restrict__ gamma,
+                                                      const float * __restrict__ beta,
+                                                      typename Store<DT>::T * __restrict__ y, int64_t n, float eps,
+                                                      int silu) {
+    using T = typename Store<DT>::T;
+    constexpr int C = 8 * LPR * CPL;
+    const int lane = threadIdx.x & 63;
+    const int li = lane % LPR;
+    const int64_t row = ((int64_t) blockIdx.x * 4 + (threadIdx.x >> 6)) * (64 / LPR) + lane / LPR;
+    const bool ok = row < n;
+    union Chunk {
+        int4 v;
+        T h[8];
+    };
+    float v[CPL][8];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        Chunk ch;
+        ch.v = ok ? *(const int4 *) (x + row * C + (li + j * LPR) * 8) : int4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[j][e] = Store<DT>::ld(ch.h, e);
+            s += v[j][e];
+        }
+    }
+#pragma unroll
+    for (int d = LPR / 2; d >= 1; d >>= 1) s += __shfl_xor(s, d);
+    const float mean = s / (float) C;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float d = v[j][e] - mean;
+            q += d * d;
+        }
+#pragma unroll
+    for (int d = LPR / 2; d >= 1; d >>= 1) q += __shfl_xor(q, d);
+    const float inv = 1.0f / sqrtf(q / (float) C + eps);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c0 = (li + j * LPR) * 8;
+        // The chunk's 8 scale and shift values as two 16-byte loads each.
+        float gv[8], bv[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float4 g4 = gamma != nullptr ? *(const float4 *) (gamma + c0 + 4 * h) : float4{1.f, 1.f, 1.f, 1.f};
+            const float4 b4 = beta != nullptr ? *(const float4 *) (beta + c0 + 4 * h) : float4{0.f, 0.f, 0.f, 0.f};
+            gv[4 * h] = g4.x, gv[4 * h + 1] = g4.y, gv[4 * h + 2] = g4.z, gv[4 * h + 3] = g4.w;
+            bv[4 * h] = b4.x, bv[4 * h + 1] = b4.y, bv[4 * h + 2] = b4.z, bv[4 * h + 3] = b4.w;
+        }
+        Chunk ch;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float o = (v[j][e] - mean) * inv;
+            if (gamma != nullptr) o *= gv[e];
+            if (beta != nullptr) o += bv[e];
+            if (silu) o = o * __builtin_amdgcn_rcpf(1.0f + __expf(-o));
+            Store<DT>::st(ch.h, e, o);
+        }
+        if (ok) *(int4 *) (y + row * C + c0) = ch.v;
+    }
+}
+
+template <int DT, int LPR, int CPL>
+hipError_t launch_row_norm_vec(const void * x, const float * gamma, const float * beta, void * y, int64_t n,
+                               float eps, int silu, hipStream_t s) {
+    using T = typename Store<DT>::T;
+    constexpr int64_t rows_per_block = 4 * (64 / LPR);
+    const int64_t g = (n + rows_per_block - 1) / rows_per_block;
+    k_row_norm_vec<DT, LPR, CPL><<<(unsigned) g, 256, 0, s>>>((const T *) x, gamma, beta, (T *) y, n, eps, silu);
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_row_norm_vec_dt(const void * x, const float * gamma, const float * beta, void * y, int64_t n, int c,
+                                  float eps, int silu, hipStream_t s) {
+    switch (c) {
+        case 64: return launch_row_norm_vec<DT, 8, 1>(x, gamma, beta, y, n, eps, silu, s);
+        case 128: return launch_row_norm_vec<DT, 16, 1>(x, gamma, beta, y, n, eps, silu, s);
+        case 256: return launch_row_norm_vec<DT, 32, 1>(x, gamma, beta, y, n, eps, silu, s);
+        case 512: return launch_row_norm_vec<DT, 64, 1>(x, gamma, beta, y, n, eps, silu, s);
+        case 1024: return launch_row_norm_vec<DT, 64, 2>(x, gamma, beta, y, n, eps, silu, s);
+        case 2048: return launch_row_norm_vec<DT, 64, 4>(x, gamma, beta, y, n, eps, silu, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+}  // namespace
+
 hipError_t launch_row_norm(int dtype, const void * x, const float * gamma, const float * beta, void * y, int64_t n,
                            int c, float eps, int silu, hipStream_t s) {
+    // 16-bit storage at the decoder's power-of-two widths: vectorised rows.
+    if (dtype != kF32 && (c == 64 || c == 128 || c == 256 || c == 512 || c == 1024 || c == 2048)) {
+        return dtype == kBF16 ? launch_row_norm_vec_dt<kBF16>(x, gamma, beta, y, n, c, eps, silu, s)
+                              : launch_row_norm_vec_dt<kF16>(x, gamma, beta, y, n, c, eps, silu, s);
+    }
     const int64_t g = (n + 3) / 4;
     switch (dtype) {
         case kF32:
