@@ -535,7 +535,7 @@ trellis_status op_add(trellis_sparse_backend * backend, const trellis_sparse_buf
 void rulebook_release(Backend * be, trellis_sparse_rulebook * r) {
     if (r == nullptr) return;
     DevMem * mems[] = {&r->coords_mem, &r->bkeys, &r->bidx, &r->pool, &r->counters, &r->nbr, &r->mask,
-                       &r->tile_counts, &r->tile_off, &r->k_count, &r->scan_tmp, &r->pair_src, &r->pair_dst};
+                       &r->tile_counts, &r->tile_off, &r->pair_src, &r->pair_dst};
     for (DevMem * m : mems) dev_release(be, m);
     delete r;
 }
@@ -565,10 +565,8 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
         {&r->mask, (size_t) n * 4},
         {&r->tile_counts, (size_t) r->n_tiles * 27 * 4},
         {&r->tile_off, (size_t) r->n_tiles * 27 * 4},
-        {&r->k_count, 27 * 4},
-        {&r->scan_tmp, scan_tmp_bytes(r->n_tiles * 27)},
-        {&r->pair_src, (size_t) n * 27 * 4},
-        {&r->pair_dst, (size_t) n * 27 * 4},
+        {&r->pair_src, (size_t) r->n_tiles * kMapTile * 27 * 4},
+        {&r->pair_dst, (size_t) r->n_tiles * kMapTile * 27 * 4},
     };
     for (const Need & q : need) {
         const trellis_status st = dev_alloc(be, q.bytes, q.m);
@@ -585,17 +583,13 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
                                     r->table_slots, (int32_t *) r->pool.ptr, (int32_t *) r->counters.ptr, s));
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_HASH);
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
-    TSH_TRY(be, launch_neighbors(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
+    // One pass: neighbours, per-tile counts and list starts, and each tile's
+    // pair lists in its fixed region (pair total into counters[2]).
+    TSH_TRY(be, launch_map_tiles(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
                                  r->table_slots, (const int32_t *) r->pool.ptr, (int32_t *) r->nbr.ptr,
-                                 (uint32_t *) r->mask.ptr, (int32_t *) r->tile_counts.ptr, s));
-    // Pairs are stored by tile, then offset: list starts = exclusive scan of
-    // the flattened [n_tiles][27] counts (total into counters[2]).
-    TSH_TRY(be, launch_scan_exclusive((const int32_t *) r->tile_counts.ptr, (int32_t *) r->tile_off.ptr,
-                                      r->n_tiles * 27, (int32_t *) r->counters.ptr + 2, r->scan_tmp.ptr, s));
-    TSH_TRY(be, launch_offset_totals((const int32_t *) r->tile_counts.ptr, r->n_tiles, (int32_t *) r->k_count.ptr, s));
-    TSH_TRY(be, launch_fill_pairs((const int32_t *) r->nbr.ptr, (const uint32_t *) r->mask.ptr, n,
-                                  (const int32_t *) r->tile_off.ptr, (int32_t *) r->pair_src.ptr,
-                                  (int32_t *) r->pair_dst.ptr, s));
+                                 (uint32_t *) r->mask.ptr, (int32_t *) r->tile_counts.ptr, (int32_t *) r->tile_off.ptr,
+                                 (int32_t *) r->pair_src.ptr, (int32_t *) r->pair_dst.ptr,
+                                 (int32_t *) r->counters.ptr, s));
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
     if (be->policy.reject_duplicates) {
         int32_t flags[4] = {0, 0, 0, 0};
@@ -606,7 +600,8 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
     return TRELLIS_STATUS_OK;
 }
 
-bool n_ok(int64_t n) { return n > 0 && n <= (int64_t) (INT32_MAX / 27); }
+// Pair positions (tile regions of kMapTile * 27 entries) fit int32.
+bool n_ok(int64_t n) { return n > 0 && (n + kMapTile - 1) / kMapTile * kMapTile * 27 <= (int64_t) INT32_MAX; }
 
 trellis_status op_build_rulebook(trellis_sparse_backend * backend, const int32_t * coords_bxyz, int64_t n,
                                  trellis_sparse_rulebook ** out) {
@@ -1196,16 +1191,12 @@ trellis_status trellis_sparse_hip_rulebook_stats(trellis_sparse_backend * backen
     if (backend == nullptr || rulebook == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
     Backend * be = tsh::as_backend(backend);
     tsh::select_device(be);
-    int32_t counts[27];
     int32_t ctr[4];
-    hipError_t err = hipMemcpyAsync(counts, rulebook->k_count.ptr, sizeof(counts), hipMemcpyDeviceToHost, be->stream);
-    if (err == hipSuccess) err = hipMemcpyAsync(ctr, rulebook->counters.ptr, sizeof(ctr), hipMemcpyDeviceToHost, be->stream);
+    hipError_t err = hipMemcpyAsync(ctr, rulebook->counters.ptr, sizeof(ctr), hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
     if (err != hipSuccess) return tsh::hip_status(be, err, "rulebook_stats");
-    int64_t total = 0;
-    for (int k = 0; k < 27; ++k) total += counts[k];
     if (n != nullptr) *n = rulebook->n;
-    if (pairs != nullptr) *pairs = total;
+    if (pairs != nullptr) *pairs = ctr[2];
     if (table_slots != nullptr) *table_slots = rulebook->table_slots;
     if (bricks != nullptr) *bricks = ctr[0];
     return TRELLIS_STATUS_OK;
@@ -1230,28 +1221,31 @@ trellis_status trellis_sparse_hip_download_pairs(trellis_sparse_backend * backen
     if (backend == nullptr || rulebook == nullptr || counts_out == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
     Backend * be = tsh::as_backend(backend);
     tsh::select_device(be);
-    int32_t counts[27];
-    hipError_t err = hipMemcpyAsync(counts, rulebook->k_count.ptr, sizeof(counts), hipMemcpyDeviceToHost, be->stream);
+    // Per-offset totals are the column sums of the per-(tile, offset) counts.
+    const int64_t tiles = rulebook->n_tiles;
+    std::vector<int32_t> off((size_t) tiles * 27), cnt((size_t) tiles * 27);
+    hipError_t err =
+        hipMemcpyAsync(cnt.data(), rulebook->tile_counts.ptr, cnt.size() * 4, hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
     if (err != hipSuccess) return tsh::hip_status(be, err, "download_pairs");
     int64_t total = 0;
     for (int k = 0; k < 27; ++k) {
-        counts_out[k] = counts[k];
-        total += counts[k];
+        int64_t c = 0;
+        for (int64_t t = 0; t < tiles; ++t) c += cnt[(size_t) t * 27 + k];
+        counts_out[k] = c;
+        total += c;
     }
     if (src_out == nullptr && dst_out == nullptr) return TRELLIS_STATUS_OK;
     if (total > capacity) return tsh::fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "download_pairs: capacity too small");
     // The device lists are tile-major; reorder them to the canonical
     // offset-major order (destination ascending within an offset).
-    const int64_t tiles = rulebook->n_tiles;
-    std::vector<int32_t> off((size_t) tiles * 27), cnt((size_t) tiles * 27), hs((size_t) total), hd((size_t) total);
+    const size_t span = (size_t) tiles * tsh::kMapTile * 27;  // every tile's region
+    std::vector<int32_t> hs(span), hd(span);
     err = hipMemcpyAsync(off.data(), rulebook->tile_off.ptr, off.size() * 4, hipMemcpyDeviceToHost, be->stream);
-    if (err == hipSuccess)
-        err = hipMemcpyAsync(cnt.data(), rulebook->tile_counts.ptr, cnt.size() * 4, hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess && total > 0)
-        err = hipMemcpyAsync(hs.data(), rulebook->pair_src.ptr, (size_t) total * 4, hipMemcpyDeviceToHost, be->stream);
+        err = hipMemcpyAsync(hs.data(), rulebook->pair_src.ptr, span * 4, hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess && total > 0)
-        err = hipMemcpyAsync(hd.data(), rulebook->pair_dst.ptr, (size_t) total * 4, hipMemcpyDeviceToHost, be->stream);
+        err = hipMemcpyAsync(hd.data(), rulebook->pair_dst.ptr, span * 4, hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
     if (err != hipSuccess) return tsh::hip_status(be, err, "download_pairs");
     int64_t at = 0;

@@ -182,24 +182,35 @@ __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict
     }
 }
 
-// Neighbour table + mask + per-tile per-offset counts.  One block = one
-// 256-row tile; the tile's [256][27] table is staged in LDS and written out
-// as one contiguous, 16-byte-vectorised block.
-__global__ void __launch_bounds__(kBlock) k_neighbors(const int4 * __restrict__ coords, int64_t n,
+// Kernel map in one pass.  One block = one 256-row tile:
+//  1. the tile's [256][27] neighbour rows are found and staged in LDS (a few
+//     brick probes per voxel plus 27 pool reads), with the row masks;
+//  2. per-offset pair counts of the tile (wavefront ballots);
+//  3. the neighbour table (16-byte vectorised copy of the LDS block), the
+//     per-(tile, offset) counts and list starts, and the pair lists,
+//     destination ascending within each (tile, offset).
+// Tile t owns the fixed region [t * 256 * 27, (t + 1) * 256 * 27) of the
+// pair arrays (the most pairs 256 rows can have), so no tile waits for the
+// counts of the tiles before it; the lists of a tile are packed from the
+// region's start, offsets in order.
+__global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ coords, int64_t n,
                                                       const uint64_t * __restrict__ bkeys,
                                                       const int32_t * __restrict__ bidx, uint64_t hmask,
                                                       const int32_t * __restrict__ pool, int32_t * __restrict__ nbr,
                                                       uint32_t * __restrict__ mask_out,
-                                                      int32_t * __restrict__ tile_counts) {
-    __shared__ int32_t s_nbr[kBlock * 27];
-    __shared__ int32_t s_cnt[27];
+                                                      int32_t * __restrict__ tile_counts,
+                                                      int32_t * __restrict__ tile_off,
+                                                      int32_t * __restrict__ pair_src,
+                                                      int32_t * __restrict__ pair_dst, int32_t * __restrict__ counters) {
+    __shared__ __attribute__((aligned(16))) int32_t s_nbr[kBlock * 27];
+    __shared__ int32_t s_wave_cnt[27][kBlock / 64];
+    __shared__ int32_t s_koff[27];
     const int t = threadIdx.x;
+    const int lane = lane_id();
+    const int wave = t >> 6;
     const int64_t tile = blockIdx.x;
     const int64_t row0 = tile * kBlock;
     const int64_t i = row0 + t;
-    if (t < 27) {
-        s_cnt[t] = 0;
-    }
     uint32_t m = 0;
     if (i < n) {
         const int4 c = coords[i];
@@ -251,16 +262,38 @@ __global__ void __launch_bounds__(kBlock) k_neighbors(const int4 * __restrict__ 
         }
         mask_out[i] = m;
     }
-    __syncthreads();
-    const int lane = lane_id();
+    // Rank of this row among the tile's rows with a neighbour at k, per wavefront.
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int32_t rank[27];
 #pragma unroll
     for (int k = 0; k < 27; ++k) {
         const uint64_t bal = __ballot((m >> k) & 1u);
-        if (lane == 0 && bal != 0) {
-            atomicAdd(&s_cnt[k], __popcll(bal));
-        }
+        rank[k] = __popcll(bal & lt);
+        if (lane == 0) s_wave_cnt[k][wave] = __popcll(bal);
     }
-    // Coalesced copy of the tile's table.
+    __syncthreads();
+    if (t < 64) {
+        // Tile counts per offset (lanes 0..26), their exclusive scan, the total.
+        int32_t cnt = 0;
+        if (t < 27) {
+#pragma unroll
+            for (int w = 0; w < kBlock / 64; ++w) cnt += s_wave_cnt[t][w];
+            tile_counts[tile * 27 + t] = cnt;
+        }
+        int32_t incl = cnt;
+#pragma unroll
+        for (int d = 1; d < 32; d <<= 1) {
+            const int32_t o = __shfl_up(incl, d);
+            if (lane >= d) incl += o;
+        }
+        if (t < 27) s_koff[t] = incl - cnt;
+        const int32_t total = __shfl(incl, 26);
+        if (t == 0) atomicAdd(&counters[2], total);
+    }
+    __syncthreads();
+    const int64_t base = tile * kBlock * 27;
+    if (t < 27) tile_off[tile * 27 + t] = (int32_t) (base + s_koff[t]);
+    // Coalesced copy of the tile's neighbour table.
     const int64_t rows = (n - row0) < kBlock ? (n - row0) : kBlock;
     const int64_t words = rows * 27;
     int32_t * dst = nbr + row0 * 27;
@@ -273,81 +306,12 @@ __global__ void __launch_bounds__(kBlock) k_neighbors(const int4 * __restrict__ 
             dst[w] = s_nbr[w];
         }
     }
-    __syncthreads();
-    if (t < 27) {
-        tile_counts[tile * 27 + t] = s_cnt[t];
-    }
-}
-
-// Per-offset pair totals: block k sums column k of tile_counts [n_tiles][27].
-// (The list starts themselves are an exclusive scan of the flattened
-// tile_counts, since the pair arrays are ordered by tile, then offset.)
-__global__ void __launch_bounds__(kBlock) k_offset_totals(const int32_t * __restrict__ tile_counts, int64_t n_tiles,
-                                                          int32_t * __restrict__ k_count) {
-    __shared__ int32_t s_wave[kBlock / 64];
-    const int k = blockIdx.x;
-    int32_t v = 0;
-    for (int64_t t = threadIdx.x; t < n_tiles; t += kBlock) v += tile_counts[t * 27 + k];
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
-    if (lane_id() == 0) s_wave[threadIdx.x >> 6] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int32_t total = 0;
-#pragma unroll
-        for (int w = 0; w < kBlock / 64; ++w) total += s_wave[w];
-        k_count[k] = total;
-    }
-}
-
-// Compacted pair lists in tile-major order, destination ascending within each (tile, offset).
-__global__ void __launch_bounds__(kBlock) k_fill_pairs(const int32_t * __restrict__ nbr,
-                                                       const uint32_t * __restrict__ mask, int64_t n,
-                                                       const int32_t * __restrict__ tile_off,
-                                                       int32_t * __restrict__ pair_src,
-                                                       int32_t * __restrict__ pair_dst) {
-    __shared__ int32_t s_wave_cnt[27][kBlock / 64];
-    __shared__ __attribute__((aligned(16))) int32_t s_nbr[kBlock * 27];
-    const int t = threadIdx.x;
-    const int lane = lane_id();
-    const int wave = t >> 6;
-    const int64_t tile = blockIdx.x;
-    const int64_t i = tile * kBlock + t;
-    const uint32_t m = i < n ? mask[i] : 0u;
-    // The tile's neighbour rows are contiguous: stage them with coalesced
-    // 16-byte loads (a thread's own row is 108 bytes, so direct per-offset
-    // reads would stride across the wavefront).
-    {
-        const int64_t first = tile * kBlock * 27;
-        const int64_t end = n * 27;
-        const int count = (int) ((end - first) < kBlock * 27 ? (end - first) : kBlock * 27);
-        const int32_t * src = nbr + first;
-        const int vec = count / 4;  // first is a multiple of 4 (kBlock * 27 is)
-        for (int v = t; v < vec; v += kBlock) *(int4 *) &s_nbr[v * 4] = *(const int4 *) (src + v * 4);
-        for (int e = vec * 4 + t; e < count; e += kBlock) s_nbr[e] = src[e];
-    }
-    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int32_t rank[27];
-#pragma unroll
-    for (int k = 0; k < 27; ++k) {
-        const uint64_t bal = __ballot((m >> k) & 1u);
-        rank[k] = __popcll(bal & lt);
-        if (lane == 0) {
-            s_wave_cnt[k][wave] = __popcll(bal);
-        }
-    }
-    __syncthreads();
-    if (i >= n || m == 0) {
-        return;
-    }
+    if (i >= n || m == 0) return;
 #pragma unroll
     for (int k = 0; k < 27; ++k) {
         if ((m >> k) & 1u) {
-            int32_t base = tile_off[tile * 27 + k];
-            for (int w = 0; w < wave; ++w) {
-                base += s_wave_cnt[k][w];
-            }
-            const int64_t pos = (int64_t) base + rank[k];
+            int64_t pos = base + s_koff[k] + rank[k];
+            for (int w = 0; w < wave; ++w) pos += s_wave_cnt[k][w];
             pair_src[pos] = s_nbr[t * 27 + k];
             pair_dst[pos] = (int32_t) i;
         }
@@ -396,24 +360,14 @@ hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t
     return hipGetLastError();
 }
 
-hipError_t launch_neighbors(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
+hipError_t launch_map_tiles(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
                             int64_t slots, const int32_t * pool, int32_t * nbr, uint32_t * mask,
-                            int32_t * tile_counts, hipStream_t s) {
+                            int32_t * tile_counts, int32_t * tile_off, int32_t * pair_src, int32_t * pair_dst,
+                            int32_t * counters, hipStream_t s) {
     const int64_t blocks = (n + kBlock - 1) / kBlock;
-    k_neighbors<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx, (uint64_t) (slots - 1),
-                                                     pool, nbr, mask, tile_counts);
-    return hipGetLastError();
-}
-
-hipError_t launch_offset_totals(const int32_t * tile_counts, int64_t n_tiles, int32_t * k_count, hipStream_t s) {
-    k_offset_totals<<<27, kBlock, 0, s>>>(tile_counts, n_tiles, k_count);
-    return hipGetLastError();
-}
-
-hipError_t launch_fill_pairs(const int32_t * nbr, const uint32_t * mask, int64_t n, const int32_t * tile_off,
-                             int32_t * pair_src, int32_t * pair_dst, hipStream_t s) {
-    const int64_t blocks = (n + kBlock - 1) / kBlock;
-    k_fill_pairs<<<(unsigned) blocks, kBlock, 0, s>>>(nbr, mask, n, tile_off, pair_src, pair_dst);
+    k_map_tiles<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx, (uint64_t) (slots - 1),
+                                                     pool, nbr, mask, tile_counts, tile_off, pair_src, pair_dst,
+                                                     counters);
     return hipGetLastError();
 }
 

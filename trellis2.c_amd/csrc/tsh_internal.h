@@ -90,10 +90,8 @@ struct trellis_sparse_rulebook {
     int64_t n_tiles;         // ceil(n / kMapTile)
     tsh::DevMem tile_counts; // int32  [n_tiles][27]
     tsh::DevMem tile_off;    // int32  [n_tiles][27] start of (tile, k) in the pair arrays
-    tsh::DevMem k_count;     // int32  [27]
-    tsh::DevMem scan_tmp;    // scratch of the tile_off scan
-    tsh::DevMem pair_src;    // int32  [P] tile-major: tiles ascending, then k, then dst ascending
-    tsh::DevMem pair_dst;    // int32  [P]
+    tsh::DevMem pair_src;    // int32  [n_tiles][kMapTile * 27]: per tile, offsets ascending, dst ascending
+    tsh::DevMem pair_dst;    // int32  [n_tiles][kMapTile * 27]
 };
 
 struct trellis_sparse_c2s_device_map {
@@ -119,14 +117,14 @@ hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bke
 hipError_t launch_pool_init(int32_t * pool, const int32_t * counters, int64_t cap_cells, hipStream_t s);
 hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
                                int64_t slots, int32_t * pool, int32_t * counters, hipStream_t s);
-hipError_t launch_neighbors(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
+// Neighbour table, masks, per-(tile, offset) counts and list starts, and the
+// pair lists in one pass.  Tile t's lists fill the start of its region
+// [t * kMapTile * 27, (t + 1) * kMapTile * 27) of the pair arrays; the pair
+// total is added to counters[2] (which must start at zero).
+hipError_t launch_map_tiles(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
                             int64_t slots, const int32_t * pool, int32_t * nbr, uint32_t * mask,
-                            int32_t * tile_counts, hipStream_t s);
-// Column sums of tile_counts [n_tiles][27] -> k_count[27].  (tile_off is the
-// exclusive scan of the flattened tile_counts: launch_scan_exclusive.)
-hipError_t launch_offset_totals(const int32_t * tile_counts, int64_t n_tiles, int32_t * k_count, hipStream_t s);
-hipError_t launch_fill_pairs(const int32_t * nbr, const uint32_t * mask, int64_t n, const int32_t * tile_off,
-                             int32_t * pair_src, int32_t * pair_dst, hipStream_t s);
+                            int32_t * tile_counts, int32_t * tile_off, int32_t * pair_src, int32_t * pair_dst,
+                            int32_t * counters, hipStream_t s);
 
 // Convolution (kernels_conv.hip).  Weight layouts are produced by the backend.
 //  generic: w32 fp32 [27][ci][co]
