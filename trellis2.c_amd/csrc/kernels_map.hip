@@ -119,7 +119,7 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
             s = (s + 1) & mask;
         }
         if (step > mask) {
-            atomicOr(&counters[2], 1);  // table full; cannot happen with slots >= 2n
+            atomicOr(&counters[4], 1);  // table full; cannot happen with slots >= 2n
         }
     }
     // Number the new bricks with one global atomic per block: wave ballots give
@@ -172,7 +172,7 @@ __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict
     const uint32_t x = (uint32_t) c.y & 0xffffu, y = (uint32_t) c.z & 0xffffu, z = (uint32_t) c.w & 0xffffu;
     const int32_t b = brick_find(bkeys, bidx, mask, brick_key((uint32_t) c.x & 0xffffu, x >> 2, y >> 2, z >> 2));
     if (b < 0) {
-        atomicOr(&counters[2], 2);  // unreachable: every voxel's brick was inserted
+        atomicOr(&counters[4], 2);  // unreachable: every voxel's brick was inserted
         return;
     }
     const uint32_t cell = (x & 3u) | ((y & 3u) << 2) | ((z & 3u) << 4);

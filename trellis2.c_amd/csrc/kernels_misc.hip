@@ -277,6 +277,8 @@ __global__ void k_c2s_gather(const typename Store<DT>::T * __restrict__ x, const
     }
 }
 
+constexpr int kIlp = 4;  // chunks per thread and pass in the vectorised broadcasts
+
 // 16-byte chunks with 32-bit indexing, as k_skip_repeat_vec.
 template <int DT>
 __global__ void __launch_bounds__(256) k_c2s_gather_vec(const typename Store<DT>::T * __restrict__ x,
@@ -286,11 +288,25 @@ __global__ void __launch_bounds__(256) k_c2s_gather_vec(const typename Store<DT>
                                                         int vpr, int vshift) {
     constexpr int kVec = 16 / (int) sizeof(typename Store<DT>::T);
     const int total = n_out * vpr;
-    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
-        const int r = vshift >= 0 ? e >> vshift : e / vpr;
-        const int c0 = (e - r * vpr) * kVec;
-        const int64_t from = ((int64_t) parent[r] * 8 + subidx[r]) * co + c0;
-        *(int4 *) (y + (int64_t) r * co + c0) = *(const int4 *) (x + from);
+    const int S = gridDim.x * blockDim.x;
+    for (int e0 = blockIdx.x * blockDim.x + threadIdx.x; e0 < total; e0 += kIlp * S) {
+        int r[kIlp], c0[kIlp];
+        int64_t from[kIlp];
+#pragma unroll
+        for (int u = 0; u < kIlp; ++u) {
+            const int e = e0 + u * S < total ? e0 + u * S : e0;
+            r[u] = vshift >= 0 ? e >> vshift : e / vpr;
+            c0[u] = (e - r[u] * vpr) * kVec;
+        }
+#pragma unroll
+        for (int u = 0; u < kIlp; ++u) from[u] = ((int64_t) parent[r[u]] * 8 + subidx[r[u]]) * co + c0[u];
+        int4 v[kIlp];
+#pragma unroll
+        for (int u = 0; u < kIlp; ++u) v[u] = *(const int4 *) (x + from[u]);
+#pragma unroll
+        for (int u = 0; u < kIlp; ++u) {
+            if (e0 + u * S < total) *(int4 *) (y + (int64_t) r[u] * co + c0[u]) = v[u];
+        }
     }
 }
 
@@ -307,49 +323,69 @@ __global__ void k_skip_repeat(const typename Store<DT>::T * __restrict__ x, cons
     }
 }
 
-// 16-byte output chunks, 32-bit indexing (n_out * co / kVec < 2^31).  The
-// chunks of a row are consecutive threads: row = e >> vshift when the chunk
-// count per row is a power of two (vshift >= 0), else e / vpr.  kSingle: the
-// repeat count is a multiple of the chunk width, so one source element fills
-// the whole chunk (repeat-interleave of 8 or more).
+// 16-byte output chunks, 32-bit indexing (n_out * co / kVec + kIlp * grid <
+// 2^31).  The chunks of a row are consecutive threads: row = e >> vshift when
+// the chunk count per row is a power of two (vshift >= 0), else e / vpr.
+// Each thread takes kIlp chunks a grid apart with their loads issued
+// together, so a row lookup, its source load and the store overlap across
+// them instead of running back to back.  kSingle: the repeat count is a
+// multiple of the chunk width, so one source element fills the whole chunk
+// (repeat-interleave of 8 or more); rshift >= 0: the repeat count is 2^rshift.
 template <int DT, bool kSingle>
 __global__ void __launch_bounds__(256) k_skip_repeat_vec(const typename Store<DT>::T * __restrict__ x,
                                                          const int32_t * __restrict__ parent,
                                                          const int32_t * __restrict__ subidx,
                                                          typename Store<DT>::T * __restrict__ y, int n_out, int ci,
-                                                         int co, int repeat, int vpr, int vshift) {
+                                                         int co, int repeat, int rshift, int vpr, int vshift) {
     using T = typename Store<DT>::T;
     constexpr int kVec = 16 / (int) sizeof(T);
     const int total = n_out * vpr;
-    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
-        const int r = vshift >= 0 ? e >> vshift : e / vpr;
-        const int c0 = (e - r * vpr) * kVec;
-        const T * xr = x + (int64_t) parent[r] * ci;
-        const int first = subidx[r] * co + c0;
-        union {
-            int4 v;
-            T e[kVec];
-        } out;
-        if constexpr (kSingle) {
-            int from = first / repeat;
-            from = from < ci - 1 ? from : ci - 1;
-            const T v = xr[from];
+    const int S = gridDim.x * blockDim.x;
+    union Chunk {
+        int4 v;
+        T e[kVec];
+    };
+    for (int e0 = blockIdx.x * blockDim.x + threadIdx.x; e0 < total; e0 += kIlp * S) {
+        int r[kIlp], c0[kIlp];
 #pragma unroll
-            for (int q = 0; q < kVec; ++q) out.e[q] = v;
-        } else {
-            // One division per chunk; step the quotient/remainder across it.
-            int from = first / repeat;
-            int rem = first - from * repeat;
+        for (int u = 0; u < kIlp; ++u) {
+            const int e = e0 + u * S < total ? e0 + u * S : e0;
+            r[u] = vshift >= 0 ? e >> vshift : e / vpr;
+            c0[u] = (e - r[u] * vpr) * kVec;
+        }
+        const T * xr[kIlp];
+        int first[kIlp];
 #pragma unroll
-            for (int q = 0; q < kVec; ++q) {
-                out.e[q] = xr[from < ci - 1 ? from : ci - 1];
-                if (++rem == repeat) {
-                    rem = 0;
-                    ++from;
+        for (int u = 0; u < kIlp; ++u) {
+            xr[u] = x + (int64_t) parent[r[u]] * ci;
+            first[u] = subidx[r[u]] * co + c0[u];
+        }
+        Chunk out[kIlp];
+#pragma unroll
+        for (int u = 0; u < kIlp; ++u) {
+            int from = rshift >= 0 ? first[u] >> rshift : first[u] / repeat;
+            if constexpr (kSingle) {
+                from = from < ci - 1 ? from : ci - 1;
+                const T v = xr[u][from];
+#pragma unroll
+                for (int q = 0; q < kVec; ++q) out[u].e[q] = v;
+            } else {
+                // One division per chunk; step the quotient/remainder across it.
+                int rem = first[u] - from * repeat;
+#pragma unroll
+                for (int q = 0; q < kVec; ++q) {
+                    out[u].e[q] = xr[u][from < ci - 1 ? from : ci - 1];
+                    if (++rem == repeat) {
+                        rem = 0;
+                        ++from;
+                    }
                 }
             }
         }
-        *(int4 *) (y + (int64_t) r * co + c0) = out.v;
+#pragma unroll
+        for (int u = 0; u < kIlp; ++u) {
+            if (e0 + u * S < total) *(int4 *) (y + (int64_t) r[u] * co + c0[u]) = out[u].v;
+        }
     }
 }
 
@@ -595,13 +631,13 @@ hipError_t launch_c2s_fill(int dtype, const int32_t * coords, const void * logit
 hipError_t launch_c2s_gather(int dtype, const void * x, const int32_t * parent, const int32_t * subidx, void * y,
                              int64_t n_out, int co, hipStream_t s) {
     const int kvec = 16 / (int) dtype_bytes(dtype);
-    if (co % kvec == 0 && n_out * (co / kvec) < (int64_t) INT32_MAX - 65536 * 256) {
+    if (co % kvec == 0 && n_out * (co / kvec) < (int64_t) INT32_MAX - (int64_t) kIlp * 65536 * 256) {
         const int vpr = co / kvec;
         int vshift = -1;
         for (int b = 0; b < 30; ++b) {
             if ((1 << b) == vpr) vshift = b;
         }
-        const int gv = blocks_for(n_out * vpr, 256, 65536);
+        const int gv = blocks_for((n_out * vpr + kIlp - 1) / kIlp, 256, 65536);
         switch (dtype) {
             case kF32:
                 k_c2s_gather_vec<kF32><<<gv, 256, 0, s>>>((const float *) x, parent, subidx, (float *) y, (int) n_out,
@@ -637,22 +673,23 @@ hipError_t launch_skip_repeat(int dtype, const void * x, const int32_t * parent,
                               int64_t n_out, int ci, int co, hipStream_t s) {
     const int repeat = (8 * co + ci - 1) / ci;
     const int kvec = 16 / (int) dtype_bytes(dtype);
-    if (co % kvec == 0 && n_out * (co / kvec) < (int64_t) INT32_MAX - 65536 * 256) {
+    if (co % kvec == 0 && n_out * (co / kvec) < (int64_t) INT32_MAX - (int64_t) kIlp * 65536 * 256) {
         const int vpr = co / kvec;
-        int vshift = -1;
+        int vshift = -1, rshift = -1;
         for (int b = 0; b < 30; ++b) {
             if ((1 << b) == vpr) vshift = b;
+            if ((1 << b) == repeat) rshift = b;
         }
-        const int g = blocks_for(n_out * vpr, 256, 65536);
+        const int g = blocks_for((n_out * vpr + kIlp - 1) / kIlp, 256, 65536);
         const bool single = repeat % kvec == 0;
 #define TSH_SR(DTV, TYPE)                                                                                       \
     do {                                                                                                        \
         if (single) {                                                                                           \
             k_skip_repeat_vec<DTV, true><<<g, 256, 0, s>>>((const TYPE *) x, parent, subidx, (TYPE *) y,         \
-                                                           (int) n_out, ci, co, repeat, vpr, vshift);            \
+                                                           (int) n_out, ci, co, repeat, rshift, vpr, vshift);    \
         } else {                                                                                                \
             k_skip_repeat_vec<DTV, false><<<g, 256, 0, s>>>((const TYPE *) x, parent, subidx, (TYPE *) y,        \
-                                                            (int) n_out, ci, co, repeat, vpr, vshift);           \
+                                                            (int) n_out, ci, co, repeat, rshift, vpr, vshift);   \
         }                                                                                                       \
     } while (0)
         switch (dtype) {

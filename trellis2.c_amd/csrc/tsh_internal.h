@@ -83,7 +83,7 @@ struct trellis_sparse_rulebook {
     tsh::DevMem bkeys;       // uint64 [table_slots]
     tsh::DevMem bidx;        // int32  [table_slots]
     tsh::DevMem pool;        // int32  [cap_bricks][64] voxel rows, -1 = empty
-    tsh::DevMem counters;    // int32  [16]: bricks, duplicate flag, pair total, (reserved)
+    tsh::DevMem counters;    // int32  [16]: bricks, duplicate flag, pair total, (reserved), internal-error flags
     // Kernel map.
     tsh::DevMem nbr;         // int32  [n][27]
     tsh::DevMem mask;        // uint32 [n] bit k set when nbr[i][k] >= 0
