@@ -559,8 +559,8 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
     } need[] = {
         {&r->bkeys, slots * 8},
         {&r->bidx, slots * 4},
-        {&r->pool, (size_t) n * kBrickCells * 4},
-        {&r->counters, 64},
+        {&r->pool, (size_t) (kBrickGroups * brick_group_cap(n)) * kBrickCells * 4},
+        {&r->counters, kCounterInts * 4},
         {&r->nbr, (size_t) n * 27 * 4},
         {&r->mask, (size_t) n * 4},
         {&r->tile_counts, (size_t) r->n_tiles * 27 * 4},
@@ -575,16 +575,16 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
     hipStream_t s = be->stream;
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_HASH);
     TSH_TRY(be, launch_fill_u64((uint64_t *) r->bkeys.ptr, r->table_slots, 0ull, s));
-    TSH_TRY(be, launch_fill_i32((int32_t *) r->counters.ptr, 16, 0, s));
+    TSH_TRY(be, launch_fill_i32((int32_t *) r->counters.ptr, kCounterInts, 0, s));
     TSH_TRY(be, launch_brick_insert(coords, n, (uint64_t *) r->bkeys.ptr, (int32_t *) r->bidx.ptr, r->table_slots,
                                     (int32_t *) r->counters.ptr, s));
-    TSH_TRY(be, launch_pool_init((int32_t *) r->pool.ptr, (const int32_t *) r->counters.ptr, n * kBrickCells, s));
+    TSH_TRY(be, launch_pool_init((int32_t *) r->pool.ptr, (const int32_t *) r->counters.ptr, n, s));
     TSH_TRY(be, launch_voxel_insert(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
                                     r->table_slots, (int32_t *) r->pool.ptr, (int32_t *) r->counters.ptr, s));
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_HASH);
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
     // One pass: neighbours, per-tile counts and list starts, and each tile's
-    // pair lists in its fixed region (pair total into counters[2]).
+    // pair lists in its fixed region.
     TSH_TRY(be, launch_map_tiles(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
                                  r->table_slots, (const int32_t *) r->pool.ptr, (int32_t *) r->nbr.ptr,
                                  (uint32_t *) r->mask.ptr, (int32_t *) r->tile_counts.ptr, (int32_t *) r->tile_off.ptr,
@@ -1191,14 +1191,21 @@ trellis_status trellis_sparse_hip_rulebook_stats(trellis_sparse_backend * backen
     if (backend == nullptr || rulebook == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
     Backend * be = tsh::as_backend(backend);
     tsh::select_device(be);
-    int32_t ctr[4];
+    int32_t ctr[tsh::kCounterInts];
+    std::vector<int32_t> cnt((size_t) rulebook->n_tiles * 27);
     hipError_t err = hipMemcpyAsync(ctr, rulebook->counters.ptr, sizeof(ctr), hipMemcpyDeviceToHost, be->stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(cnt.data(), rulebook->tile_counts.ptr, cnt.size() * 4, hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
     if (err != hipSuccess) return tsh::hip_status(be, err, "rulebook_stats");
+    int64_t total = 0;
+    for (const int32_t c : cnt) total += c;
+    int64_t nb = 0;
+    for (int g = 0; g < tsh::kBrickGroups; ++g) nb += ctr[tsh::kBrickCounter + g];
     if (n != nullptr) *n = rulebook->n;
-    if (pairs != nullptr) *pairs = ctr[2];
+    if (pairs != nullptr) *pairs = total;
     if (table_slots != nullptr) *table_slots = rulebook->table_slots;
-    if (bricks != nullptr) *bricks = ctr[0];
+    if (bricks != nullptr) *bricks = nb;
     return TRELLIS_STATUS_OK;
 }
 

@@ -80,7 +80,8 @@ __global__ void k_fill_i32(int32_t * __restrict__ p, int64_t count, int32_t valu
 // slot numbers the brick.
 __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict__ coords, int64_t n,
                                                          uint64_t * __restrict__ bkeys, int32_t * __restrict__ bidx,
-                                                         uint64_t mask, int32_t * __restrict__ counters) {
+                                                         uint64_t mask, int32_t * __restrict__ counters,
+                                                         int32_t group_cap) {
     const int64_t i = (int64_t) blockIdx.x * kBlock + threadIdx.x;
     const bool active = i < n;
     uint64_t key = 0;
@@ -134,9 +135,13 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
     }
     __syncthreads();
     if (threadIdx.x == 0) {
+        // Block b numbers its bricks in group b % kBrickGroups, whose counter
+        // few other blocks share; the group's range holds one brick per voxel
+        // of its blocks.
         int32_t total = 0;
         for (int w = 0; w < kBlock / 64; ++w) total += s_wave_new[w];
-        s_base = total > 0 ? atomicAdd(&counters[0], total) : 0;
+        const int g = blockIdx.x % kBrickGroups;
+        s_base = total > 0 ? g * group_cap + atomicAdd(&counters[kBrickCounter + g], total) : 0;
     }
     __syncthreads();
     if (won) {
@@ -146,15 +151,17 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
     }
 }
 
-// Clears the pool cells of the bricks numbered so far (count read on device).
-__global__ void k_pool_init(int32_t * __restrict__ pool, const int32_t * __restrict__ counters, int64_t cap_cells) {
-    int64_t cells = (int64_t) counters[0] * kBrickCells;
-    if (cells > cap_cells) {
-        cells = cap_cells;
-    }
+// Clears the pool cells of the bricks numbered so far (counts read on
+// device); blockIdx.y = brick group.
+__global__ void k_pool_init(int32_t * __restrict__ pool, const int32_t * __restrict__ counters, int32_t group_cap) {
+    const int g = blockIdx.y;
+    int32_t bricks = counters[kBrickCounter + g];
+    bricks = bricks < group_cap ? bricks : group_cap;
+    int32_t * gp = pool + (int64_t) g * group_cap * kBrickCells;
+    const int64_t cells = (int64_t) bricks * kBrickCells;
     const int64_t stride = (int64_t) gridDim.x * blockDim.x * 4;
     for (int64_t i = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) * 4; i < cells; i += stride) {
-        *(int4 *) (pool + i) = make_int4(-1, -1, -1, -1);
+        *(int4 *) (gp + i) = make_int4(-1, -1, -1, -1);
     }
 }
 
@@ -287,8 +294,6 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
             if (lane >= d) incl += o;
         }
         if (t < 27) s_koff[t] = incl - cnt;
-        const int32_t total = __shfl(incl, 26);
-        if (t == 0) atomicAdd(&counters[2], total);
     }
     __syncthreads();
     const int64_t base = tile * kBlock * 27;
@@ -339,16 +344,21 @@ hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_
     return hipGetLastError();
 }
 
+int64_t brick_group_cap(int64_t n) { return ((n + kBlock - 1) / kBlock + kBrickGroups - 1) / kBrickGroups * kBlock; }
+
 hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx, int64_t slots,
                                int32_t * counters, hipStream_t s) {
     const int64_t blocks = (n + kBlock - 1) / kBlock;
     k_brick_insert<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
-                                                        (uint64_t) (slots - 1), counters);
+                                                        (uint64_t) (slots - 1), counters,
+                                                        (int32_t) brick_group_cap(n));
     return hipGetLastError();
 }
 
-hipError_t launch_pool_init(int32_t * pool, const int32_t * counters, int64_t cap_cells, hipStream_t s) {
-    k_pool_init<<<grid_for(cap_cells / 4, 256, 8192), 256, 0, s>>>(pool, counters, cap_cells);
+hipError_t launch_pool_init(int32_t * pool, const int32_t * counters, int64_t n, hipStream_t s) {
+    const int64_t cap = brick_group_cap(n);
+    const dim3 grid((unsigned) grid_for(cap * kBrickCells / 4, 256, 256), kBrickGroups);
+    k_pool_init<<<grid, 256, 0, s>>>(pool, counters, (int32_t) cap);
     return hipGetLastError();
 }
 

@@ -54,6 +54,11 @@ template <> struct Store<kBF16> {
 // Work split of a rulebook build / conv: rows per tile of the kernel map.
 constexpr int kMapTile = 256;
 constexpr int kBrickCells = 64;  // 4x4x4 cells per brick
+// Bricks are numbered in kBrickGroups groups (counters[kBrickCounter + g]);
+// group g owns bricks [g * cap, (g + 1) * cap), cap = brick_group_cap(n).
+constexpr int kBrickGroups = 64;
+constexpr int kBrickCounter = 64;
+constexpr int kCounterInts = kBrickCounter + kBrickGroups;
 
 struct Backend;
 
@@ -83,7 +88,7 @@ struct trellis_sparse_rulebook {
     tsh::DevMem bkeys;       // uint64 [table_slots]
     tsh::DevMem bidx;        // int32  [table_slots]
     tsh::DevMem pool;        // int32  [cap_bricks][64] voxel rows, -1 = empty
-    tsh::DevMem counters;    // int32  [16]: bricks, duplicate flag, pair total, (reserved), internal-error flags
+    tsh::DevMem counters;    // int32  [kCounterInts]: [1] duplicate flag, [4] internal-error flags, [64..] brick groups
     // Kernel map.
     tsh::DevMem nbr;         // int32  [n][27]
     tsh::DevMem mask;        // uint32 [n] bit k set when nbr[i][k] >= 0
@@ -114,13 +119,14 @@ hipError_t launch_fill_u64(uint64_t * p, int64_t count, uint64_t value, hipStrea
 hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_t s);
 hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx,
                                int64_t slots, int32_t * counters, hipStream_t s);
-hipError_t launch_pool_init(int32_t * pool, const int32_t * counters, int64_t cap_cells, hipStream_t s);
+// Bricks per group for n voxels (pool capacity = kBrickGroups * that).
+int64_t brick_group_cap(int64_t n);
+hipError_t launch_pool_init(int32_t * pool, const int32_t * counters, int64_t n, hipStream_t s);
 hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
                                int64_t slots, int32_t * pool, int32_t * counters, hipStream_t s);
 // Neighbour table, masks, per-(tile, offset) counts and list starts, and the
 // pair lists in one pass.  Tile t's lists fill the start of its region
-// [t * kMapTile * 27, (t + 1) * kMapTile * 27) of the pair arrays; the pair
-// total is added to counters[2] (which must start at zero).
+// [t * kMapTile * 27, (t + 1) * kMapTile * 27) of the pair arrays.
 hipError_t launch_map_tiles(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
                             int64_t slots, const int32_t * pool, int32_t * nbr, uint32_t * mask,
                             int32_t * tile_counts, int32_t * tile_off, int32_t * pair_src, int32_t * pair_dst,
