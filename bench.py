@@ -140,6 +140,8 @@ class Block:
     convnext: on the ~1.26M config-3 children, C = 128:
       conv(128->128) -> row_norm -> linear_silu(128->512) -> linear(512->128) -> add
       (src/architectures/sparse_unet_decoder/executor.c:176-255).
+    convnext_fused: the same block with its tail (row_norm .. add) in the one
+      fused entry point trellis_sparse_hip_convnext_mlp.
     c2s: the C2S up-block on the ~0.32M config-3 parents, Ci = 256 -> Co = 128:
       linear(256->8) logits -> build_c2s_map_device -> build_rulebook_for_c2s_map;
       row_norm_silu -> conv(256->1024) on the parents -> c2s_gather_device;
@@ -153,7 +155,7 @@ class Block:
         w = wl.workload(3)
         rng = np.random.default_rng(11)
         f32 = lambda a: np.ascontiguousarray(a, np.float32)
-        if kind == "convnext":
+        if kind in ("convnext", "convnext_fused"):
             c = 128
             pmap = be.upload_coords(w["parent_coords"])
             dm = be.build_c2s_map_device(be.upload(w["logits"]), w["parent_coords"].shape[0], coords_map=pmap)
@@ -172,6 +174,8 @@ class Block:
             self.bufs = [be.alloc(self.n * c), be.alloc(self.n * c), be.alloc(self.n * 4 * c),
                          be.alloc(self.n * c), be.alloc(self.n * c)]
             self.slots = ["sparse_conv3d", "row_norm", "linear_silu", "linear", "add"]
+            if kind == "convnext_fused":
+                self.slots = ["sparse_conv3d", "convnext_mlp"]
         else:
             ci, co = 256, 128
             self.ci, self.co = ci, co
@@ -207,6 +211,14 @@ class Block:
         be = self.be
         ev = iter(range(1, 16))
         be.event(0)
+        if self.kind == "convnext_fused":
+            conv, out = self.bufs[0], self.bufs[4]
+            be.conv(self.rb, self.h, self.conv_w, self.conv_b, conv, self.c, self.c)
+            be.event(next(ev))
+            be.convnext_mlp(conv, self.gamma, self.beta, self.w0, self.b0, self.w2, self.b2, self.h, out, self.n,
+                            self.c, 1e-6)
+            be.event(next(ev))
+            return
         if self.kind == "convnext":
             n, c = self.n, self.c
             conv, norm, mlp1, mlp2, out = self.bufs
@@ -247,7 +259,7 @@ class Block:
         be.free_map(dm)
 
     def flops(self):
-        if self.kind == "convnext":
+        if self.kind in ("convnext", "convnext_fused"):
             n, c = self.n, self.c
             return wl.conv_flops(self.pairs, c, c) + 2 * (2 * n * c * 4 * c)
         return (wl.conv_flops(self.ppairs, self.ci, 8 * self.co) + wl.conv_flops(self.pairs, self.co, self.co)
@@ -274,7 +286,7 @@ def run_block(args):
            "steps": args.steps, "warmup": args.warmup, "ms_per_block": round(dev, 4),
            "wall_ms_per_block": round(wall, 4), "effective_tflops": round(job.flops() / (dev * 1e-3) / 1e12, 2),
            "slot_ms": slots}
-    if args.block == "convnext":
+    if args.block in ("convnext", "convnext_fused"):
         out.update({"voxels": int(job.n), "pairs": int(job.pairs), "channels": job.c})
     else:
         out.update({"parents": int(job.n), "children": int(job.m), "parent_pairs": int(job.ppairs),
@@ -343,7 +355,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-stride", type=int, default=16)
     ap.add_argument("--conv-algo", type=int, default=sh.CONV_AUTO)
-    ap.add_argument("--block", choices=["convnext", "c2s"],
+    ap.add_argument("--block", choices=["convnext", "convnext_fused", "c2s"],
                     help="instead of the configuration step, time one decoder block composed from the backend's "
                          "slots at config-3 scale and print its own JSON line")
     ap.add_argument("--calibrate", action="store_true",

@@ -272,6 +272,25 @@ trellis_status trellis_sparse_hip_free_c2s_map(trellis_sparse_backend * backend,
                                                trellis_sparse_c2s_device_map * map);
 
 /* ------------------------------------------------------------------------ */
+/* Fused ConvNeXt MLP tail (no counterpart in the reference vtable: it       */
+/* replaces the slot sequence row_norm -> linear_silu -> linear -> add of     */
+/* the decoder's ConvNeXt block, sparse_unet_decoder/executor.c:206-241).    */
+/* ------------------------------------------------------------------------ */
+
+/* y = residual + mlp2(SiLU(mlp0(row_norm(x, gamma, beta, eps)))), x, residual
+ * and y [n][c] in the backend's compute_dtype; mlp0_w fp32 [4c][c],
+ * mlp0_b [4c], mlp2_w fp32 [c][4c], mlp2_b [c] (biases, gamma and beta may be
+ * NULL).  Each intermediate is rounded to the storage type where the slot
+ * sequence stores it; the 4c-wide hidden rows never leave the chip.
+ * TRELLIS_STATUS_NOT_IMPLEMENTED unless compute_dtype is F16 or BF16 and
+ * c is 64 or 128; callers then run the slot sequence. */
+trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                               const float * gamma, const float * beta, const float * mlp0_w,
+                                               const float * mlp0_b, const float * mlp2_w, const float * mlp2_b,
+                                               const trellis_sparse_buffer * residual, trellis_sparse_buffer * y,
+                                               int64_t n, int c, float eps);
+
+/* ------------------------------------------------------------------------ */
 /* Stage timing with HIP events recorded on the backend's own stream.        */
 /* ------------------------------------------------------------------------ */
 typedef enum trellis_sparse_hip_stage {

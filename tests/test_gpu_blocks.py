@@ -117,6 +117,88 @@ def test_convnext_block_vs_oracle(backends, dtype, c):
     rb.free()
 
 
+def mlp_params(rng, c, dtype):
+    rnd = lambda a: sh.storage_round(a, dtype)
+    gamma = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    w0 = rnd(rng.standard_normal((4 * c, c)) / math.sqrt(c))
+    b0 = (0.1 * rng.standard_normal(4 * c)).astype(np.float32)
+    w2 = rnd(rng.standard_normal((c, 4 * c)) / math.sqrt(4 * c))
+    b2 = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    return gamma, beta, w0, b0, w2, b2
+
+
+@pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
+@pytest.mark.parametrize("c", [64, 128])
+@pytest.mark.parametrize("n", [1, 63, 65, 4099])
+def test_convnext_mlp_fused_vs_oracle(backends, dtype, c, n):
+    """The fused tail against the oracle's slot chain with the same storage
+    roundings (norm, hidden, second linear, add); rows past a tile edge and a
+    single row included."""
+    be = backends[dtype]
+    rnd = lambda a: sh.storage_round(a, dtype)
+    rng = np.random.default_rng(1000 * c + n + dtype)
+    say(f"convnext_mlp fused dtype={dtype} c={c} n={n}")
+    x = rnd(2 * rng.standard_normal((n, c)) + 0.5)
+    res = rnd(rng.standard_normal((n, c)))
+    gamma, beta, w0, b0, w2, b2 = mlp_params(rng, c, dtype)
+    xb, rb_, yb = be.upload(x), be.upload(res), be.alloc(n * c)
+    be.convnext_mlp(xb, gamma, beta, w0, b0, w2, b2, rb_, yb, n, c, 1e-6)
+    got = be.download(yb).reshape(n, c)
+    e = rnd(orc.row_norm(x, gamma, beta, n, c, 1e-6))
+    e = rnd(orc.linear(e, w0, b0, n, c, 4 * c, silu=True))
+    e = rnd(orc.linear(e, w2, b2, n, 4 * c, c))
+    e = rnd(orc.add(res, e))
+    err = max_rel_err(got, e)
+    say(f"convnext_mlp fused dtype={dtype} c={c} n={n} max_rel_err={err:.3e}")
+    assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
+@pytest.mark.parametrize("c", [64, 128])
+def test_convnext_mlp_fused_vs_slots(backends, dtype, c):
+    """At a size where blocks walk many tiles (and the weight ring runs
+    across tile boundaries), the fused tail matches the slot sequence it
+    replaces, itself checked against the oracle above; calling it twice with
+    the same weights (cached packing) gives identical results."""
+    be = backends[dtype]
+    rnd = lambda a: sh.storage_round(a, dtype)
+    n = 250_007
+    rng = np.random.default_rng(31 + c + dtype)
+    say(f"convnext_mlp fused vs slots dtype={dtype} c={c} n={n}")
+    x = rnd(rng.standard_normal((n, c)))
+    res = rnd(rng.standard_normal((n, c)))
+    gamma, beta, w0, b0, w2, b2 = mlp_params(rng, c, dtype)
+    xb, rb_ = be.upload(x), be.upload(res)
+    norm, hid, lin2, ref = be.alloc(n * c), be.alloc(n * 4 * c), be.alloc(n * c), be.alloc(n * c)
+    be.row_norm(xb, gamma, beta, norm, n, c, 1e-6)
+    be.linear(norm, w0, b0, hid, n, c, 4 * c, silu=True)
+    be.linear(hid, w2, b2, lin2, n, 4 * c, c)
+    be.add(rb_, lin2, ref, n * c)
+    y1, y2 = be.alloc(n * c), be.alloc(n * c)
+    be.convnext_mlp(xb, gamma, beta, w0, b0, w2, b2, rb_, y1, n, c, 1e-6)
+    be.convnext_mlp(xb, gamma, beta, w0, b0, w2, b2, rb_, y2, n, c, 1e-6)
+    g1, g2 = be.download(y1), be.download(y2)
+    assert np.array_equal(g1, g2)
+    err = max_rel_err(g1, be.download(ref))
+    say(f"convnext_mlp fused vs slots dtype={dtype} c={c} max_rel_err={err:.3e}")
+    assert err <= TOL[dtype]
+
+
+def test_convnext_mlp_rejects_unsupported(backends):
+    """fp32 storage and widths other than 64 / 128 report NOT_IMPLEMENTED
+    (the caller then runs the slot sequence); nothing is launched."""
+    rng = np.random.default_rng(5)
+    for dtype, c in ((sh.F32, 64), (sh.BF16, 96), (sh.F16, 256)):
+        be = backends[dtype]
+        n = 10
+        gamma, beta, w0, b0, w2, b2 = mlp_params(rng, c, dtype)
+        xb, yb = be.upload(np.zeros((n, c), np.float32)), be.alloc(n * c)
+        with pytest.raises(sh.HipError) as ei:
+            be.convnext_mlp(xb, gamma, beta, w0, b0, w2, b2, xb, yb, n, c, 1e-6)
+        assert ei.value.status == sh.NOT_IMPLEMENTED
+
+
 @pytest.mark.parametrize("dtype", [sh.F32, sh.BF16])
 def test_c2s_upblock_vs_oracle(backends, dtype):
     be = backends[dtype]

@@ -44,7 +44,9 @@ enum WeightLayout : int {
     kLayoutLinearT = 3,   // fp32 [ci][co]
     kLayoutVector = 4,    // fp32 [count]
     kLayoutConvMfmaGrouped = 5,  // kLayoutConvMfma with the compacted kernels' column grouping
-    kLayoutLinearMfma = 6        // storage type [ci/8][co][8], linear_mfma_group column grouping
+    kLayoutLinearMfma = 6,       // storage type [ci/8][co][8], linear_mfma_group column grouping
+    kLayoutMlp0 = 7,             // as kLayoutLinearMfma, the fused MLP's first GEMM grouping
+    kLayoutMlp2 = 8              // as kLayoutLinearMfma, the fused MLP's second GEMM grouping
 };
 
 struct StageMark {
@@ -275,10 +277,18 @@ trellis_status get_weight(Backend * be, const float * host, size_t count, int la
             }
             break;
         }
-        case kLayoutLinearMfma: {  // [co][ci] -> [ci/8][co][8] in the storage type, grouped columns
+        case kLayoutLinearMfma:  // [co][ci] -> [ci/8][co][8] in the storage type, grouped columns
+        case kLayoutMlp0:
+        case kLayoutMlp2: {
             staged.resize((size_t) ci * co * 2);
             uint16_t * w = (uint16_t *) staged.data();
-            const int g = linear_mfma_group(co), wn = 16 * g;
+            int g = linear_mfma_group(co);
+            if (layout != kLayoutLinearMfma) {
+                int g0 = 1, g2 = 1;
+                convnext_mlp_groups(layout == kLayoutMlp0 ? ci : co, &g0, &g2);
+                g = layout == kLayoutMlp0 ? g0 : g2;
+            }
+            const int wn = 16 * g;
             for (int o = 0; o < co; ++o) {
                 const int pos = (o / wn) * wn + (o % g) * 16 + (o % wn) / g;
                 for (int c = 0; c < ci; ++c) {
@@ -472,6 +482,39 @@ trellis_status op_linear(trellis_sparse_backend * backend, const trellis_sparse_
 trellis_status op_linear_silu(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * weight,
                               const float * bias, trellis_sparse_buffer * y, int64_t n, int ci, int co) {
     return linear_impl(backend, x, weight, bias, y, n, ci, co, 1);
+}
+
+// The ConvNeXt block's MLP tail fused: y = residual + W2 SiLU(W0 LN(x) + b0) + b2.
+trellis_status mlp_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * gamma,
+                        const float * beta, const float * w0, const float * b0, const float * w2, const float * b2,
+                        const trellis_sparse_buffer * residual, trellis_sparse_buffer * y, int64_t n, int c,
+                        float eps) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (w0 == nullptr || w2 == nullptr || n <= 0 || c <= 0 || !(eps >= 0.0f) ||
+        !float_buffer_ok(be, x, (size_t) n * c) || !float_buffer_ok(be, residual, (size_t) n * c) ||
+        !float_buffer_ok(be, y, (size_t) n * c)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "convnext_mlp: bad argument");
+    }
+    if (!convnext_mlp_supported(be->policy.compute_dtype, c)) {
+        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, "convnext_mlp: needs bf16/fp16 storage and c = 64 or 128");
+    }
+    CallScope scope(be);
+    const void *g = nullptr, *bt = nullptr, *pw0 = nullptr, *pb0 = nullptr, *pw2 = nullptr, *pb2 = nullptr;
+    trellis_status st = get_weight(be, gamma, (size_t) c, kLayoutVector, 0, c, &g);
+    if (st == TRELLIS_STATUS_OK) st = get_weight(be, beta, (size_t) c, kLayoutVector, 0, c, &bt);
+    if (st == TRELLIS_STATUS_OK) st = get_weight(be, w0, (size_t) c * 4 * c, kLayoutMlp0, c, 4 * c, &pw0);
+    if (st == TRELLIS_STATUS_OK) st = get_weight(be, b0, (size_t) 4 * c, kLayoutVector, 0, 4 * c, &pb0);
+    if (st == TRELLIS_STATUS_OK) st = get_weight(be, w2, (size_t) 4 * c * c, kLayoutMlp2, 4 * c, c, &pw2);
+    if (st == TRELLIS_STATUS_OK) st = get_weight(be, b2, (size_t) c, kLayoutVector, 0, c, &pb2);
+    if (st != TRELLIS_STATUS_OK) return st;
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+    const hipError_t err =
+        launch_convnext_mlp(be->policy.compute_dtype, x->ptr, (const float *) g, (const float *) bt, pw0,
+                            (const float *) pb0, pw2, (const float *) pb2, residual->ptr, y->ptr, n, c, eps, be->cus,
+                            be->stream);
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+    return hip_status(be, err, "convnext_mlp");
 }
 
 trellis_status norm_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * gamma,
@@ -1334,6 +1377,14 @@ trellis_status trellis_sparse_hip_free_c2s_map(trellis_sparse_backend * backend,
     tsh::select_device(be);
     tsh::map_release(be, map);
     return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                               const float * gamma, const float * beta, const float * mlp0_w,
+                                               const float * mlp0_b, const float * mlp2_w, const float * mlp2_b,
+                                               const trellis_sparse_buffer * residual, trellis_sparse_buffer * y,
+                                               int64_t n, int c, float eps) {
+    return tsh::mlp_impl(backend, x, gamma, beta, mlp0_w, mlp0_b, mlp2_w, mlp2_b, residual, y, n, c, eps);
 }
 
 trellis_status trellis_sparse_hip_profile_enable(trellis_sparse_backend * backend, int enable) {

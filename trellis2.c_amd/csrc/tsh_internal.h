@@ -167,6 +167,14 @@ int linear_mfma_group(int co);
 bool linear_mfma_supported(int dtype, int ci, int co);
 hipError_t launch_linear_mfma(int dtype, const void * x, const void * w16, const float * bias, void * y, int64_t n,
                               int ci, int co, int silu, int cus, hipStream_t s);
+// Fused ConvNeXt MLP tail (kernels_block.hip): bf16/fp16, C = 64 or 128.
+// w0 [C/8][4C][8] and w2 [4C/8][C][8] in the storage type with the grouped
+// column packing of the MFMA linear, groups g0 and g2 from convnext_mlp_groups.
+bool convnext_mlp_supported(int dtype, int c);
+void convnext_mlp_groups(int c, int * g0, int * g2);
+hipError_t launch_convnext_mlp(int dtype, const void * x, const float * gamma, const float * beta, const void * w0,
+                               const float * b0, const void * w2, const float * b2, const void * res, void * y,
+                               int64_t n, int c, float eps, int cus, hipStream_t s);
 hipError_t launch_c2s_count(int dtype, const void * logits, int64_t n, int32_t * counts, hipStream_t s);
 // Exclusive scan of n int32 values; total written to *total_dev.  tmp needs scan_tmp_bytes(n).
 size_t scan_tmp_bytes(int64_t n);

@@ -108,6 +108,8 @@ ABI = {
     "trellis_sparse_hip_profile_read": (c_int, [_p, POINTER(StageTimes), c_int]),
     "trellis_sparse_hip_event_record": (c_int, [_p, c_int]),
     "trellis_sparse_hip_event_elapsed": (c_int, [_p, c_int, c_int, POINTER(c_float)]),
+    "trellis_sparse_hip_convnext_mlp": (c_int, [_p, _p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _p, _p, c_int64,
+                                                c_int, c_float]),
 }
 
 
@@ -320,6 +322,16 @@ class Backend:
         b = None if beta is None else self.keep(_f32(beta))
         fn = self.ops.row_norm_silu if silu else self.ops.row_norm
         self._check(fn(self.ptr, x.handle, _ptr(g, _f32p), _ptr(b, _f32p), y.handle, n, c, eps), "row_norm")
+
+    def convnext_mlp(self, x: Buffer, gamma, beta, w0, b0, w2, b2, residual: Buffer, y: Buffer, n: int, c: int,
+                     eps: float):
+        """Fused row_norm -> linear_silu (c -> 4c) -> linear (4c -> c) -> add(residual, .)."""
+        g, bt, b0a, b2a = (None if a is None else self.keep(_f32(a)) for a in (gamma, beta, b0, b2))
+        w0a, w2a = self.keep(_f32(w0)), self.keep(_f32(w2))
+        self._check(LIB.trellis_sparse_hip_convnext_mlp(self.ptr, x.handle, _ptr(g, _f32p), _ptr(bt, _f32p),
+                                                        _ptr(w0a, _f32p), _ptr(b0a, _f32p), _ptr(w2a, _f32p),
+                                                        _ptr(b2a, _f32p), residual.handle, y.handle, n, c, eps),
+                    "convnext_mlp")
 
     def silu_inplace(self, x: Buffer, count: int):
         self._check(self.ops.silu_inplace(self.ptr, x.handle, count), "silu_inplace")
