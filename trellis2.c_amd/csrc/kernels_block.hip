@@ -5,28 +5,67 @@
 // (src/architectures/sparse_unet_decoder/executor.c:206-241: row_norm ->
 // linear_silu (C -> 4C) -> linear (4C -> C) -> add), whose 4C-wide
 // intermediate otherwise makes a round trip through HBM (n * 4C * s written
-// and read back).  Here it stays in LDS.
+// and read back).  Here it stays in LDS.  Values are rounded to the storage
+// type where the slot sequence stores them: after the norm, after the SiLU,
+// after the second linear and after the add.
 //
-// Persistent blocks of 8 wavefronts walk 64-row tiles.  Per tile:
-//  A. LayerNorm: C/8 lanes per row hold the row's 16-byte chunks; mean and
-//     squared deviations reduced with shuffles; the normalised row (scale,
-//     shift, one rounding) goes to LDS in the MFMA operand layout.
+// Persistent blocks of 8 wavefronts walk 64-row tiles.  At this width the
+// SiLU (two transcendental instructions per hidden value) and the norm cost
+// more vector-ALU time than the two GEMMs cost matrix-core time, so the work
+// is arranged for the two to overlap:
 //  B. GEMM 1 (64 x C times C x 4C): wavefront w owns hidden columns
 //     [w * 4C/8, (w + 1) * 4C/8) for all 64 rows; its weight fragments stay in
-//     registers for every tile.  Bias and SiLU in fp32, one rounding, the
-//     hidden tile written to LDS in the operand layout.
+//     registers for every tile.  Row block q's MFMAs run while the bias,
+//     SiLU and rounding of row block q - 1 go through the vector ALU; the
+//     hidden tile is written to LDS in the operand layout.
 //  C. GEMM 2 (64 x 4C times 4C x C): 2 row groups x 4 channel groups; weight
-//     fragments streamed from global memory through a 4-step register ring.
-//     Bias in fp32 into an fp32 LDS staging tile.
-//  D. staged value rounded to the storage type, residual added, rounded
-//     again, 16-byte coalesced stores.
-// Operand tiles in LDS use the a_granule layout per (K step, 16-row block),
-// conflict-free for the fragment reads.  fp32 accumulation throughout.
+//     fragments streamed from global memory through a 4-step register ring
+//     that runs on across tiles.  Meanwhile the LayerNorm of the NEXT tile
+//     (its rows loaded into registers during B) goes into the operand tile of
+//     GEMM 1: C/8 lanes per row, shuffle reductions.  The GEMM 2 result, with
+//     bias, is rounded into a storage-type staging tile.
+//  D. residual (loaded during B) + staged value, rounded, 16-byte stores.
+// Two block barriers per tile (after B and after C).  Operand tiles in LDS
+// use the a_granule layout per (K step, 16-row block), conflict-free for the
+// fragment reads.  fp32 accumulation throughout.
 #include "tsh_internal.h"
 #include "mfma_common.h"
 
 namespace tsh {
 namespace {
+
+template <int DT> __device__ inline typename Store<DT>::T to_store(float v) {
+    if constexpr (DT == kBF16) {
+        return __builtin_bit_cast(uint16_t, (__bf16) v);  // round to nearest even
+    } else {
+        return (typename Store<DT>::T) v;
+    }
+}
+
+// The 8 storage values of a 16-byte chunk as fp32.
+template <int DT> __device__ inline void unpack8(const int4 & c, float * v) {
+    const uint32_t w[4] = {(uint32_t) c.x, (uint32_t) c.y, (uint32_t) c.z, (uint32_t) c.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if constexpr (DT == kBF16) {
+            v[2 * k] = __builtin_bit_cast(float, w[k] << 16);
+            v[2 * k + 1] = __builtin_bit_cast(float, w[k] & 0xffff0000u);
+        } else {
+            v[2 * k] = (float) __builtin_bit_cast(_Float16, (uint16_t) (w[k] & 0xffffu));
+            v[2 * k + 1] = (float) __builtin_bit_cast(_Float16, (uint16_t) (w[k] >> 16));
+        }
+    }
+}
+
+template <int DT> __device__ inline int4 pack8(const float * v) {
+    union {
+        int4 c;
+        typename Store<DT>::T h[8];
+    } u;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) u.h[k] = to_store<DT>(v[k]);
+    return u.c;
+}
 
 template <int DT, int C>
 __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::T * __restrict__ x,
@@ -49,15 +88,18 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
     constexpr int NT1 = WN1 / 16;
     constexpr int WN2 = C / 4;        // output columns per wavefront (GEMM 2: 4 channel groups)
     constexpr int NT2 = WN2 / 16;
-    constexpr int LPR = C / 8;        // LayerNorm lanes per row
+    constexpr int LPR = C / 8;        // LayerNorm lanes per row (one 16-byte chunk each)
     constexpr int RPP = 64 / LPR;     // LayerNorm rows per wavefront pass
+    constexpr int LNP = 8 / RPP;      // LayerNorm passes (8 rows per wavefront)
+    constexpr int CH = C / 8;         // 16-byte chunks per row
+    constexpr int DP = BM * CH / 512; // output chunks per thread
     constexpr int D2 = 4;             // GEMM 2 weight ring depth (steps)
-    constexpr int OSTR = C + 4;       // fp32 staging row stride
+    constexpr int OSTR = C + 8;       // staging row stride (storage elements)
     static_assert(C == 64 || C == 128, "C = 64 or 128");
-    static_assert(KS2 % D2 == 0 && 8 % RPP == 0, "shapes");
+    static_assert(KS2 % D2 == 0 && 8 % RPP == 0 && DP >= 1, "shapes");
     __shared__ __attribute__((aligned(16))) T s_x[KS1 * 4 * 64 * 8];
     __shared__ __attribute__((aligned(16))) T s_h[KS2 * 4 * 64 * 8];
-    __shared__ __attribute__((aligned(16))) float s_o[BM * OSTR];
+    __shared__ __attribute__((aligned(16))) T s_o[BM * OSTR];
 
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -84,6 +126,14 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
     float bias2[NT2];
 #pragma unroll
     for (int nt = 0; nt < NT2; ++nt) bias2[nt] = b2 != nullptr ? b2[ch * WN2 + l16 * NT2 + nt] : 0.0f;
+    // LayerNorm: lane handles chunk li of rows wave*8 + p*RPP + lane/LPR.
+    const int li = lane % LPR;
+    float gv[8], bv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        gv[e] = gamma != nullptr ? gamma[li * 8 + e] : 1.0f;
+        bv[e] = beta != nullptr ? beta[li * 8 + e] : 0.0f;
+    }
     const T * w2lane = w2 + ((int64_t) lg * C + ch * WN2 + l16) * 8;
     // wofs is 0, hidden from the compiler once per tile: the W2 loads are the
     // same for every tile, and hoisting them out of the tile loop would hold
@@ -94,105 +144,112 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
         for (int nt = 0; nt < NT2; ++nt)
             f[nt] = *(const V *) (w2lane + wofs + (int64_t) s * 4 * C * 8 + nt * 16 * 8);
     };
+    auto load_x = [&](int4 * xr, int tile) {
+#pragma unroll
+        for (int p = 0; p < LNP; ++p) {
+            const int64_t row = (int64_t) tile * BM + wave * 8 + p * RPP + lane / LPR;
+            xr[p] = row < n ? *(const int4 *) (x + row * C + li * 8) : int4{0, 0, 0, 0};
+        }
+    };
+    // Normalised rows into s_x (rows past n normalise zeros; never stored).
+    auto layer_norm = [&](const int4 * xr) {
+#pragma unroll
+        for (int p = 0; p < LNP; ++p) {
+            const int rloc = wave * 8 + p * RPP + lane / LPR;
+            float v[8];
+            unpack8<DT>(xr[p], v);
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s += v[e];
+#pragma unroll
+            for (int d = LPR / 2; d >= 1; d >>= 1) s += __shfl_xor(s, d);
+            const float mean = s / (float) C;
+            float q = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[e] -= mean;
+                q += v[e] * v[e];
+            }
+#pragma unroll
+            for (int d = LPR / 2; d >= 1; d >>= 1) q += __shfl_xor(q, d);
+            const float inv = 1.0f / sqrtf(q / (float) C + eps);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = v[e] * inv * gv[e] + bv[e];
+            // Channels li*8 .. li*8+7 of row rloc: one operand granule.
+            *(int4 *) (&s_x[opnd(li / 4, rloc / 16, rloc % 16, li % 4)]) = pack8<DT>(v);
+        }
+    };
+    // Bias, SiLU and rounding of GEMM 1 row block q: the lane's hidden
+    // channels h0 .. h0 + NT1 - 1 (adjacent) of rows q*16 + lg*4 + i are NT1
+    // elements of one operand granule of s_h.
+    const int h0 = wave * WN1 + l16 * NT1;
+    auto silu_store = [&](const f32x4 * a, int q) {
+        using Hv = T __attribute__((ext_vector_type(NT1)));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            Hv o;
+#pragma unroll
+            for (int nt = 0; nt < NT1; ++nt) {
+                float v = a[nt][i] + bias1[nt];
+                v = v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+                o[nt] = to_store<DT>(v);
+            }
+            *(Hv *) (&s_h[opnd(h0 / 32, q, lg * 4 + i, (h0 % 32) / 8) + h0 % 8]) = o;
+        }
+    };
+
     // GEMM 2 weight ring: wr[r] holds K step s0 + r; the last steps of a tile
     // fetch the first steps of the next.
     V wr[D2][NT2];
 #pragma unroll
     for (int s = 0; s < D2; ++s) load_w2(wr[s], s);
+    {
+        int4 xr[LNP];
+        load_x(xr, lb);
+        layer_norm(xr);
+    }
+    lds_barrier();
 
     for (int tile = lb; tile < n_tiles; tile += G) {
         const int64_t row0 = (int64_t) tile * BM;
         asm volatile("" : "+s"(wofs));
-        // ---- A. LayerNorm into s_x --------------------------------------
+        // Loads for later phases: the next tile's rows (LayerNorm during C;
+        // zeros past the last tile) and this tile's residual (D).
+        int4 xr[LNP];
+        load_x(xr, tile + G);
+        int4 rr[DP];
+#pragma unroll
+        for (int p = 0; p < DP; ++p) {
+            const int e = t + p * 512;
+            const int64_t row = row0 + e / CH;
+            rr[p] = row < n ? *(const int4 *) (res + row * C + (e % CH) * 8) : int4{0, 0, 0, 0};
+        }
+        // ---- B. GEMM 1 by row block; SiLU of the previous block meanwhile --
         {
-            const int li = lane % LPR;
+            f32x4 acc[2][NT1];
 #pragma unroll
-            for (int p = 0; p < 8 / RPP; ++p) {
-                const int rloc = wave * 8 + p * RPP + lane / LPR;
-                const int64_t row = row0 + rloc;
-                union {
-                    int4 v;
-                    T h[8];
-                } ch8;
-                ch8.v = row < n ? *(const int4 *) (x + row * C + li * 8) : int4{0, 0, 0, 0};
-                float v[8];
-                float s = 0.0f;
+            for (int q = 0; q < 4; ++q) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    v[e] = Store<DT>::ld(ch8.h, e);
-                    s += v[e];
+                for (int nt = 0; nt < NT1; ++nt) acc[q & 1][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < KS1; ++s) {
+                    const V af = *(const V *) (&s_x[opnd(s, q, l16, lg)]);
+#pragma unroll
+                    for (int nt = 0; nt < NT1; ++nt) acc[q & 1][nt] = Mfma<DT>::mac(af, wf1[s][nt], acc[q & 1][nt]);
                 }
-#pragma unroll
-                for (int d = LPR / 2; d >= 1; d >>= 1) s += __shfl_xor(s, d);
-                const float mean = s / (float) C;
-                float q = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) q += (v[e] - mean) * (v[e] - mean);
-#pragma unroll
-                for (int d = LPR / 2; d >= 1; d >>= 1) q += __shfl_xor(q, d);
-                const float inv = 1.0f / sqrtf(q / (float) C + eps);
-                const float4 g0 = gamma != nullptr ? *(const float4 *) (gamma + li * 8) : float4{1.f, 1.f, 1.f, 1.f};
-                const float4 g1 = gamma != nullptr ? *(const float4 *) (gamma + li * 8 + 4) : float4{1.f, 1.f, 1.f, 1.f};
-                const float4 bb0 = beta != nullptr ? *(const float4 *) (beta + li * 8) : float4{0.f, 0.f, 0.f, 0.f};
-                const float4 bb1 = beta != nullptr ? *(const float4 *) (beta + li * 8 + 4) : float4{0.f, 0.f, 0.f, 0.f};
-                const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-                const float bv[8] = {bb0.x, bb0.y, bb0.z, bb0.w, bb1.x, bb1.y, bb1.z, bb1.w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) Store<DT>::st(ch8.h, e, (v[e] - mean) * inv * gv[e] + bv[e]);
-                // Channels li*8 .. li*8+7 of row rloc: one operand granule.
-                *(int4 *) (&s_x[opnd(li / 4, rloc / 16, rloc % 16, li % 4)]) = ch8.v;
+                if (q > 0) silu_store(acc[(q - 1) & 1], q - 1);
             }
+            silu_store(acc[1], 3);
         }
         lds_barrier();
-        // ---- B. GEMM 1, bias, SiLU into s_h --------------------------------
-        {
-            f32x4 acc[4][NT1];
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int nt = 0; nt < NT1; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < KS1; ++s) {
-                V af[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) af[q] = *(const V *) (&s_x[opnd(s, q, l16, lg)]);
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-#pragma unroll
-                    for (int nt = 0; nt < NT1; ++nt) acc[q][nt] = Mfma<DT>::mac(af[q], wf1[s][nt], acc[q][nt]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            // Lane's hidden channels h0 .. h0 + NT1 - 1 (adjacent) of rows
-            // q*16 + lg*4 + i: NT1 elements of one operand granule of s_h.
-            const int h0 = wave * WN1 + l16 * NT1;
-            using Hv = T __attribute__((ext_vector_type(NT1)));
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    Hv o;
-#pragma unroll
-                    for (int nt = 0; nt < NT1; ++nt) {
-                        float v = acc[q][nt][i] + bias1[nt];
-                        v = v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
-                        if constexpr (DT == kBF16) {
-                            o[nt] = __builtin_bit_cast(uint16_t, (__bf16) v);
-                        } else {
-                            o[nt] = (T) v;
-                        }
-                    }
-                    const int r = lg * 4 + i;
-                    *(Hv *) (&s_h[opnd(h0 / 32, q, r, (h0 % 32) / 8) + h0 % 8]) = o;
-                }
-        }
-        lds_barrier();
-        // ---- C. GEMM 2, bias into s_o ------------------------------------
+        // ---- C. GEMM 2; the next tile's LayerNorm meanwhile -----------------
         {
             f32x4 acc[2][NT2];
 #pragma unroll
             for (int q = 0; q < 2; ++q)
 #pragma unroll
                 for (int nt = 0; nt < NT2; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
             for (int s0 = 0; s0 < KS2; s0 += D2) {
 #pragma unroll
                 for (int r = 0; r < D2; ++r) {
@@ -207,47 +264,38 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
                     const int sn = s + D2 < KS2 ? s + D2 : s + D2 - KS2;
                     load_w2(wr[r], sn);
                 }
+                // s_x was last read by GEMM 1, before the barrier above.
+                if (s0 == 0) layer_norm(xr);
             }
             const int c0 = ch * WN2 + l16 * NT2;
+            using Ov = T __attribute__((ext_vector_type(NT2)));
 #pragma unroll
             for (int q = 0; q < 2; ++q)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int r = (rh + 2 * q) * 16 + lg * 4 + i;
+                    Ov o;
 #pragma unroll
-                    for (int nt = 0; nt < NT2; ++nt) s_o[r * OSTR + c0 + nt] = acc[q][nt][i] + bias2[nt];
+                    for (int nt = 0; nt < NT2; ++nt) o[nt] = to_store<DT>(acc[q][nt][i] + bias2[nt]);
+                    *(Ov *) (&s_o[r * OSTR + c0]) = o;
                 }
         }
         lds_barrier();
-        // ---- D. residual add, 16-byte stores ------------------------------
-        {
-            constexpr int CH = C / 8;  // 16-byte chunks per row
+        // ---- D. residual add, 16-byte stores -------------------------------
+        // s_o is rewritten only after the next tile's first barrier.
 #pragma unroll
-            for (int p = 0; p < BM * CH / 512; ++p) {
-                const int e = t + p * 512;
-                const int r = e / CH, j = e % CH;
-                const int64_t row = row0 + r;
-                if (row >= n) continue;
-                union {
-                    int4 v;
-                    T h[8];
-                } rr, o;
-                rr.v = *(const int4 *) (res + row * C + j * 8);
-                const float4 a = *(const float4 *) (&s_o[r * OSTR + j * 8]);
-                const float4 b = *(const float4 *) (&s_o[r * OSTR + j * 8 + 4]);
-                const float sv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-                // The second linear's output is rounded to the storage type
-                // before the add, as where the two are separate slots.
+        for (int p = 0; p < DP; ++p) {
+            const int e = t + p * 512;
+            const int r = e / CH, j = e % CH;
+            const int64_t row = row0 + r;
+            if (row >= n) continue;
+            float a[8], b[8];
+            unpack8<DT>(rr[p], a);
+            unpack8<DT>(*(const int4 *) (&s_o[r * OSTR + j * 8]), b);
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    Store<DT>::st(o.h, k, sv[k]);
-                    Store<DT>::st(o.h, k, Store<DT>::ld(rr.h, k) + Store<DT>::ld(o.h, k));
-                }
-                *(int4 *) (y + row * C + j * 8) = o.v;
-            }
+            for (int k = 0; k < 8; ++k) a[k] += b[k];
+            *(int4 *) (y + row * C + j * 8) = pack8<DT>(a);
         }
-        // s_x and s_h are rewritten only after the next tile's barriers, and
-        // s_o after two more; no barrier needed here.
     }
 }
 
