@@ -272,6 +272,47 @@ trellis_status trellis_sparse_hip_free_c2s_map(trellis_sparse_backend * backend,
                                                trellis_sparse_c2s_device_map * map);
 
 /* ------------------------------------------------------------------------ */
+/* Spatial-to-channel downsample of the encoder on the device (no vtable     */
+/* counterpart: the reference runs it on the host, replacing                 */
+/* trellis_sparse_s2c_host_build, sparse_unet_encoder/s2c_host.c:33-120, and  */
+/* the download / pack / skip-mean / upload round trip of encoder_s2c_exec,  */
+/* sparse_unet_encoder/executor.c:258-300).                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Builds the S2C relation of fine_n fine voxels, given as host coordinates
+ * [fine_n][4] or as a device map (fine_coords_map, which wins when both are
+ * given).  fine_map_out: a device map of the fine level (coords = a copy of
+ * the fine coordinates, parent[f] = coarse row, subidx[f] = (x&1) |
+ * (y&1)<<1 | (z&1)<<2, n_parent = coarse_n) - the decoder's C2S guide for
+ * this level, usable with c2s_gather_device, skip_repeat_device,
+ * download_c2s_map and build_rulebook_for_c2s_map.  coarse_map_out: a
+ * coordinates-only map of the coarse voxels (b, x/2, y/2, z/2) in ascending
+ * (b, x, y, z) order, for build_rulebook_for_c2s_map and download_c2s_coords.
+ * Negative coordinates -> INVALID_ARGUMENT; a fine voxel given twice ->
+ * PARSE_ERROR (every repeat; the host build catches a repeat only when no
+ * other child of its coarse voxel lies between the two rows).  Both maps
+ * live until destroy or trellis_sparse_hip_free_c2s_map. */
+trellis_status trellis_sparse_hip_s2c_build_device(trellis_sparse_backend * backend, const int32_t * fine_coords_bxyz,
+                                                   const trellis_sparse_c2s_device_map * fine_coords_map,
+                                                   int64_t fine_n, trellis_sparse_c2s_device_map ** fine_map_out,
+                                                   trellis_sparse_c2s_device_map ** coarse_map_out,
+                                                   int64_t * coarse_n_out);
+/* y[c][s*(co/8) + j] = x[f][j] for the fine row f in child slot s of coarse
+ * voxel c, zero for empty slots (executor.c:279-286).  x [fine_n][co/8],
+ * y [coarse_n][co]; co % 8 == 0. */
+trellis_status trellis_sparse_hip_s2c_pack_device(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                                  const trellis_sparse_c2s_device_map * fine_map,
+                                                  trellis_sparse_buffer * y, int co);
+/* y[c][s*(co/8) + j] = sum over t < g of x[f][j*g + t] / g in fp32 from zero,
+ * g = 8*ci/co, for the fine row f in child slot s of coarse voxel c; zero for
+ * empty slots (executor.c:287-292).  x [fine_n][ci], y [coarse_n][co];
+ * co % 8 == 0 and (8*ci) % co == 0 (executor.c:172-175). */
+trellis_status trellis_sparse_hip_s2c_skip_mean_device(trellis_sparse_backend * backend,
+                                                       const trellis_sparse_buffer * x,
+                                                       const trellis_sparse_c2s_device_map * fine_map,
+                                                       trellis_sparse_buffer * y, int ci, int co);
+
+/* ------------------------------------------------------------------------ */
 /* Fused ConvNeXt MLP tail (no counterpart in the reference vtable: it       */
 /* replaces the slot sequence row_norm -> linear_silu -> linear -> add of     */
 /* the decoder's ConvNeXt block, sparse_unet_decoder/executor.c:206-241).    */

@@ -310,6 +310,123 @@ int orc_c2s_map(const int32_t * coords, const float * logits, int64_t n, int32_t
 
 void orc_free(void * p) { free(p); }
 
+/* Sort record: the coarse voxel as four non-negative int32 fields, then the
+ * fine row (which makes the order total, so qsort's instability is moot). */
+typedef struct orc_s2c_rec {
+    int32_t key[4];
+    int32_t row;
+    int32_t sub;
+} orc_s2c_rec;
+
+static int orc_s2c_cmp(const void * pa, const void * pb) {
+    const orc_s2c_rec * a = (const orc_s2c_rec *) pa;
+    const orc_s2c_rec * b = (const orc_s2c_rec *) pb;
+    static const int lex[4] = {0, 1, 2, 3};
+    static const int zyxb[4] = {3, 2, 1, 0};
+    const int * ord = g_mutation == ORC_MUT_S2C_ORDER ? zyxb : lex;
+    for (int i = 0; i < 4; ++i) {
+        const int32_t u = a->key[ord[i]], v = b->key[ord[i]];
+        if (u != v) return u < v ? -1 : 1;
+    }
+    return a->row < b->row ? -1 : (a->row > b->row ? 1 : 0);
+}
+
+static int orc_s2c_same(const orc_s2c_rec * a, const orc_s2c_rec * b) {
+    return memcmp(a->key, b->key, sizeof(a->key)) == 0;
+}
+
+int orc_s2c_map(const int32_t * fine_coords, int64_t n, int32_t ** coarse_out, int32_t ** parent_out,
+                int32_t ** subidx_out, int64_t * coarse_n_out) {
+    if (fine_coords == NULL || coarse_out == NULL || parent_out == NULL || subidx_out == NULL ||
+        coarse_n_out == NULL || n <= 0 || n > INT32_MAX) {
+        return 2;
+    }
+    *coarse_out = NULL;
+    *parent_out = NULL;
+    *subidx_out = NULL;
+    *coarse_n_out = 0;
+    orc_s2c_rec * rec = (orc_s2c_rec *) malloc((size_t) n * sizeof(orc_s2c_rec));
+    int32_t * parent = (int32_t *) malloc((size_t) n * sizeof(int32_t));
+    int32_t * subidx = (int32_t *) malloc((size_t) n * sizeof(int32_t));
+    int32_t * coarse = NULL;
+    int rc = 0;
+    if (rec == NULL || parent == NULL || subidx == NULL) {
+        rc = 5;
+    }
+    for (int64_t f = 0; rc == 0 && f < n; ++f) {
+        const int32_t * c = fine_coords + 4 * f;
+        if (c[0] < 0 || c[1] < 0 || c[2] < 0 || c[3] < 0) {
+            rc = 2;
+            break;
+        }
+        rec[f].key[0] = c[0];
+        for (int a = 1; a < 4; ++a) rec[f].key[a] = c[a] / 2;
+        rec[f].row = (int32_t) f;
+        rec[f].sub = (c[1] & 1) | ((c[2] & 1) << 1) | ((c[3] & 1) << 2);
+    }
+    int64_t m = 0;
+    if (rc == 0) {
+        qsort(rec, (size_t) n, sizeof(orc_s2c_rec), orc_s2c_cmp);
+        for (int64_t i = 0; i < n; ++i) {
+            const int head = i == 0 || !orc_s2c_same(&rec[i - 1], &rec[i]);
+            if (!head && rec[i - 1].sub == rec[i].sub) {
+                rc = 4;  /* the same fine voxel twice */
+                break;
+            }
+            m += head;
+        }
+    }
+    if (rc == 0) {
+        coarse = (int32_t *) malloc((size_t) m * 4u * sizeof(int32_t));
+        if (coarse == NULL) rc = 5;
+    }
+    if (rc == 0) {
+        int64_t row = -1;
+        for (int64_t i = 0; i < n; ++i) {
+            if (i == 0 || !orc_s2c_same(&rec[i - 1], &rec[i])) {
+                ++row;
+                memcpy(coarse + 4 * row, rec[i].key, 4 * sizeof(int32_t));
+            }
+            parent[rec[i].row] = (int32_t) row;
+            subidx[rec[i].row] = rec[i].sub;
+        }
+    }
+    free(rec);
+    if (rc != 0) {
+        free(parent);
+        free(subidx);
+        free(coarse);
+        return rc;
+    }
+    *coarse_out = coarse;
+    *parent_out = parent;
+    *subidx_out = subidx;
+    *coarse_n_out = m;
+    return 0;
+}
+
+void orc_s2c_pack(const float * x, const int32_t * parent, const int32_t * subidx, float * y, int64_t n_fine,
+                  int64_t n_coarse, int co) {
+    const int pc = co / 8;
+    memset(y, 0, (size_t) n_coarse * (size_t) co * sizeof(float));
+    for (int64_t f = 0; f < n_fine; ++f) {
+        memcpy(y + (int64_t) parent[f] * co + subidx[f] * pc, x + f * pc, (size_t) pc * sizeof(float));
+    }
+}
+
+void orc_s2c_skip_mean(const float * x, const int32_t * parent, const int32_t * subidx, float * y, int64_t n_fine,
+                       int64_t n_coarse, int ci, int co) {
+    const int g = 8 * ci / co;
+    memset(y, 0, (size_t) n_coarse * (size_t) co * sizeof(float));
+    for (int64_t f = 0; f < n_fine; ++f) {
+        float * yr = y + (int64_t) parent[f] * co;
+        for (int c = 0; c < ci; ++c) {
+            const int flat = g_mutation == ORC_MUT_S2C_CHANNEL ? c * 8 + subidx[f] : subidx[f] * ci + c;
+            yr[flat / g] += x[f * ci + c] / (float) g;
+        }
+    }
+}
+
 void orc_c2s_gather(const float * x, const int32_t * parent, const int32_t * subidx, float * y, int64_t n_out,
                     int co) {
     for (int64_t r = 0; r < n_out; ++r) {

@@ -21,6 +21,13 @@
  *   orc_c2s_gather - the host channel2spatial known answer (test_trellis.c:1521-1533)
  *       and closed-form numpy indexing.
  *   orc_skip_repeat - closed-form numpy indexing with the ceil-div repeat.
+ *   orc_s2c_map / orc_s2c_skip_mean - the reference encoder's known-answer
+ *       vector (test_sparse_encoder_backend.c:84-110: coarse coords, parent,
+ *       subidx and the skip means it produces with zero conv weights); the map
+ *       against numpy unique(axis=0) on random sets; S2C of a C2S map
+ *       returns the parents.
+ *   orc_s2c_pack - c2s_gather (the reference's inverse index map) of the
+ *       packed rows returns the input rows; all other slots are zero.
  *   orc_row_norm / orc_silu / orc_add / orc_linear - torch.nn.functional in float64.
  * Each pin is exercised with a planted mistake (orc_set_mutation) to show the
  * check would fail on a plausible error.
@@ -45,7 +52,9 @@ enum {
     ORC_MUT_NORM_SAMPLE_VAR = 5, /* row_norm divides the variance by C-1 */
     ORC_MUT_NEIGHBOR_SIGN = 6,   /* neighbour offset uses (1 - kd) instead of (kd - 1) on x */
     ORC_MUT_CROSS_BATCH = 7,     /* neighbour lookup ignores the batch index */
-    ORC_MUT_SUBDIV_GE = 8        /* subdivide keeps logits >= 0 instead of > 0 */
+    ORC_MUT_SUBDIV_GE = 8,       /* subdivide keeps logits >= 0 instead of > 0 */
+    ORC_MUT_S2C_ORDER = 9,       /* S2C orders coarse voxels z-major (z, y, x, b) instead of (b, x, y, z) */
+    ORC_MUT_S2C_CHANNEL = 10     /* S2C skip mean groups channel-major ((c*8 + s) / g instead of (s*ci + c) / g) */
 };
 void orc_set_mutation(int mutation);
 int orc_get_mutation(void);
@@ -100,6 +109,22 @@ void orc_conv3d_bruteforce(const int32_t * coords, const float * feats, const fl
 int orc_c2s_map(const int32_t * coords, const float * logits, int64_t n, int32_t ** coords_out,
                 int32_t ** parent_out, int32_t ** subidx_out, int64_t * m_out);
 void orc_free(void * p);
+
+/* sparse_unet_encoder/s2c_host.c:33-120 - coarse voxel (b, x/2, y/2, z/2) of
+ * every fine voxel, the distinct coarse voxels in ascending (b, x, y, z)
+ * order, parent[f] = coarse row, subidx[f] = (x&1) | (y&1)<<1 | (z&1)<<2.
+ * Returns 0, 2 (bad argument or a negative coordinate), 4 (two fine voxels
+ * with the same coarse voxel and subidx) or 5 (OOM); arrays are malloc'd. */
+int orc_s2c_map(const int32_t * fine_coords, int64_t n, int32_t ** coarse_out, int32_t ** parent_out,
+                int32_t ** subidx_out, int64_t * coarse_n_out);
+/* sparse_unet_encoder/executor.c:279-286 - packed[parent[f]][subidx[f]*pc + c]
+ * = x[f][c] (pc = co/8), zero where a coarse voxel lacks that child. */
+void orc_s2c_pack(const float * x, const int32_t * parent, const int32_t * subidx, float * y, int64_t n_fine,
+                  int64_t n_coarse, int co);
+/* sparse_unet_encoder/executor.c:287-292 - skip[parent[f]][(subidx[f]*ci + c)/g]
+ * += x[f][c] / g, g = 8*ci/co, fp32 in fine-row then channel order from 0. */
+void orc_s2c_skip_mean(const float * x, const int32_t * parent, const int32_t * subidx, float * y, int64_t n_fine,
+                       int64_t n_coarse, int ci, int co);
 
 /* trellis_sparse_cpu.c:385-409. */
 void orc_c2s_gather(const float * x, const int32_t * parent, const int32_t * subidx, float * y, int64_t n_out,

@@ -44,6 +44,9 @@ def _load():
         "orc_c2s_map": (c_int, [_i32p, _f32p, c_int64, POINTER(_i32p), POINTER(_i32p), POINTER(_i32p),
                                 POINTER(c_int64)]),
         "orc_free": (None, [c_void_p]),
+        "orc_s2c_map": (c_int, [_i32p, c_int64, POINTER(_i32p), POINTER(_i32p), POINTER(_i32p), POINTER(c_int64)]),
+        "orc_s2c_pack": (None, [_f32p, _i32p, _i32p, _f32p, c_int64, c_int64, c_int]),
+        "orc_s2c_skip_mean": (None, [_f32p, _i32p, _i32p, _f32p, c_int64, c_int64, c_int, c_int]),
         "orc_c2s_gather": (None, [_f32p, _i32p, _i32p, _f32p, c_int64, c_int]),
         "orc_skip_repeat": (None, [_f32p, _i32p, _i32p, _f32p, c_int64, c_int, c_int]),
         "orc_row_norm": (None, [_f32p, _f32p, _f32p, _f32p, c_int64, c_int, c_float, c_int]),
@@ -161,6 +164,40 @@ def c2s_map(coords, logits):
     finally:
         for q in (pc, pp, ps):
             L.orc_free(ctypes.cast(q, c_void_p))
+
+
+def s2c_map(fine_coords):
+    """(rc, coarse [m][4], parent [n], subidx [n]); rc 0 ok, 2 bad input, 4 duplicate."""
+    c = np.ascontiguousarray(fine_coords, dtype=np.int32).reshape(-1, 4)
+    pc, pp, ps, m = _i32p(), _i32p(), _i32p(), c_int64()
+    rc = L.orc_s2c_map(_ip(c), c.shape[0], ctypes.byref(pc), ctypes.byref(pp), ctypes.byref(ps), ctypes.byref(m))
+    if rc != 0:
+        return rc, None, None, None
+    n = c.shape[0]
+    try:
+        return (0, np.ctypeslib.as_array(pc, shape=(m.value, 4)).copy(),
+                np.ctypeslib.as_array(pp, shape=(n,)).copy(), np.ctypeslib.as_array(ps, shape=(n,)).copy())
+    finally:
+        for q in (pc, pp, ps):
+            L.orc_free(ctypes.cast(q, c_void_p))
+
+
+def s2c_pack(x, parent, subidx, n_coarse, co):
+    x = _f(x)
+    p = np.ascontiguousarray(parent, dtype=np.int32)
+    s = np.ascontiguousarray(subidx, dtype=np.int32)
+    y = np.empty((n_coarse, co), dtype=np.float32)
+    L.orc_s2c_pack(_fp(x), _ip(p), _ip(s), _fp(y), p.size, n_coarse, co)
+    return y
+
+
+def s2c_skip_mean(x, parent, subidx, n_coarse, ci, co):
+    x = _f(x)
+    p = np.ascontiguousarray(parent, dtype=np.int32)
+    s = np.ascontiguousarray(subidx, dtype=np.int32)
+    y = np.empty((n_coarse, co), dtype=np.float32)
+    L.orc_s2c_skip_mean(_fp(x), _ip(p), _ip(s), _fp(y), p.size, n_coarse, ci, co)
+    return y
 
 
 def c2s_gather(x, parent, subidx, co):

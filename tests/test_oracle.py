@@ -302,6 +302,122 @@ def test_skip_repeat_matches_repeat_interleave(ci, co):
             assert not np.array_equal(orc.skip_repeat(x, parent, sub, ci, co), exp)
 
 
+# ------------------------------------------------------------ S2C (encoder)
+def s2c_kat():
+    """tests/test_sparse_encoder_backend.c:84-110: five fine voxels (b, x, y, z),
+    their features, the expected coarse voxels, parent and subidx, and the
+    coarse channels the encoder produces with zero conv weights (the skip
+    means, Ci = 2 -> Co = 8, identity input layer)."""
+    coords = np.array([[0, 3, 1, 0], [0, 0, 0, 0], [0, 1, 0, 0], [0, 2, 1, 1], [0, 0, 2, 0]], np.int32)
+    feats = np.array([[2, 4], [1, 3], [-2, 0], [6, 2], [5, -1]], np.float32)
+    exp_coarse = np.array([[0, 0, 0, 0], [0, 0, 1, 0], [0, 1, 0, 0]], np.int32)
+    exp_parent = np.array([2, 0, 0, 2, 1])
+    exp_subidx = np.array([3, 0, 1, 6, 0])
+    exp_channels = np.array([[2, -1, 0, 0, 0, 0, 0, 0], [2, 0, 0, 0, 0, 0, 0, 0], [0, 0, 0, 3, 0, 0, 4, 0]],
+                            np.float32)
+    return coords, feats, exp_coarse, exp_parent, exp_subidx, exp_channels
+
+
+def test_s2c_map_and_skip_mean_known_answer():
+    coords, feats, ec, ep, es, ech = s2c_kat()
+    rc, oc, op, os_ = orc.s2c_map(coords)
+    assert rc == 0
+    assert np.array_equal(oc, ec) and np.array_equal(op, ep) and np.array_equal(os_, es)
+    assert np.array_equal(orc.s2c_skip_mean(feats, op, os_, 3, 2, 8), ech)
+    with orc.mutation(9):  # coarse order z-major
+        rc, oc_bad, _, _ = orc.s2c_map(coords)
+    assert rc == 0 and not np.array_equal(oc_bad, ec)
+    with orc.mutation(10):  # channel-major skip groups
+        assert not np.array_equal(orc.s2c_skip_mean(feats, op, os_, 3, 2, 8), ech)
+
+
+def random_fine_set(rng, n, extent, batches):
+    c = np.stack([rng.integers(0, batches, n), rng.integers(0, extent, n), rng.integers(0, extent, n),
+                  rng.integers(0, extent, n)], axis=1).astype(np.int32)
+    c = np.unique(c, axis=0)
+    return c[rng.permutation(c.shape[0])]
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_s2c_map_matches_numpy_unique(seed):
+    rng = np.random.default_rng(seed)
+    fine = random_fine_set(rng, 3000, 37, 3)
+    coarse_of = fine.copy()
+    coarse_of[:, 1:] //= 2
+    exp_coarse, exp_parent = np.unique(coarse_of, axis=0, return_inverse=True)
+    rc, oc, op, os_ = orc.s2c_map(fine)
+    assert rc == 0
+    assert np.array_equal(oc, exp_coarse) and np.array_equal(op, exp_parent.ravel())
+    assert np.array_equal(os_, (fine[:, 1] & 1) | ((fine[:, 2] & 1) << 1) | ((fine[:, 3] & 1) << 2))
+    with orc.mutation(9):
+        _, oc_bad, _, _ = orc.s2c_map(fine)
+    assert not np.array_equal(oc_bad, exp_coarse)
+
+
+def test_s2c_inverts_c2s():
+    """The S2C of a C2S map recovers the parents that have children, in
+    order, with the C2S parent and subidx of every child."""
+    rng = np.random.default_rng(4)
+    parents = np.unique(np.stack([rng.integers(0, 2, 500), rng.integers(0, 50, 500), rng.integers(0, 50, 500),
+                                  rng.integers(0, 50, 500)], axis=1).astype(np.int32), axis=0)
+    logits = rng.choice([-1.0, 1.0], size=(parents.shape[0], 8)).astype(np.float32)
+    rc, children, cpar, csub = orc.c2s_map(parents, logits)
+    assert rc == 0
+    perm = rng.permutation(children.shape[0])
+    rc, coarse, par, sub = orc.s2c_map(children[perm])
+    assert rc == 0
+    has_child = np.unique(cpar)
+    assert np.array_equal(coarse, parents[has_child])
+    assert np.array_equal(has_child[par], cpar[perm]) and np.array_equal(sub, csub[perm])
+
+
+def test_s2c_rejects_negative_and_duplicate():
+    ok = np.array([[0, 1, 2, 3], [0, 4, 4, 4]], np.int32)
+    assert orc.s2c_map(ok)[0] == 0
+    assert orc.s2c_map(np.array([[0, 1, -2, 3]], np.int32))[0] == 2  # s2c_host.c:61-67
+    assert orc.s2c_map(np.array([[-1, 1, 2, 3]], np.int32))[0] == 2
+    assert orc.s2c_map(np.array([[0, 1, 2, 3], [0, 5, 5, 5], [0, 1, 2, 3]], np.int32))[0] == 4  # :80-88
+
+
+@pytest.mark.parametrize("co", [8, 64, 24])
+def test_s2c_pack_inverted_by_c2s_gather(co):
+    rng = np.random.default_rng(co)
+    fine = random_fine_set(rng, 800, 21, 2)
+    rc, coarse, par, sub = orc.s2c_map(fine)
+    pc = co // 8
+    x = rng.standard_normal((fine.shape[0], pc)).astype(np.float32)
+    packed = orc.s2c_pack(x, par, sub, coarse.shape[0], co)
+    assert np.array_equal(orc.c2s_gather(packed, par, sub, pc), x)
+    filled = np.zeros((coarse.shape[0], 8), bool)
+    filled[par, sub] = True
+    assert not np.any(packed.reshape(coarse.shape[0], 8, pc)[~filled])
+
+
+@pytest.mark.parametrize("ci,co", [(2, 8), (64, 128), (128, 256), (96, 64)])
+def test_s2c_skip_mean_closed_form(ci, co):
+    rng = np.random.default_rng(ci + co)
+    fine = random_fine_set(rng, 600, 17, 2)
+    rc, coarse, par, sub = orc.s2c_map(fine)
+    m, g, pc = coarse.shape[0], 8 * ci // co, co // 8
+    x = rng.standard_normal((fine.shape[0], ci)).astype(np.float32)
+    # Child slot s of a coarse row holds the g-channel group means of that
+    # child, summed left to right in fp32 from zero.
+    exp = np.zeros((m, 8, pc), np.float32)
+    terms = (x / np.float32(g)).reshape(-1, pc, g)
+    acc = np.zeros((fine.shape[0], pc), np.float32)
+    for t in range(g):
+        acc = (acc + terms[:, :, t]).astype(np.float32)
+    exp[par, sub] = acc
+    assert np.array_equal(orc.s2c_skip_mean(x, par, sub, m, ci, co), exp.reshape(m, co))
+    # Groups of equal values come back unchanged through skip_repeat (g = 2^k).
+    if g & (g - 1) == 0:
+        xc = np.repeat(rng.integers(-8, 8, (fine.shape[0], pc)).astype(np.float32), g, axis=1)
+        mean = orc.s2c_skip_mean(xc, par, sub, m, ci, co)
+        assert np.array_equal(orc.skip_repeat(mean, par, sub, co, ci), xc)
+    with orc.mutation(10):
+        assert not np.array_equal(orc.s2c_skip_mean(x, par, sub, m, ci, co), exp.reshape(m, co))
+
+
 # ------------------------------------------------------------------ row ops
 
 def test_row_norm_matches_torch_layer_norm():

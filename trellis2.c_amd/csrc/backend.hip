@@ -805,6 +805,7 @@ void map_release(Backend * be, trellis_sparse_c2s_device_map * m) {
     dev_release(be, &m->coords);
     dev_release(be, &m->parent);
     dev_release(be, &m->subidx);
+    dev_release(be, &m->child);
     delete m;
 }
 
@@ -1052,6 +1053,182 @@ trellis_status op_download_c2s_map(trellis_sparse_backend * backend, const trell
     TSH_TRY(be, hipMemcpyAsync(subidx_out, map->subidx.ptr, (size_t) n * 4, hipMemcpyDeviceToHost, be->stream));
     TSH_TRY(be, hipStreamSynchronize(be->stream));
     return TRELLIS_STATUS_OK;
+}
+
+// ---- S2C downsample (encoder) -------------------------------------------------
+// Radix sort of the coarse keys, heads, scan, emit; two small reads back (the
+// field maxima that size the key, then the coarse count and error flags).
+trellis_status s2c_build(Backend * be, const int32_t * fine_coords_host, const int32_t * fine_coords_dev, int64_t n,
+                         trellis_sparse_c2s_device_map ** fine_out, trellis_sparse_c2s_device_map ** coarse_out) {
+    hipStream_t s = be->stream;
+    auto * fine = new (std::nothrow) trellis_sparse_c2s_device_map();
+    auto * coarse = new (std::nothrow) trellis_sparse_c2s_device_map();
+    if (fine == nullptr || coarse == nullptr) {
+        delete fine;
+        delete coarse;
+        return TRELLIS_STATUS_OUT_OF_MEMORY;
+    }
+    fine->n = n;
+    DevMem flags, klo[2], khi[2], row[2], hist, offs, total, tmp, head, excl;
+    int32_t hf[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    trellis_status st = dev_alloc(be, (size_t) n * 16, &fine->coords);
+    if (st == TRELLIS_STATUS_OK) {
+        const hipMemcpyKind kind = fine_coords_host != nullptr ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
+        const void * src = fine_coords_host != nullptr ? (const void *) fine_coords_host : (const void *) fine_coords_dev;
+        st = hip_status(be, hipMemcpyAsync(fine->coords.ptr, src, (size_t) n * 16, kind, s), "s2c coords");
+    }
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) n * 4, &fine->subidx);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, 32, &flags);
+    const int32_t * coords = (const int32_t *) fine->coords.ptr;
+    if (st == TRELLIS_STATUS_OK) {
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
+        hipError_t err = launch_fill_i32((int32_t *) flags.ptr, 8, 0, s);
+        if (err == hipSuccess) err = launch_s2c_prep(coords, n, (int32_t *) fine->subidx.ptr, (int32_t *) flags.ptr, s);
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
+        if (err == hipSuccess) err = hipMemcpyAsync(hf, flags.ptr, 32, hipMemcpyDeviceToHost, s);
+        if (err == hipSuccess) err = hipStreamSynchronize(s);
+        st = hip_status(be, err, "s2c prep");
+    }
+    if (st == TRELLIS_STATUS_OK && (hf[0] & 1)) {
+        st = fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "s2c: negative coordinate");
+    }
+    int shifts[4] = {0, 0, 0, 0};
+    const int key_bits = s2c_key_shape(hf + 1, shifts);
+    const bool wide = key_bits > 64;
+    const int64_t tiles = s2c_sort_tiles(n);
+    for (int b = 0; b < 2 && st == TRELLIS_STATUS_OK; ++b) {
+        st = dev_alloc(be, (size_t) n * 8, &klo[b]);
+        if (st == TRELLIS_STATUS_OK && wide) st = dev_alloc(be, (size_t) n * 8, &khi[b]);
+        if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) n * 4, &row[b]);
+    }
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) tiles * 256 * 4, &hist);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) tiles * 256 * 4, &offs);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, 16, &total);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, s2c_sort_tmp_bytes(n), &tmp);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) n * 4, &head);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) n * 4, &excl);
+    int cur = 0;
+    int32_t m = 0;
+    if (st == TRELLIS_STATUS_OK) {
+        uint64_t * plo[2] = {(uint64_t *) klo[0].ptr, (uint64_t *) klo[1].ptr};
+        uint64_t * phi[2] = {(uint64_t *) khi[0].ptr, (uint64_t *) khi[1].ptr};
+        int32_t * prow[2] = {(int32_t *) row[0].ptr, (int32_t *) row[1].ptr};
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
+        hipError_t err = launch_s2c_sort(coords, n, shifts, key_bits, plo, phi, prow, (int32_t *) hist.ptr,
+                                         (int32_t *) offs.ptr, (int32_t *) total.ptr, tmp.ptr, &cur, s);
+        if (err == hipSuccess) {
+            err = launch_s2c_heads(plo[cur], wide ? phi[cur] : nullptr, n, (int32_t *) head.ptr,
+                                   (int32_t *) flags.ptr, s);
+        }
+        if (err == hipSuccess) {
+            err = launch_scan_exclusive((const int32_t *) head.ptr, (int32_t *) excl.ptr, n, (int32_t *) total.ptr,
+                                        tmp.ptr, s);
+        }
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
+        if (err == hipSuccess) err = hipMemcpyAsync(hf, flags.ptr, 4, hipMemcpyDeviceToHost, s);
+        if (err == hipSuccess) err = hipMemcpyAsync(&m, total.ptr, 4, hipMemcpyDeviceToHost, s);
+        if (err == hipSuccess) err = hipStreamSynchronize(s);
+        st = hip_status(be, err, "s2c sort");
+    }
+    if (st == TRELLIS_STATUS_OK && (hf[0] & 2)) {
+        st = fail(be, TRELLIS_STATUS_PARSE_ERROR, "s2c: the same fine voxel appears twice");
+    }
+    if (st == TRELLIS_STATUS_OK) {
+        fine->n_parent = m;
+        coarse->n = m;
+        st = dev_alloc(be, (size_t) n * 4, &fine->parent);
+        if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) m * 32, &fine->child);
+        if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) m * 16, &coarse->coords);
+    }
+    if (st == TRELLIS_STATUS_OK) {
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
+        hipError_t err = launch_fill_i32((int32_t *) fine->child.ptr, (int64_t) m * 8, -1, s);
+        if (err == hipSuccess) {
+            err = launch_s2c_emit(coords, (const int32_t *) row[cur].ptr, (const int32_t *) fine->subidx.ptr,
+                                  (const int32_t *) head.ptr, (const int32_t *) excl.ptr, n,
+                                  (int32_t *) fine->parent.ptr, (int32_t *) coarse->coords.ptr,
+                                  (int32_t *) fine->child.ptr, s);
+        }
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
+        st = hip_status(be, err, "s2c emit");
+    }
+    for (DevMem * d : {&flags, &klo[0], &klo[1], &khi[0], &khi[1], &row[0], &row[1], &hist, &offs, &total, &tmp,
+                       &head, &excl}) {
+        dev_release(be, d);
+    }
+    if (st != TRELLIS_STATUS_OK) {
+        map_release(be, fine);
+        map_release(be, coarse);
+        return st;
+    }
+    *fine_out = fine;
+    *coarse_out = coarse;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status s2c_build_impl(trellis_sparse_backend * backend, const int32_t * fine_coords_bxyz,
+                              const trellis_sparse_c2s_device_map * fine_coords_map, int64_t fine_n,
+                              trellis_sparse_c2s_device_map ** fine_map_out,
+                              trellis_sparse_c2s_device_map ** coarse_map_out, int64_t * coarse_n_out) {
+    if (backend == nullptr || fine_map_out == nullptr || coarse_map_out == nullptr || coarse_n_out == nullptr ||
+        (fine_coords_bxyz == nullptr && fine_coords_map == nullptr) || fine_n <= 0 || fine_n > INT32_MAX) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    *fine_map_out = nullptr;
+    *coarse_map_out = nullptr;
+    *coarse_n_out = 0;
+    Backend * be = as_backend(backend);
+    if (fine_coords_map != nullptr && (!map_known(be, fine_coords_map) || fine_coords_map->n != fine_n)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "s2c_build_device: unknown fine_coords_map or n mismatch");
+    }
+    CallScope scope(be);
+    trellis_sparse_c2s_device_map *fine = nullptr, *coarse = nullptr;
+    const trellis_status st =
+        s2c_build(be, fine_coords_map != nullptr ? nullptr : fine_coords_bxyz,
+                  fine_coords_map != nullptr ? (const int32_t *) fine_coords_map->coords.ptr : nullptr, fine_n, &fine,
+                  &coarse);
+    if (st != TRELLIS_STATUS_OK) return st;
+    be->maps.push_back(fine);
+    be->maps.push_back(coarse);
+    *fine_map_out = fine;
+    *coarse_map_out = coarse;
+    *coarse_n_out = coarse->n;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status s2c_pack_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                             const trellis_sparse_c2s_device_map * map, trellis_sparse_buffer * y, int co) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (!map_known(be, map) || map->child.ptr == nullptr || co <= 0 || co % 8 != 0 ||
+        !float_buffer_ok(be, x, (size_t) map->n * (size_t) (co / 8)) ||
+        !float_buffer_ok(be, y, (size_t) map->n_parent * (size_t) co)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "s2c_pack_device: bad argument");
+    }
+    CallScope scope(be);
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+    const hipError_t err = launch_s2c_pack(be->policy.compute_dtype, x->ptr, (const int32_t *) map->child.ptr, y->ptr,
+                                           map->n_parent, co, be->stream);
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+    return hip_status(be, err, "s2c_pack_device");
+}
+
+trellis_status s2c_skip_mean_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                  const trellis_sparse_c2s_device_map * map, trellis_sparse_buffer * y, int ci,
+                                  int co) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (!map_known(be, map) || map->child.ptr == nullptr || ci <= 0 || co <= 0 || co % 8 != 0 ||
+        (8 * (int64_t) ci) % co != 0 || !float_buffer_ok(be, x, (size_t) map->n * (size_t) ci) ||
+        !float_buffer_ok(be, y, (size_t) map->n_parent * (size_t) co)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "s2c_skip_mean_device: bad argument");
+    }
+    CallScope scope(be);
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+    const hipError_t err = launch_s2c_skip_mean(be->policy.compute_dtype, x->ptr, (const int32_t *) map->child.ptr,
+                                                y->ptr, map->n_parent, ci, co, be->stream);
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_BROADCAST);
+    return hip_status(be, err, "s2c_skip_mean_device");
 }
 
 trellis_status op_trim(trellis_sparse_backend * backend, unsigned flags, size_t * released_bytes) {
@@ -1377,6 +1554,28 @@ trellis_status trellis_sparse_hip_free_c2s_map(trellis_sparse_backend * backend,
     tsh::select_device(be);
     tsh::map_release(be, map);
     return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_s2c_build_device(trellis_sparse_backend * backend, const int32_t * fine_coords_bxyz,
+                                                   const trellis_sparse_c2s_device_map * fine_coords_map,
+                                                   int64_t fine_n, trellis_sparse_c2s_device_map ** fine_map_out,
+                                                   trellis_sparse_c2s_device_map ** coarse_map_out,
+                                                   int64_t * coarse_n_out) {
+    return tsh::s2c_build_impl(backend, fine_coords_bxyz, fine_coords_map, fine_n, fine_map_out, coarse_map_out,
+                               coarse_n_out);
+}
+
+trellis_status trellis_sparse_hip_s2c_pack_device(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
+                                                  const trellis_sparse_c2s_device_map * fine_map,
+                                                  trellis_sparse_buffer * y, int co) {
+    return tsh::s2c_pack_impl(backend, x, fine_map, y, co);
+}
+
+trellis_status trellis_sparse_hip_s2c_skip_mean_device(trellis_sparse_backend * backend,
+                                                       const trellis_sparse_buffer * x,
+                                                       const trellis_sparse_c2s_device_map * fine_map,
+                                                       trellis_sparse_buffer * y, int ci, int co) {
+    return tsh::s2c_skip_mean_impl(backend, x, fine_map, y, ci, co);
 }
 
 trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,

@@ -1,0 +1,412 @@
+// kernels_s2c.hip - the encoder's spatial-to-channel downsample (S2C) on the device.
+//
+// Reference semantics:
+//   S2C map   src/architectures/sparse_unet_encoder/s2c_host.c:33-120: the coarse
+//             voxel of fine voxel (b, x, y, z) is (b, x/2, y/2, z/2), its child slot
+//             subidx = (x&1) | (y&1)<<1 | (z&1)<<2; the distinct coarse voxels in
+//             ascending (b, x, y, z) order; parent[f] = coarse row.  Negative
+//             coordinates are rejected; two fine voxels in one child slot are a
+//             parse error.
+//   pack      sparse_unet_encoder/executor.c:279-286: packed[parent][subidx*pc + c]
+//             = x[f][c], pc = co/8, zero where a coarse voxel lacks that child.
+//   skip mean executor.c:287-292: skip[parent][(subidx*ci + c)/g] += x[f][c]/g,
+//             g = 8ci/co, fp32, channels in ascending order from zero.
+//
+// The reference sorts on the host (qsort of the n records by coarse voxel,
+// then fine row).  Here the order comes from a least-significant-digit radix
+// sort of a key holding the coarse voxel in just the bits its coordinates use
+// (b highest, then x/2, y/2, z/2, each field as wide as its largest value)
+// and the child slot in the lowest 3 bits; at most 127 bits, in two words;
+// the fine row is the payload.  Within one coarse voxel the order is by child
+// slot instead of fine row, which changes nothing the map records (parent,
+// subidx and the child table are slot-indexed) and puts the two rows of a
+// repeated fine voxel next to each other, so every repeat is found (the
+// reference compares neighbours in fine-row order and misses a repeat with
+// another child of the same coarse voxel between them).  Per 8-bit pass: a
+// per-tile digit histogram, one exclusive scan over the digit-major
+// [256][tiles] counts, and a stable scatter (ranks within a 64-element round
+// from eight ballots, running per-digit counters per wavefront in LDS).
+// Afterwards head flags, a scan of them and one pass that writes parent,
+// the coarse voxels and the [coarse][8] child table, which makes pack and
+// skip mean plain gathers with coalesced stores.
+#include "tsh_internal.h"
+
+namespace tsh {
+namespace {
+
+constexpr int kSortBlock = 256;                   // threads per sort block (4 wavefronts)
+constexpr int kSortPer = 8;                       // items per thread
+constexpr int kSortTile = kSortBlock * kSortPer;  // items per tile
+constexpr int kWaveItems = 64 * kSortPer;         // contiguous items per wavefront
+
+int grid_for(int64_t count, int block, int cap) {
+    int64_t g = (count + block - 1) / block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (int) g;
+}
+
+// ---------------------------------------------------------------------------
+// Validation, child slot, per-field maxima.  flags[0] bit 0: a negative
+// coordinate; flags[1..4] = max b, max x/2, max y/2, max z/2.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_s2c_prep(const int32_t * __restrict__ coords, int64_t n,
+                                                  int32_t * __restrict__ subidx, int32_t * __restrict__ flags) {
+    int32_t mx[4] = {0, 0, 0, 0};
+    int bad = 0;
+    for (int64_t f = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; f < n; f += (int64_t) gridDim.x * blockDim.x) {
+        const int4 c = *(const int4 *) (coords + 4 * f);
+        bad |= (c.x | c.y | c.z | c.w) < 0;
+        subidx[f] = (c.y & 1) | ((c.z & 1) << 1) | ((c.w & 1) << 2);
+        mx[0] = max(mx[0], c.x);
+        mx[1] = max(mx[1], c.y >> 1);
+        mx[2] = max(mx[2], c.z >> 1);
+        mx[3] = max(mx[3], c.w >> 1);
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) mx[a] = max(mx[a], __shfl_xor(mx[a], d));
+        bad |= __shfl_xor(bad, d);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        if (bad) atomicOr(&flags[0], 1);
+#pragma unroll
+        for (int a = 0; a < 4; ++a) atomicMax(&flags[1 + a], mx[a]);
+    }
+}
+
+// Key fields from the top: b, x/2, y/2, z/2 (widths from the maxima), then
+// the 3-bit child slot at bit 0.
+struct KeyShape {
+    int sh[4];  // left shift of b, x/2, y/2, z/2 in the 128-bit key
+};
+
+__device__ inline void make_key(const int4 c, const KeyShape & ks, uint64_t & lo, uint64_t & hi) {
+    const uint32_t v[4] = {(uint32_t) c.x, (uint32_t) c.y >> 1, (uint32_t) c.z >> 1, (uint32_t) c.w >> 1};
+    lo = (uint64_t) ((c.y & 1) | ((c.z & 1) << 1) | ((c.w & 1) << 2));
+    hi = 0;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        const int s = ks.sh[a];
+        const uint64_t f = v[a];
+        if (s < 64) {
+            lo |= f << s;
+            if (s > 32) hi |= f >> (64 - s);  // the field straddles the word boundary
+        } else {
+            hi |= f << (s - 64);
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) k_s2c_keys(const int32_t * __restrict__ coords, int64_t n, KeyShape ks,
+                                                  uint64_t * __restrict__ klo, uint64_t * __restrict__ khi,
+                                                  int32_t * __restrict__ row) {
+    for (int64_t f = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; f < n; f += (int64_t) gridDim.x * blockDim.x) {
+        uint64_t lo, hi;
+        make_key(*(const int4 *) (coords + 4 * f), ks, lo, hi);
+        klo[f] = lo;
+        if (khi != nullptr) khi[f] = hi;
+        row[f] = (int32_t) f;
+    }
+}
+
+template <bool WIDE> __device__ inline int digit_of(uint64_t lo, uint64_t hi, int shift) {
+    if (WIDE && shift >= 64) return (int) ((hi >> (shift - 64)) & 255u);
+    return (int) ((lo >> shift) & 255u);
+}
+
+// Digit histogram of one tile -> hist[digit * n_tiles + tile].
+template <bool WIDE>
+__global__ void __launch_bounds__(kSortBlock) k_radix_count(const uint64_t * __restrict__ klo,
+                                                            const uint64_t * __restrict__ khi, int64_t n, int shift,
+                                                            int32_t * __restrict__ hist, int n_tiles) {
+    __shared__ int32_t s_cnt[256];
+    s_cnt[threadIdx.x] = 0;
+    __syncthreads();
+    const int64_t base = (int64_t) blockIdx.x * kSortTile;
+#pragma unroll
+    for (int q = 0; q < kSortPer; ++q) {
+        const int64_t i = base + q * kSortBlock + threadIdx.x;
+        if (i < n) atomicAdd(&s_cnt[digit_of<WIDE>(klo[i], WIDE ? khi[i] : 0, shift)], 1);
+    }
+    __syncthreads();
+    hist[(int64_t) threadIdx.x * n_tiles + blockIdx.x] = s_cnt[threadIdx.x];
+}
+
+// Lanes of this wavefront whose digit equals this lane's (valid lanes only).
+__device__ inline uint64_t match_digit(int d, bool valid) {
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const uint64_t set = __ballot((d >> b) & 1);
+        m &= ((d >> b) & 1) ? set : ~set;
+    }
+    return m;
+}
+
+// Stable scatter of one tile: wavefront w owns items [w*512, (w+1)*512) of the
+// tile in 8 rounds of 64 consecutive items; offs = exclusive scan of hist.
+template <bool WIDE>
+__global__ void __launch_bounds__(kSortBlock) k_radix_scatter(const uint64_t * __restrict__ klo,
+                                                              const uint64_t * __restrict__ khi,
+                                                              const int32_t * __restrict__ row, int64_t n, int shift,
+                                                              const int32_t * __restrict__ offs, int n_tiles,
+                                                              uint64_t * __restrict__ olo, uint64_t * __restrict__ ohi,
+                                                              int32_t * __restrict__ orow) {
+    __shared__ int32_t s_cnt[kSortBlock / 64][256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int d = threadIdx.x; d < (kSortBlock / 64) * 256; d += kSortBlock) (&s_cnt[0][0])[d] = 0;
+    __syncthreads();
+    const int64_t wbase = (int64_t) blockIdx.x * kSortTile + (int64_t) wave * kWaveItems;
+    const uint64_t below = (1ull << lane) - 1ull;
+    uint64_t lo[kSortPer], hi[kSortPer];
+    int32_t rw[kSortPer];
+    int dg[kSortPer];
+    // Pass 1: this wavefront's count per digit.
+#pragma unroll
+    for (int q = 0; q < kSortPer; ++q) {
+        const int64_t i = wbase + q * 64 + lane;
+        const bool valid = i < n;
+        lo[q] = valid ? klo[i] : 0;
+        hi[q] = (WIDE && valid) ? khi[i] : 0;
+        rw[q] = valid ? row[i] : 0;
+        dg[q] = digit_of<WIDE>(lo[q], hi[q], shift);
+        const uint64_t m = match_digit(dg[q], valid);
+        if (valid && (m & below) == 0) s_cnt[wave][dg[q]] += __popcll(m);
+    }
+    __syncthreads();
+    // Exclusive prefix over wavefronts plus the tile's global start, per digit.
+    {
+        const int d = threadIdx.x;
+        int32_t run = offs[(int64_t) d * n_tiles + blockIdx.x];
+#pragma unroll
+        for (int w = 0; w < kSortBlock / 64; ++w) {
+            const int32_t c = s_cnt[w][d];
+            s_cnt[w][d] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    // Pass 2: ranks in item order; the lowest lane of each digit group
+    // advances the counter after every lane of the group has read it.
+#pragma unroll
+    for (int q = 0; q < kSortPer; ++q) {
+        const int64_t i = wbase + q * 64 + lane;
+        const bool valid = i < n;
+        const uint64_t m = match_digit(dg[q], valid);
+        if (valid) {
+            const int32_t dst = s_cnt[wave][dg[q]] + __popcll(m & below);
+            olo[dst] = lo[q];
+            if (WIDE) ohi[dst] = hi[q];
+            orow[dst] = rw[q];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (valid && (m & below) == 0) s_cnt[wave][dg[q]] += __popcll(m);
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// head[i] = 1 where sorted key i starts a coarse voxel; flags[0] bit 1 when a
+// whole key repeats (the same fine voxel twice).
+template <bool WIDE>
+__global__ void __launch_bounds__(256) k_s2c_heads(const uint64_t * __restrict__ klo, const uint64_t * __restrict__ khi,
+                                                   int64_t n, int32_t * __restrict__ head, int32_t * __restrict__ flags) {
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t) gridDim.x * blockDim.x) {
+        bool h = true;
+        if (i > 0) {
+            const bool hi_same = !WIDE || khi[i] == khi[i - 1];
+            h = !hi_same || (klo[i] >> 3) != (klo[i - 1] >> 3);
+            if (hi_same && klo[i] == klo[i - 1]) atomicOr(&flags[0], 2);
+        }
+        head[i] = h ? 1 : 0;
+    }
+}
+
+// parent, coarse voxels and the child table; excl = exclusive scan of head.
+__global__ void __launch_bounds__(256) k_s2c_emit(const int32_t * __restrict__ coords, const int32_t * __restrict__ row,
+                                                  const int32_t * __restrict__ subidx,
+                                                  const int32_t * __restrict__ head, const int32_t * __restrict__ excl,
+                                                  int64_t n, int32_t * __restrict__ parent,
+                                                  int32_t * __restrict__ coarse, int32_t * __restrict__ child) {
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t) gridDim.x * blockDim.x) {
+        const int32_t f = row[i];
+        const int32_t c = excl[i] + head[i] - 1;
+        parent[f] = c;
+        child[(int64_t) c * 8 + subidx[f]] = f;
+        if (head[i]) {
+            const int4 v = *(const int4 *) (coords + 4 * (int64_t) f);
+            *(int4 *) (coarse + 4 * (int64_t) c) = int4{v.x, v.y >> 1, v.z >> 1, v.w >> 1};
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Pack and skip mean as gathers over the child table.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ void k_s2c_pack(const typename Store<DT>::T * __restrict__ x, const int32_t * __restrict__ child,
+                           typename Store<DT>::T * __restrict__ y, int64_t m, int co) {
+    const int pc = co / 8;
+    const int64_t count = m * co;
+    for (int64_t e = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; e < count; e += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t c = e / co;
+        const int o = (int) (e - c * co);
+        const int s = o / pc, j = o - s * pc;
+        const int32_t f = child[c * 8 + s];
+        y[e] = f >= 0 ? x[(int64_t) f * pc + j] : (typename Store<DT>::T) 0;
+    }
+}
+
+// 16-byte chunks when a child slot is a whole number of chunks.
+__global__ void k_s2c_pack_vec(const int4 * __restrict__ x, const int32_t * __restrict__ child, int4 * __restrict__ y,
+                               int64_t m, int vpc) {
+    const int64_t count = m * 8 * vpc;
+    for (int64_t e = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; e < count; e += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t slot = e / vpc;  // coarse * 8 + s
+        const int j = (int) (e - slot * vpc);
+        const int32_t f = child[slot];
+        y[e] = f >= 0 ? x[(int64_t) f * vpc + j] : int4{0, 0, 0, 0};
+    }
+}
+
+template <int DT>
+__global__ void k_s2c_skip_mean(const typename Store<DT>::T * __restrict__ x, const int32_t * __restrict__ child,
+                                typename Store<DT>::T * __restrict__ y, int64_t m, int ci, int co) {
+    const int pc = co / 8, g = 8 * ci / co;
+    const float gf = (float) g;
+    const int64_t count = m * co;
+    for (int64_t e = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; e < count; e += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t c = e / co;
+        const int o = (int) (e - c * co);
+        const int s = o / pc, j = o - s * pc;
+        const int32_t f = child[c * 8 + s];
+        float acc = 0.0f;
+        if (f >= 0) {
+            const typename Store<DT>::T * xr = x + (int64_t) f * ci + (int64_t) j * g;
+            for (int t = 0; t < g; ++t) acc += Store<DT>::ld(xr, t) / gf;
+        }
+        Store<DT>::st(y, e, acc);
+    }
+}
+
+}  // namespace
+
+int64_t s2c_sort_tiles(int64_t n) { return (n + kSortTile - 1) / kSortTile; }
+
+size_t s2c_sort_tmp_bytes(int64_t n) {
+    const size_t a = scan_tmp_bytes(256 * s2c_sort_tiles(n)), b = scan_tmp_bytes(n);
+    return a > b ? a : b;
+}
+
+hipError_t launch_s2c_prep(const int32_t * coords, int64_t n, int32_t * subidx, int32_t * flags, hipStream_t s) {
+    if (n <= 0) return hipErrorInvalidValue;
+    k_s2c_prep<<<grid_for(n, 256, 4096), 256, 0, s>>>(coords, n, subidx, flags);
+    return hipGetLastError();
+}
+
+int s2c_key_shape(const int32_t * maxima, int shifts[4]) {
+    int w[4];
+    for (int a = 0; a < 4; ++a) {
+        uint32_t v = (uint32_t) maxima[a];
+        w[a] = 0;
+        while (v != 0) {
+            ++w[a];
+            v >>= 1;
+        }
+    }
+    shifts[3] = 3;
+    shifts[2] = shifts[3] + w[3];
+    shifts[1] = shifts[2] + w[2];
+    shifts[0] = shifts[1] + w[1];
+    return shifts[0] + w[0];
+}
+
+hipError_t launch_s2c_sort(const int32_t * coords, int64_t n, const int shifts[4], int key_bits, uint64_t * klo[2],
+                           uint64_t * khi[2], int32_t * row[2], int32_t * hist, int32_t * offs, int32_t * total,
+                           void * tmp, int * out_buffer, hipStream_t s) {
+    if (n <= 0 || n > 0x7fffffffLL) return hipErrorInvalidValue;
+    const bool wide = key_bits > 64;
+    KeyShape ks;
+    for (int a = 0; a < 4; ++a) ks.sh[a] = shifts[a];
+    k_s2c_keys<<<grid_for(n, 256, 8192), 256, 0, s>>>(coords, n, ks, klo[0], wide ? khi[0] : nullptr, row[0]);
+    hipError_t err = hipGetLastError();
+    const int n_tiles = (int) ((n + kSortTile - 1) / kSortTile);
+    int cur = 0;
+    for (int shift = 0; shift < key_bits && err == hipSuccess; shift += 8) {
+        if (wide) {
+            k_radix_count<true><<<n_tiles, kSortBlock, 0, s>>>(klo[cur], khi[cur], n, shift, hist, n_tiles);
+        } else {
+            k_radix_count<false><<<n_tiles, kSortBlock, 0, s>>>(klo[cur], nullptr, n, shift, hist, n_tiles);
+        }
+        err = hipGetLastError();
+        if (err == hipSuccess) err = launch_scan_exclusive(hist, offs, 256LL * n_tiles, total, tmp, s);
+        if (err != hipSuccess) break;
+        if (wide) {
+            k_radix_scatter<true><<<n_tiles, kSortBlock, 0, s>>>(klo[cur], khi[cur], row[cur], n, shift, offs,
+                                                                 n_tiles, klo[cur ^ 1], khi[cur ^ 1], row[cur ^ 1]);
+        } else {
+            k_radix_scatter<false><<<n_tiles, kSortBlock, 0, s>>>(klo[cur], nullptr, row[cur], n, shift, offs, n_tiles,
+                                                                  klo[cur ^ 1], nullptr, row[cur ^ 1]);
+        }
+        err = hipGetLastError();
+        cur ^= 1;
+    }
+    *out_buffer = cur;
+    return err;
+}
+
+hipError_t launch_s2c_heads(const uint64_t * klo, const uint64_t * khi, int64_t n, int32_t * head, int32_t * flags,
+                            hipStream_t s) {
+    if (khi != nullptr) {
+        k_s2c_heads<true><<<grid_for(n, 256, 8192), 256, 0, s>>>(klo, khi, n, head, flags);
+    } else {
+        k_s2c_heads<false><<<grid_for(n, 256, 8192), 256, 0, s>>>(klo, nullptr, n, head, flags);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_s2c_emit(const int32_t * coords, const int32_t * row, const int32_t * subidx, const int32_t * head,
+                           const int32_t * excl, int64_t n, int32_t * parent, int32_t * coarse, int32_t * child,
+                           hipStream_t s) {
+    k_s2c_emit<<<grid_for(n, 256, 8192), 256, 0, s>>>(coords, row, subidx, head, excl, n, parent, coarse, child);
+    return hipGetLastError();
+}
+
+hipError_t launch_s2c_pack(int dtype, const void * x, const int32_t * child, void * y, int64_t m, int co,
+                           hipStream_t s) {
+    if (m <= 0 || co <= 0 || co % 8 != 0) return hipErrorInvalidValue;
+    const size_t es = dtype_bytes(dtype);
+    const size_t slot_bytes = (size_t) (co / 8) * es;
+    if (slot_bytes % 16 == 0) {
+        const int vpc = (int) (slot_bytes / 16);
+        const int g = grid_for(m * 8 * vpc, 256, 65536);
+        k_s2c_pack_vec<<<g, 256, 0, s>>>((const int4 *) x, child, (int4 *) y, m, vpc);
+        return hipGetLastError();
+    }
+    const int g = grid_for(m * co, 256, 65536);
+    switch (dtype) {
+        case kF32: k_s2c_pack<kF32><<<g, 256, 0, s>>>((const float *) x, child, (float *) y, m, co); break;
+        case kF16: k_s2c_pack<kF16><<<g, 256, 0, s>>>((const _Float16 *) x, child, (_Float16 *) y, m, co); break;
+        default: k_s2c_pack<kBF16><<<g, 256, 0, s>>>((const uint16_t *) x, child, (uint16_t *) y, m, co); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_s2c_skip_mean(int dtype, const void * x, const int32_t * child, void * y, int64_t m, int ci,
+                                int co, hipStream_t s) {
+    if (m <= 0 || ci <= 0 || co <= 0 || co % 8 != 0 || (8 * ci) % co != 0) return hipErrorInvalidValue;
+    const int g = grid_for(m * co, 256, 65536);
+    switch (dtype) {
+        case kF32: k_s2c_skip_mean<kF32><<<g, 256, 0, s>>>((const float *) x, child, (float *) y, m, ci, co); break;
+        case kF16:
+            k_s2c_skip_mean<kF16><<<g, 256, 0, s>>>((const _Float16 *) x, child, (_Float16 *) y, m, ci, co);
+            break;
+        default:
+            k_s2c_skip_mean<kBF16><<<g, 256, 0, s>>>((const uint16_t *) x, child, (uint16_t *) y, m, ci, co);
+            break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace tsh

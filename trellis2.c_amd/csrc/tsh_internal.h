@@ -105,6 +105,7 @@ struct trellis_sparse_c2s_device_map {
     tsh::DevMem coords;  // int32 [n][4]
     tsh::DevMem parent;  // int32 [n]
     tsh::DevMem subidx;  // int32 [n]
+    tsh::DevMem child;   // int32 [n_parent][8] row of each child slot or -1 (maps built by S2C)
 };
 
 namespace tsh {
@@ -175,6 +176,28 @@ void convnext_mlp_groups(int c, int * g0, int * g2);
 hipError_t launch_convnext_mlp(int dtype, const void * x, const float * gamma, const float * beta, const void * w0,
                                const float * b0, const void * w2, const float * b2, const void * res, void * y,
                                int64_t n, int c, float eps, int cus, hipStream_t s);
+// Spatial-to-channel downsample (kernels_s2c.hip).  flags: int32[8], zeroed
+// before prep; prep sets flags[0] bit 0 on a negative coordinate and
+// flags[1..4] to the field maxima; heads sets flags[0] bit 1 on a repeated
+// fine voxel.  The sort ping-pongs between buffers [0] and [1] of klo/khi/row
+// (khi only when key_bits > 64) and reports which holds the result.
+hipError_t launch_s2c_prep(const int32_t * coords, int64_t n, int32_t * subidx, int32_t * flags, hipStream_t s);
+int s2c_key_shape(const int32_t * maxima, int shifts[4]);  // returns the key width in bits
+int64_t s2c_sort_tiles(int64_t n);
+size_t s2c_sort_tmp_bytes(int64_t n);
+hipError_t launch_s2c_sort(const int32_t * coords, int64_t n, const int shifts[4], int key_bits, uint64_t * klo[2],
+                           uint64_t * khi[2], int32_t * row[2], int32_t * hist, int32_t * offs, int32_t * total,
+                           void * tmp, int * out_buffer, hipStream_t s);
+hipError_t launch_s2c_heads(const uint64_t * klo, const uint64_t * khi, int64_t n, int32_t * head, int32_t * flags,
+                            hipStream_t s);
+hipError_t launch_s2c_emit(const int32_t * coords, const int32_t * row, const int32_t * subidx, const int32_t * head,
+                           const int32_t * excl, int64_t n, int32_t * parent, int32_t * coarse, int32_t * child,
+                           hipStream_t s);
+hipError_t launch_s2c_pack(int dtype, const void * x, const int32_t * child, void * y, int64_t m, int co,
+                           hipStream_t s);
+hipError_t launch_s2c_skip_mean(int dtype, const void * x, const int32_t * child, void * y, int64_t m, int ci,
+                                int co, hipStream_t s);
+
 hipError_t launch_c2s_count(int dtype, const void * logits, int64_t n, int32_t * counts, hipStream_t s);
 // Exclusive scan of n int32 values; total written to *total_dev.  tmp needs scan_tmp_bytes(n).
 size_t scan_tmp_bytes(int64_t n);

@@ -108,6 +108,9 @@ ABI = {
     "trellis_sparse_hip_profile_read": (c_int, [_p, POINTER(StageTimes), c_int]),
     "trellis_sparse_hip_event_record": (c_int, [_p, c_int]),
     "trellis_sparse_hip_event_elapsed": (c_int, [_p, c_int, c_int, POINTER(c_float)]),
+    "trellis_sparse_hip_s2c_build_device": (c_int, [_p, _i32p, _p, c_int64, POINTER(_p), POINTER(_p), POINTER(c_int64)]),
+    "trellis_sparse_hip_s2c_pack_device": (c_int, [_p, _p, _p, _p, c_int]),
+    "trellis_sparse_hip_s2c_skip_mean_device": (c_int, [_p, _p, _p, _p, c_int, c_int]),
     "trellis_sparse_hip_convnext_mlp": (c_int, [_p, _p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _p, _p, c_int64,
                                                 c_int, c_float]),
 }
@@ -409,6 +412,27 @@ class Backend:
         self._check(LIB.trellis_sparse_hip_upload_coords(self.ptr, _ptr(c, _i32p), c.shape[0], ctypes.byref(h)),
                     "upload_coords")
         return DeviceMap(h, c.shape[0])
+
+    # -- S2C downsample (encoder) ------------------------------------------------
+    def s2c_build_device(self, coords=None, coords_map: DeviceMap | None = None, n: int | None = None):
+        """(fine_map, coarse_map): the fine level's parent/subidx map and the
+        coarse voxels; from host coordinates or a device coordinates map."""
+        c = None if coords is None else np.ascontiguousarray(coords, dtype=np.int32).reshape(-1, 4)
+        if n is None:
+            n = coords_map.n if coords_map is not None else c.shape[0]
+        hf, hc, m = c_void_p(), c_void_p(), c_int64()
+        self._check(LIB.trellis_sparse_hip_s2c_build_device(self.ptr, _ptr(c, _i32p), None if coords_map is None else
+                                                            coords_map.handle, n, ctypes.byref(hf), ctypes.byref(hc),
+                                                            ctypes.byref(m)), "s2c_build_device")
+        return DeviceMap(hf, n), DeviceMap(hc, m.value)
+
+    def s2c_pack_device(self, x: Buffer, fine_map: DeviceMap, y: Buffer, co: int):
+        self._check(LIB.trellis_sparse_hip_s2c_pack_device(self.ptr, x.handle, fine_map.handle, y.handle, co),
+                    "s2c_pack_device")
+
+    def s2c_skip_mean_device(self, x: Buffer, fine_map: DeviceMap, y: Buffer, ci: int, co: int):
+        self._check(LIB.trellis_sparse_hip_s2c_skip_mean_device(self.ptr, x.handle, fine_map.handle, y.handle, ci, co),
+                    "s2c_skip_mean_device")
 
     def free_map(self, dmap: DeviceMap):
         self._check(LIB.trellis_sparse_hip_free_c2s_map(self.ptr, dmap.handle), "free_c2s_map")
