@@ -142,6 +142,12 @@ class Block:
       (src/architectures/sparse_unet_decoder/executor.c:176-255).
     convnext_fused: the same block with its tail (row_norm .. add) in the one
       fused entry point trellis_sparse_hip_convnext_mlp.
+    s2c: the encoder's S2C down-block on the ~1.26M config-3 children, Ci = 64 -> Co = 128
+      (sparse_unet_encoder/executor.c:160-360): row_norm_silu -> conv(64->16) on the fine
+      rulebook; S2C map, pack and skip mean on the device (the reference does these on
+      the host, s2c_host.c:33-120, executor.c:258-300); coarse rulebook; row_norm_silu
+      -> conv(128->128) on the coarse voxels -> add(skip).  The line also carries the
+      CPU oracle's S2C map time on the same voxels.
     c2s: the C2S up-block on the ~0.32M config-3 parents, Ci = 256 -> Co = 128:
       linear(256->8) logits -> build_c2s_map_device -> build_rulebook_for_c2s_map;
       row_norm_silu -> conv(256->1024) on the parents -> c2s_gather_device;
@@ -176,6 +182,35 @@ class Block:
             self.slots = ["sparse_conv3d", "row_norm", "linear_silu", "linear", "add"]
             if kind == "convnext_fused":
                 self.slots = ["sparse_conv3d", "convnext_mlp"]
+        elif kind == "s2c":
+            ci, co = 64, 128
+            self.ci, self.co = ci, co
+            pmap = be.upload_coords(w["parent_coords"])
+            dm = be.build_c2s_map_device(be.upload(w["logits"]), w["parent_coords"].shape[0], coords_map=pmap)
+            self.fine_map, self.n = dm, dm.n
+            self.frb = be.build_rulebook_for_c2s_map(dm)
+            self.fpairs = be.rulebook_stats(self.frb)["pairs"]
+            self.h = be.upload(rng.standard_normal((self.n, ci)).astype(np.float32))
+            self.g1 = be.keep(f32(1 + 0.1 * rng.standard_normal(ci)))
+            self.b1 = be.keep(f32(0.1 * rng.standard_normal(ci)))
+            self.w1 = be.keep(f32(rng.standard_normal((co // 8, 27, ci)) / np.sqrt(27 * ci)))
+            self.c1b = be.keep(f32(0.1 * rng.standard_normal(co // 8)))
+            self.w2 = be.keep(f32(rng.standard_normal((co, 27, co)) / np.sqrt(27 * co)))
+            self.c2b = be.keep(f32(0.1 * rng.standard_normal(co)))
+            self.norm1 = be.alloc(self.n * ci)
+            self.conv1 = be.alloc(self.n * (co // 8))
+            fmap, cmap = be.s2c_build_device(coords_map=dm)
+            self.m = cmap.n
+            crb = be.build_rulebook_for_c2s_map(cmap)
+            self.pairs = be.rulebook_stats(crb)["pairs"]
+            crb.free()
+            self.fine_coords = be.download_c2s_coords(dm)
+            be.free_map(fmap)
+            be.free_map(cmap)
+            self.bufs = [be.alloc(self.m * co) for _ in range(5)]
+            self.slots = ["row_norm_silu_pre", "sparse_conv3d_pre", "s2c_build_device", "s2c_pack_device",
+                          "s2c_skip_mean_device", "build_rulebook_for_c2s_map", "row_norm_silu_post",
+                          "sparse_conv3d_post", "add"]
         else:
             ci, co = 256, 128
             self.ci, self.co = ci, co
@@ -211,6 +246,31 @@ class Block:
         be = self.be
         ev = iter(range(1, 16))
         be.event(0)
+        if self.kind == "s2c":
+            n, ci, co, m = self.n, self.ci, self.co, self.m
+            packed, skip, norm2, conv2, out = self.bufs
+            be.row_norm(self.h, self.g1, self.b1, self.norm1, n, ci, 1e-6, silu=True)
+            be.event(next(ev))
+            be.conv(self.frb, self.norm1, self.w1, self.c1b, self.conv1, ci, co // 8)
+            be.event(next(ev))
+            fmap, cmap = be.s2c_build_device(coords_map=self.fine_map)
+            be.event(next(ev))
+            be.s2c_pack_device(self.conv1, fmap, packed, co)
+            be.event(next(ev))
+            be.s2c_skip_mean_device(self.h, fmap, skip, ci, co)
+            be.event(next(ev))
+            rb = be.build_rulebook_for_c2s_map(cmap)
+            be.event(next(ev))
+            be.row_norm(packed, None, None, norm2, m, co, 1e-6, silu=True)
+            be.event(next(ev))
+            be.conv(rb, norm2, self.w2, self.c2b, conv2, co, co)
+            be.event(next(ev))
+            be.add(conv2, skip, out, m * co)
+            be.event(next(ev))
+            rb.free()
+            be.free_map(fmap)
+            be.free_map(cmap)
+            return
         if self.kind == "convnext_fused":
             conv, out = self.bufs[0], self.bufs[4]
             be.conv(self.rb, self.h, self.conv_w, self.conv_b, conv, self.c, self.c)
@@ -259,6 +319,8 @@ class Block:
         be.free_map(dm)
 
     def flops(self):
+        if self.kind == "s2c":
+            return wl.conv_flops(self.fpairs, self.ci, self.co // 8) + wl.conv_flops(self.pairs, self.co, self.co)
         if self.kind in ("convnext", "convnext_fused"):
             n, c = self.n, self.c
             return wl.conv_flops(self.pairs, c, c) + 2 * (2 * n * c * 4 * c)
@@ -286,7 +348,21 @@ def run_block(args):
            "steps": args.steps, "warmup": args.warmup, "ms_per_block": round(dev, 4),
            "wall_ms_per_block": round(wall, 4), "effective_tflops": round(job.flops() / (dev * 1e-3) / 1e12, 2),
            "slot_ms": slots}
-    if args.block in ("convnext", "convnext_fused"):
+    if args.block == "s2c":
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle_lib as orc
+
+        t0 = time.perf_counter()
+        rc, coarse, _, _ = orc.s2c_map(job.fine_coords)
+        cpu_ms = (time.perf_counter() - t0) * 1e3
+        assert rc == 0 and coarse.shape[0] == job.m
+        map_ms = slots["s2c_build_device"]
+        out.update({"fine_voxels": int(job.n), "coarse_voxels": int(job.m), "fine_pairs": int(job.fpairs),
+                    "coarse_pairs": int(job.pairs), "ci": job.ci, "co": job.co,
+                    "s2c_map_mvoxels_per_s": round(job.n / (map_ms * 1e-3) / 1e6, 1),
+                    "s2c_map_cpu_oracle_ms": round(cpu_ms, 2),
+                    "s2c_map_cpu_note": "oracle/trellis_oracle.c orc_s2c_map (qsort, 1 thread), same fine voxels"})
+    elif args.block in ("convnext", "convnext_fused"):
         out.update({"voxels": int(job.n), "pairs": int(job.pairs), "channels": job.c})
     else:
         out.update({"parents": int(job.n), "children": int(job.m), "parent_pairs": int(job.ppairs),
@@ -355,7 +431,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-stride", type=int, default=16)
     ap.add_argument("--conv-algo", type=int, default=sh.CONV_AUTO)
-    ap.add_argument("--block", choices=["convnext", "convnext_fused", "c2s"],
+    ap.add_argument("--block", choices=["convnext", "convnext_fused", "c2s", "s2c"],
                     help="instead of the configuration step, time one decoder block composed from the backend's "
                          "slots at config-3 scale and print its own JSON line")
     ap.add_argument("--calibrate", action="store_true",

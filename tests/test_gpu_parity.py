@@ -227,6 +227,27 @@ def test_conv_mfma_ragged_rows(be_sched, algo, n):
     assert err <= 2e-2
 
 
+@pytest.mark.parametrize("algo", ["compact", "masked"])
+@pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])
+@pytest.mark.parametrize("ci,co,n", [(64, 16, 14648), (128, 32, 14648), (256, 32, 5000), (32, 16, 300),
+                                     (64, 16, 1), (64, 32, 129)])
+def test_conv_narrow_output_vs_oracle(be_sched, algo, dtype, ci, co, n):
+    """16 and 32 output channels (the encoder's S2C conv to co/8 channels):
+    the masked MFMA schedule with all four wavefronts on rows (the compacted
+    one needs 64-channel multiples and hands these over); ragged row counts."""
+    be = be_sched[(algo, dtype)]
+    c = wl.make_coords(1)[:n]
+    rng = np.random.default_rng(ci * 3 + co + n + dtype)
+    x = sh.storage_round(rng.standard_normal((c.shape[0], ci)).astype(np.float32), dtype)
+    w = (rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci)).astype(np.float32)
+    bias = rng.standard_normal(co).astype(np.float32) * 0.1
+    got = run_conv(be, c, x, w, bias, ci, co)
+    exp = orc.Rulebook(c).conv(x, sh.storage_round(w, dtype), bias, ci, co)
+    err = max_rel_err(got, exp)
+    say(f"narrow {algo} dtype={dtype} ci={ci} co={co} n={n} max_rel_err={err:.3e}")
+    assert err <= TOL[dtype]
+
+
 def test_conv_generic_small_channels_all_dtypes(be32, be16, bebf):
     coords, feats, w, bias, ci, co = small_conv_cases()["direct"]
     for dtype in (sh.F16, sh.BF16):

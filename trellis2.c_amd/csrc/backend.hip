@@ -1069,7 +1069,7 @@ trellis_status s2c_build(Backend * be, const int32_t * fine_coords_host, const i
         return TRELLIS_STATUS_OUT_OF_MEMORY;
     }
     fine->n = n;
-    DevMem flags, klo[2], khi[2], row[2], hist, offs, total, tmp, head, excl;
+    DevMem flags, part, klo[2], khi[2], row[2], hist, offs, total, tmp, head, excl;
     int32_t hf[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     trellis_status st = dev_alloc(be, (size_t) n * 16, &fine->coords);
     if (st == TRELLIS_STATUS_OK) {
@@ -1079,11 +1079,12 @@ trellis_status s2c_build(Backend * be, const int32_t * fine_coords_host, const i
     }
     if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) n * 4, &fine->subidx);
     if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, 32, &flags);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, s2c_prep_part_bytes(), &part);
     const int32_t * coords = (const int32_t *) fine->coords.ptr;
     if (st == TRELLIS_STATUS_OK) {
         stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
-        hipError_t err = launch_fill_i32((int32_t *) flags.ptr, 8, 0, s);
-        if (err == hipSuccess) err = launch_s2c_prep(coords, n, (int32_t *) fine->subidx.ptr, (int32_t *) flags.ptr, s);
+        hipError_t err = launch_s2c_prep(coords, n, (int32_t *) fine->subidx.ptr, (int32_t *) part.ptr,
+                                         (int32_t *) flags.ptr, s);
         stage_end(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
         if (err == hipSuccess) err = hipMemcpyAsync(hf, flags.ptr, 32, hipMemcpyDeviceToHost, s);
         if (err == hipSuccess) err = hipStreamSynchronize(s);
@@ -1152,7 +1153,7 @@ trellis_status s2c_build(Backend * be, const int32_t * fine_coords_host, const i
         stage_end(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
         st = hip_status(be, err, "s2c emit");
     }
-    for (DevMem * d : {&flags, &klo[0], &klo[1], &khi[0], &khi[1], &row[0], &row[1], &hist, &offs, &total, &tmp,
+    for (DevMem * d : {&flags, &part, &klo[0], &klo[1], &khi[0], &khi[1], &row[0], &row[1], &hist, &offs, &total, &tmp,
                        &head, &excl}) {
         dev_release(be, d);
     }

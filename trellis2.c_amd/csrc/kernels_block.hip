@@ -34,39 +34,6 @@
 namespace tsh {
 namespace {
 
-template <int DT> __device__ inline typename Store<DT>::T to_store(float v) {
-    if constexpr (DT == kBF16) {
-        return __builtin_bit_cast(uint16_t, (__bf16) v);  // round to nearest even
-    } else {
-        return (typename Store<DT>::T) v;
-    }
-}
-
-// The 8 storage values of a 16-byte chunk as fp32.
-template <int DT> __device__ inline void unpack8(const int4 & c, float * v) {
-    const uint32_t w[4] = {(uint32_t) c.x, (uint32_t) c.y, (uint32_t) c.z, (uint32_t) c.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        if constexpr (DT == kBF16) {
-            v[2 * k] = __builtin_bit_cast(float, w[k] << 16);
-            v[2 * k + 1] = __builtin_bit_cast(float, w[k] & 0xffff0000u);
-        } else {
-            v[2 * k] = (float) __builtin_bit_cast(_Float16, (uint16_t) (w[k] & 0xffffu));
-            v[2 * k + 1] = (float) __builtin_bit_cast(_Float16, (uint16_t) (w[k] >> 16));
-        }
-    }
-}
-
-template <int DT> __device__ inline int4 pack8(const float * v) {
-    union {
-        int4 c;
-        typename Store<DT>::T h[8];
-    } u;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) u.h[k] = to_store<DT>(v[k]);
-    return u.c;
-}
-
 template <int DT, int C>
 __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::T * __restrict__ x,
                                                       const float * __restrict__ gamma,
@@ -157,7 +124,7 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
         for (int p = 0; p < LNP; ++p) {
             const int rloc = wave * 8 + p * RPP + lane / LPR;
             float v[8];
-            unpack8<DT>(xr[p], v);
+            unpack_chunk<DT>(xr[p], v);
             float s = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) s += v[e];
@@ -176,7 +143,7 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = v[e] * inv * gv[e] + bv[e];
             // Channels li*8 .. li*8+7 of row rloc: one operand granule.
-            *(int4 *) (&s_x[opnd(li / 4, rloc / 16, rloc % 16, li % 4)]) = pack8<DT>(v);
+            *(int4 *) (&s_x[opnd(li / 4, rloc / 16, rloc % 16, li % 4)]) = pack_chunk<DT>(v);
         }
     };
     // Bias, SiLU and rounding of GEMM 1 row block q: the lane's hidden
@@ -192,7 +159,7 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
             for (int nt = 0; nt < NT1; ++nt) {
                 float v = a[nt][i] + bias1[nt];
                 v = v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
-                o[nt] = to_store<DT>(v);
+                o[nt] = round_to_store<DT>(v);
             }
             *(Hv *) (&s_h[opnd(h0 / 32, q, lg * 4 + i, (h0 % 32) / 8) + h0 % 8]) = o;
         }
@@ -276,7 +243,7 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
                     const int r = (rh + 2 * q) * 16 + lg * 4 + i;
                     Ov o;
 #pragma unroll
-                    for (int nt = 0; nt < NT2; ++nt) o[nt] = to_store<DT>(acc[q][nt][i] + bias2[nt]);
+                    for (int nt = 0; nt < NT2; ++nt) o[nt] = round_to_store<DT>(acc[q][nt][i] + bias2[nt]);
                     *(Ov *) (&s_o[r * OSTR + c0]) = o;
                 }
         }
@@ -290,11 +257,11 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
             const int64_t row = row0 + r;
             if (row >= n) continue;
             float a[8], b[8];
-            unpack8<DT>(rr[p], a);
-            unpack8<DT>(*(const int4 *) (&s_o[r * OSTR + j * 8]), b);
+            unpack_chunk<DT>(rr[p], a);
+            unpack_chunk<DT>(*(const int4 *) (&s_o[r * OSTR + j * 8]), b);
 #pragma unroll
             for (int k = 0; k < 8; ++k) a[k] += b[k];
-            *(int4 *) (y + row * C + j * 8) = pack8<DT>(a);
+            *(int4 *) (y + row * C + j * 8) = pack_chunk<DT>(a);
         }
     }
 }

@@ -138,7 +138,11 @@ __global__ void __launch_bounds__(256) k_conv_generic(const typename Store<DT>::
 // ---------------------------------------------------------------------------
 // MFMA kernel (bf16 / fp16 storage).
 // ---------------------------------------------------------------------------
-template <int DT, int BN>
+// WR wavefronts split the rows (32 each), 4/WR the BN channels: WR = 2 for
+// 64/128-channel blocks, WR = 4 for the narrow outputs (16 or 32 channels,
+// e.g. the encoder's S2C conv to co/8 channels), whose one column group is
+// the whole output.
+template <int DT, int BN, int WR>
 __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<DT>::T * __restrict__ x,
                                                           const int32_t * __restrict__ nbr,
                                                           const uint32_t * __restrict__ mask,
@@ -147,13 +151,14 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
                                                           typename Store<DT>::T * __restrict__ y, int64_t n, int ci,
                                                           int co, int64_t n_col_tiles) {
     using V = typename Mfma<DT>::V;
-    constexpr int BM = 64;
-    constexpr int WN = BN / 2;      // channels per wavefront
-    constexpr int NT = WN / 16;     // 16-wide MFMA column tiles per wavefront
+    constexpr int BM = 32 * WR;
+    constexpr int WN = BN / (4 / WR);  // channels per wavefront
+    constexpr int NT = WN / 16;        // 16-wide MFMA column tiles per wavefront
+    static_assert(NT >= 1 && WN % 16 == 0, "column split");
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const int wr = wave & 1, wc = wave >> 1;
+    const int wr = wave % WR, wc = wave / WR;
     const int64_t grid = (int64_t) gridDim.x;
     const int64_t logical = xcd_remap(blockIdx.x, grid);
     const int64_t row_tile = logical / n_col_tiles;
@@ -920,7 +925,8 @@ hipError_t launch_conv_generic(int dtype, const void * x, const int32_t * nbr, c
 }
 
 bool conv_mfma_supported(int dtype, int ci, int co) {
-    return (dtype == kF16 || dtype == kBF16) && ci > 0 && co > 0 && ci % 32 == 0 && co % 64 == 0;
+    return (dtype == kF16 || dtype == kBF16) && ci > 0 && co > 0 && ci % 32 == 0 &&
+           (co % 64 == 0 || co == 16 || co == 32);
 }
 
 hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nbr, const uint32_t * mask,
@@ -929,23 +935,28 @@ hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nb
     if (!conv_mfma_supported(dtype, ci, co)) {
         return hipErrorInvalidValue;
     }
-    const int bn = (co % 128 == 0) ? 128 : 64;
-    const int64_t row_tiles = (n + 63) / 64;
+    const int bn = (co % 128 == 0) ? 128 : (co % 64 == 0 ? 64 : co);
+    const int bm = bn >= 64 ? 64 : 128;
+    const int64_t row_tiles = (n + bm - 1) / bm;
     const int64_t col_tiles = co / bn;
     const int64_t grid = row_tiles * col_tiles;
     if (grid > 0x7fffffffLL) {
         return hipErrorInvalidValue;
     }
-#define TSH_LAUNCH(DTV, TYPE, BNV)                                                                           \
-    k_conv_mfma_masked<DTV, BNV><<<(unsigned) grid, 256, 0, s>>>((const TYPE *) x, nbr, mask,               \
-                                                                  (const TYPE *) w16, bias, (TYPE *) y, n, ci, \
-                                                                  co, col_tiles)
+#define TSH_LAUNCH(DTV, TYPE, BNV, WRV)                                                                       \
+    k_conv_mfma_masked<DTV, BNV, WRV><<<(unsigned) grid, 256, 0, s>>>((const TYPE *) x, nbr, mask,               \
+                                                                       (const TYPE *) w16, bias, (TYPE *) y, n, ci, \
+                                                                       co, col_tiles)
     if (dtype == kBF16) {
-        if (bn == 128) TSH_LAUNCH(kBF16, uint16_t, 128);
-        else TSH_LAUNCH(kBF16, uint16_t, 64);
+        if (bn == 128) TSH_LAUNCH(kBF16, uint16_t, 128, 2);
+        else if (bn == 64) TSH_LAUNCH(kBF16, uint16_t, 64, 2);
+        else if (bn == 32) TSH_LAUNCH(kBF16, uint16_t, 32, 4);
+        else TSH_LAUNCH(kBF16, uint16_t, 16, 4);
     } else {
-        if (bn == 128) TSH_LAUNCH(kF16, _Float16, 128);
-        else TSH_LAUNCH(kF16, _Float16, 64);
+        if (bn == 128) TSH_LAUNCH(kF16, _Float16, 128, 2);
+        else if (bn == 64) TSH_LAUNCH(kF16, _Float16, 64, 2);
+        else if (bn == 32) TSH_LAUNCH(kF16, _Float16, 32, 4);
+        else TSH_LAUNCH(kF16, _Float16, 16, 4);
     }
 #undef TSH_LAUNCH
     return hipGetLastError();
@@ -962,7 +973,7 @@ int conv_stream_group(int co) {
 bool conv_stream_supported(int dtype, int ci, int co) {
     // A unit (Ci/32 K steps) spans a whole number of 4-step blocks, or two
     // units (Ci = 64) make one block.
-    return conv_mfma_supported(dtype, ci, co) && (ci % 128 == 0 || ci == 64);
+    return conv_mfma_supported(dtype, ci, co) && co % 64 == 0 && (ci % 128 == 0 || ci == 64);
 }
 
 namespace {

@@ -47,11 +47,16 @@ int grid_for(int64_t count, int block, int cap) {
 }
 
 // ---------------------------------------------------------------------------
-// Validation, child slot, per-field maxima.  flags[0] bit 0: a negative
-// coordinate; flags[1..4] = max b, max x/2, max y/2, max z/2.
+// Validation, child slot, per-field maxima: each block writes its
+// {negative seen, max b, max x/2, max y/2, max z/2} to part[block][0..4];
+// k_s2c_prep_reduce folds them into flags[0..4] (flags[0] bit 0: a negative
+// coordinate).  No atomics: thousands of them on five words serialise.
 // ---------------------------------------------------------------------------
+constexpr int kPrepBlocks = 1024;
+
 __global__ void __launch_bounds__(256) k_s2c_prep(const int32_t * __restrict__ coords, int64_t n,
-                                                  int32_t * __restrict__ subidx, int32_t * __restrict__ flags) {
+                                                  int32_t * __restrict__ subidx, int32_t * __restrict__ part) {
+    __shared__ int32_t s_red[4][5];
     int32_t mx[4] = {0, 0, 0, 0};
     int bad = 0;
     for (int64_t f = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; f < n; f += (int64_t) gridDim.x * blockDim.x) {
@@ -69,11 +74,27 @@ __global__ void __launch_bounds__(256) k_s2c_prep(const int32_t * __restrict__ c
         for (int a = 0; a < 4; ++a) mx[a] = max(mx[a], __shfl_xor(mx[a], d));
         bad |= __shfl_xor(bad, d);
     }
+    const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
-        if (bad) atomicOr(&flags[0], 1);
+        s_red[wave][0] = bad;
 #pragma unroll
-        for (int a = 0; a < 4; ++a) atomicMax(&flags[1 + a], mx[a]);
+        for (int a = 0; a < 4; ++a) s_red[wave][1 + a] = mx[a];
     }
+    __syncthreads();
+    if (threadIdx.x < 5) {
+        int32_t v = s_red[0][threadIdx.x];
+        for (int w = 1; w < 4; ++w) v = threadIdx.x == 0 ? (v | s_red[w][0]) : max(v, s_red[w][threadIdx.x]);
+        part[blockIdx.x * 5 + threadIdx.x] = v;
+    }
+}
+
+__global__ void __launch_bounds__(64) k_s2c_prep_reduce(const int32_t * __restrict__ part, int blocks,
+                                                        int32_t * __restrict__ flags) {
+    const int a = threadIdx.x;
+    if (a >= 5) return;
+    int32_t v = 0;
+    for (int b = 0; b < blocks; ++b) v = a == 0 ? (v | part[b * 5]) : max(v, part[b * 5 + a]);
+    flags[a] = v;
 }
 
 // Key fields from the top: b, x/2, y/2, z/2 (widths from the maxima), then
@@ -290,6 +311,38 @@ __global__ void k_s2c_skip_mean(const typename Store<DT>::T * __restrict__ x, co
     }
 }
 
+// Eight consecutive outputs of one child slot per thread (co % 64 == 0,
+// g <= 8): their 8g inputs are contiguous, read as 16-byte chunks, summed in
+// the same order as above; one 16-byte store.
+template <int DT, int G>
+__global__ void k_s2c_skip_mean_vec(const typename Store<DT>::T * __restrict__ x, const int32_t * __restrict__ child,
+                                    typename Store<DT>::T * __restrict__ y, int64_t m, int ci, int co) {
+    using T = typename Store<DT>::T;
+    constexpr int CHUNKS = 8 * G * (int) sizeof(T) / 16;
+    constexpr int PER = 16 / (int) sizeof(T);  // values per chunk
+    const int pc = co / 8, v8 = co / 8;        // v8 = groups of 8 outputs per row
+    const float gf = (float) G;
+    const int64_t count = m * v8;
+    for (int64_t e = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; e < count; e += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t c = e / v8;
+        const int o0 = (int) (e - c * v8) * 8;  // first output column
+        const int s = o0 / pc, j0 = o0 - s * pc;
+        const int32_t f = child[c * 8 + s];
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (f >= 0) {
+            const int4 * src = (const int4 *) (x + (int64_t) f * ci + (int64_t) j0 * G);
+            float v[CHUNKS * PER];
+#pragma unroll
+            for (int q = 0; q < CHUNKS; ++q) unpack_chunk<DT>(src[q], v + q * PER);
+#pragma unroll
+            for (int t = 0; t < G; ++t)
+#pragma unroll
+                for (int o = 0; o < 8; ++o) acc[o] += v[o * G + t] / gf;
+        }
+        *(int4 *) (y + c * co + o0) = pack_chunk<DT>(acc);
+    }
+}
+
 }  // namespace
 
 int64_t s2c_sort_tiles(int64_t n) { return (n + kSortTile - 1) / kSortTile; }
@@ -299,9 +352,14 @@ size_t s2c_sort_tmp_bytes(int64_t n) {
     return a > b ? a : b;
 }
 
-hipError_t launch_s2c_prep(const int32_t * coords, int64_t n, int32_t * subidx, int32_t * flags, hipStream_t s) {
+size_t s2c_prep_part_bytes() { return (size_t) kPrepBlocks * 5 * sizeof(int32_t); }
+
+hipError_t launch_s2c_prep(const int32_t * coords, int64_t n, int32_t * subidx, int32_t * part, int32_t * flags,
+                           hipStream_t s) {
     if (n <= 0) return hipErrorInvalidValue;
-    k_s2c_prep<<<grid_for(n, 256, 4096), 256, 0, s>>>(coords, n, subidx, flags);
+    const int g = grid_for(n, 256, kPrepBlocks);
+    k_s2c_prep<<<g, 256, 0, s>>>(coords, n, subidx, part);
+    k_s2c_prep_reduce<<<1, 64, 0, s>>>(part, g, flags);
     return hipGetLastError();
 }
 
@@ -396,6 +454,23 @@ hipError_t launch_s2c_pack(int dtype, const void * x, const int32_t * child, voi
 hipError_t launch_s2c_skip_mean(int dtype, const void * x, const int32_t * child, void * y, int64_t m, int ci,
                                 int co, hipStream_t s) {
     if (m <= 0 || ci <= 0 || co <= 0 || co % 8 != 0 || (8 * ci) % co != 0) return hipErrorInvalidValue;
+    const int grp = 8 * ci / co;
+    if (dtype != kF32 && co % 64 == 0 && (grp == 2 || grp == 4 || grp == 8)) {
+        const int gv = grid_for(m * (co / 8), 256, 65536);
+#define TSH_SKIP(DTV, TYPE, GV) \
+    k_s2c_skip_mean_vec<DTV, GV><<<gv, 256, 0, s>>>((const TYPE *) x, child, (TYPE *) y, m, ci, co)
+        if (dtype == kBF16) {
+            if (grp == 2) TSH_SKIP(kBF16, uint16_t, 2);
+            else if (grp == 4) TSH_SKIP(kBF16, uint16_t, 4);
+            else TSH_SKIP(kBF16, uint16_t, 8);
+        } else {
+            if (grp == 2) TSH_SKIP(kF16, _Float16, 2);
+            else if (grp == 4) TSH_SKIP(kF16, _Float16, 4);
+            else TSH_SKIP(kF16, _Float16, 8);
+        }
+#undef TSH_SKIP
+        return hipGetLastError();
+    }
     const int g = grid_for(m * co, 256, 65536);
     switch (dtype) {
         case kF32: k_s2c_skip_mean<kF32><<<g, 256, 0, s>>>((const float *) x, child, (float *) y, m, ci, co); break;

@@ -51,6 +51,42 @@ template <> struct Store<kBF16> {
     __device__ static void st(T * p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
 };
 
+// A 16-byte chunk of 16-bit storage values (8 of them) to fp32 and back,
+// with round-to-nearest-even on the way back.
+template <int DT> __device__ inline void unpack_chunk(const int4 & c, float * v) {
+    static_assert(DT != kF32, "16-bit storage");
+    const uint32_t w[4] = {(uint32_t) c.x, (uint32_t) c.y, (uint32_t) c.z, (uint32_t) c.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if constexpr (DT == kBF16) {
+            v[2 * k] = __builtin_bit_cast(float, w[k] << 16);
+            v[2 * k + 1] = __builtin_bit_cast(float, w[k] & 0xffff0000u);
+        } else {
+            v[2 * k] = (float) __builtin_bit_cast(_Float16, (uint16_t) (w[k] & 0xffffu));
+            v[2 * k + 1] = (float) __builtin_bit_cast(_Float16, (uint16_t) (w[k] >> 16));
+        }
+    }
+}
+
+template <int DT> __device__ inline typename Store<DT>::T round_to_store(float v) {
+    if constexpr (DT == kBF16) {
+        return __builtin_bit_cast(uint16_t, (__bf16) v);
+    } else {
+        return (typename Store<DT>::T) v;
+    }
+}
+
+template <int DT> __device__ inline int4 pack_chunk(const float * v) {
+    static_assert(DT != kF32, "16-bit storage");
+    union {
+        int4 c;
+        typename Store<DT>::T h[8];
+    } u;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) u.h[k] = round_to_store<DT>(v[k]);
+    return u.c;
+}
+
 // Work split of a rulebook build / conv: rows per tile of the kernel map.
 constexpr int kMapTile = 256;
 constexpr int kBrickCells = 64;  // 4x4x4 cells per brick
@@ -176,12 +212,14 @@ void convnext_mlp_groups(int c, int * g0, int * g2);
 hipError_t launch_convnext_mlp(int dtype, const void * x, const float * gamma, const float * beta, const void * w0,
                                const float * b0, const void * w2, const float * b2, const void * res, void * y,
                                int64_t n, int c, float eps, int cus, hipStream_t s);
-// Spatial-to-channel downsample (kernels_s2c.hip).  flags: int32[8], zeroed
-// before prep; prep sets flags[0] bit 0 on a negative coordinate and
-// flags[1..4] to the field maxima; heads sets flags[0] bit 1 on a repeated
-// fine voxel.  The sort ping-pongs between buffers [0] and [1] of klo/khi/row
+// Spatial-to-channel downsample (kernels_s2c.hip).  flags: int32[8]; prep
+// (scratch part of s2c_prep_part_bytes()) sets flags[0] to 1 or 0 (a
+// negative coordinate) and flags[1..4] to the field maxima; heads sets
+// flags[0] bit 1 on a repeated fine voxel.  The sort ping-pongs between buffers [0] and [1] of klo/khi/row
 // (khi only when key_bits > 64) and reports which holds the result.
-hipError_t launch_s2c_prep(const int32_t * coords, int64_t n, int32_t * subidx, int32_t * flags, hipStream_t s);
+size_t s2c_prep_part_bytes();
+hipError_t launch_s2c_prep(const int32_t * coords, int64_t n, int32_t * subidx, int32_t * part, int32_t * flags,
+                           hipStream_t s);
 int s2c_key_shape(const int32_t * maxima, int shifts[4]);  // returns the key width in bits
 int64_t s2c_sort_tiles(int64_t n);
 size_t s2c_sort_tmp_bytes(int64_t n);
