@@ -88,13 +88,33 @@ __global__ void __launch_bounds__(256) k_s2c_prep(const int32_t * __restrict__ c
     }
 }
 
-__global__ void __launch_bounds__(64) k_s2c_prep_reduce(const int32_t * __restrict__ part, int blocks,
-                                                        int32_t * __restrict__ flags) {
-    const int a = threadIdx.x;
-    if (a >= 5) return;
-    int32_t v = 0;
-    for (int b = 0; b < blocks; ++b) v = a == 0 ? (v | part[b * 5]) : max(v, part[b * 5 + a]);
-    flags[a] = v;
+__global__ void __launch_bounds__(256) k_s2c_prep_reduce(const int32_t * __restrict__ part, int blocks,
+                                                         int32_t * __restrict__ flags) {
+    __shared__ int32_t s_red[4][5];
+    int32_t v[5] = {0, 0, 0, 0, 0};
+    for (int b = threadIdx.x; b < blocks; b += 256) {
+        v[0] |= part[b * 5];
+#pragma unroll
+        for (int a = 1; a < 5; ++a) v[a] = max(v[a], part[b * 5 + a]);
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        v[0] |= __shfl_xor(v[0], d);
+#pragma unroll
+        for (int a = 1; a < 5; ++a) v[a] = max(v[a], __shfl_xor(v[a], d));
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int a = 0; a < 5; ++a) s_red[wave][a] = v[a];
+    }
+    __syncthreads();
+    if (threadIdx.x < 5) {
+        const int a = threadIdx.x;
+        int32_t r = s_red[0][a];
+        for (int w = 1; w < 4; ++w) r = a == 0 ? (r | s_red[w][0]) : max(r, s_red[w][a]);
+        flags[a] = r;
+    }
 }
 
 // Key fields from the top: b, x/2, y/2, z/2 (widths from the maxima), then
@@ -359,7 +379,7 @@ hipError_t launch_s2c_prep(const int32_t * coords, int64_t n, int32_t * subidx, 
     if (n <= 0) return hipErrorInvalidValue;
     const int g = grid_for(n, 256, kPrepBlocks);
     k_s2c_prep<<<g, 256, 0, s>>>(coords, n, subidx, part);
-    k_s2c_prep_reduce<<<1, 64, 0, s>>>(part, g, flags);
+    k_s2c_prep_reduce<<<1, 256, 0, s>>>(part, g, flags);
     return hipGetLastError();
 }
 
