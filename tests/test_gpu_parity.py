@@ -477,6 +477,27 @@ def test_linear_mfma_vs_oracle(be16, bebf, dtype, ci, co, n):
             assert max_rel_err(be.download(yb), exp) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
+@pytest.mark.parametrize("ci,co,n", [(256, 8, 316027), (64, 8, 1), (128, 16, 17), (1024, 3, 1000), (32, 1, 50),
+                                     (512, 8, 4099)])
+def test_linear_narrow_vs_oracle(be16, bebf, dtype, ci, co, n):
+    """Co <= 16 (the subdivide logits, Ci -> 8) on the narrow MFMA kernel:
+    ragged 16-row blocks, a single row, bias and SiLU on and off."""
+    be = backend_for(dtype, None, be16, bebf)
+    say(f"linear narrow dtype={dtype} ci={ci} co={co} n={n}")
+    rng = np.random.default_rng(ci * 5 + co + n)
+    x = sh.storage_round(rng.standard_normal((n, ci)), dtype)
+    w = sh.storage_round(rng.standard_normal((co, ci)) / math.sqrt(ci), dtype)
+    bias = rng.standard_normal(co).astype(np.float32)
+    xb = be.upload(x)
+    yb = be.alloc(n * co)
+    for silu in (False, True):
+        for bb in (bias, None):
+            be.linear(xb, w, bb, yb, n, ci, co, silu=silu)
+            exp = orc.linear(x, w, bb, n, ci, co, silu)
+            assert max_rel_err(be.download(yb), exp) <= TOL[dtype]
+
+
 def test_linear_mfma_rows_independent(bebf):
     """Each row depends on its own input row only (no stale tile state)."""
     ci, co, n = 128, 256, 3000

@@ -46,7 +46,8 @@ enum WeightLayout : int {
     kLayoutConvMfmaGrouped = 5,  // kLayoutConvMfma with the compacted kernels' column grouping
     kLayoutLinearMfma = 6,       // storage type [ci/8][co][8], linear_mfma_group column grouping
     kLayoutMlp0 = 7,             // as kLayoutLinearMfma, the fused MLP's first GEMM grouping
-    kLayoutMlp2 = 8              // as kLayoutLinearMfma, the fused MLP's second GEMM grouping
+    kLayoutMlp2 = 8,             // as kLayoutLinearMfma, the fused MLP's second GEMM grouping
+    kLayoutLinear16 = 9          // storage type [co][ci] (narrow MFMA linear)
 };
 
 struct StageMark {
@@ -305,6 +306,19 @@ trellis_status get_weight(Backend * be, const float * host, size_t count, int la
             }
             break;
         }
+        case kLayoutLinear16: {  // [co][ci] in the storage type
+            staged.resize((size_t) ci * co * 2);
+            uint16_t * w = (uint16_t *) staged.data();
+            for (size_t i = 0; i < (size_t) ci * co; ++i) {
+                if (dt == kBF16) {
+                    w[i] = f32_to_bf16(host[i]);
+                } else {
+                    const _Float16 f = (_Float16) host[i];
+                    memcpy(&w[i], &f, 2);
+                }
+            }
+            break;
+        }
         case kLayoutLinearT: {  // [co][ci] -> [ci][co]
             staged.resize((size_t) ci * co * sizeof(float));
             float * w = (float *) staged.data();
@@ -459,17 +473,23 @@ trellis_status linear_impl(trellis_sparse_backend * backend, const trellis_spars
     const void * bd = nullptr;
     const int dt = be->policy.compute_dtype;
     // bf16/fp16 with Ci = 64 or Ci % 128 == 0 and Co % 64 == 0: MFMA kernel;
-    // otherwise (and always for fp32) the reference-order VALU kernel.
+    // Co <= 16 (the subdivide logits): the narrow MFMA kernel; otherwise (and
+    // always for fp32) the reference-order VALU kernel.
     const bool mfma = linear_mfma_supported(dt, ci, co);
-    trellis_status st =
-        get_weight(be, weight, (size_t) ci * co, mfma ? kLayoutLinearMfma : kLayoutLinearT, ci, co, &wt);
+    const bool narrow = !mfma && linear_narrow_supported(dt, ci, co);
+    const int layout = mfma ? kLayoutLinearMfma : (narrow ? kLayoutLinear16 : kLayoutLinearT);
+    trellis_status st = get_weight(be, weight, (size_t) ci * co, layout, ci, co, &wt);
     if (st == TRELLIS_STATUS_OK) st = get_weight(be, bias, (size_t) co, kLayoutVector, 0, co, &bd);
     if (st != TRELLIS_STATUS_OK) return st;
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
-    const hipError_t err =
-        mfma ? launch_linear_mfma(dt, x->ptr, wt, (const float *) bd, y->ptr, n, ci, co, silu, be->cus, be->stream)
-             : launch_linear(dt, x->ptr, (const float *) wt, (const float *) bd, y->ptr, n, ci, co, silu,
-                             be->stream);
+    hipError_t err;
+    if (mfma) {
+        err = launch_linear_mfma(dt, x->ptr, wt, (const float *) bd, y->ptr, n, ci, co, silu, be->cus, be->stream);
+    } else if (narrow) {
+        err = launch_linear_narrow(dt, x->ptr, wt, (const float *) bd, y->ptr, n, ci, co, silu, be->cus, be->stream);
+    } else {
+        err = launch_linear(dt, x->ptr, (const float *) wt, (const float *) bd, y->ptr, n, ci, co, silu, be->stream);
+    }
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
     return hip_status(be, err, "linear");
 }

@@ -255,7 +255,85 @@ hipError_t launch_linear_dt(const void * x, const void * w16, const float * bias
     TSH_LINEAR(64);
 #undef TSH_LINEAR
 }
+// Narrow outputs (Co <= 16: the subdivide logits, Ci -> 8): one wavefront
+// per 16-row block at a time.  The block's KS A fragments come straight from
+// the rows (four lanes per 64-byte segment), all loads issued before the
+// MFMAs; the B fragments are the [co][ci] weights' rows read from cache (the
+// columns past Co are zero); bias and SiLU in fp32; lanes of the Co valid
+// columns store.
+template <int DT, int KS>
+__global__ void __launch_bounds__(256) k_linear_narrow(const typename Store<DT>::T * __restrict__ x,
+                                                       const typename Store<DT>::T * __restrict__ w,
+                                                       const float * __restrict__ bias,
+                                                       typename Store<DT>::T * __restrict__ y, int64_t n, int co,
+                                                       int silu) {
+    using V = typename Mfma<DT>::V;
+    constexpr int CI = KS * 32;
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int64_t waves = (int64_t) gridDim.x * (blockDim.x >> 6);
+    const int64_t wid = (int64_t) blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const bool colok = l16 < co;
+    V b[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) b[s] = colok ? *(const V *) (w + (int64_t) l16 * CI + s * 32 + lg * 8) : V{};
+    const float bv = (colok && bias != nullptr) ? bias[l16] : 0.0f;
+    const int64_t blocks16 = (n + 15) / 16;
+    for (int64_t rb = wid; rb < blocks16; rb += waves) {
+        const int64_t row = rb * 16 + l16;
+        V a[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) a[s] = row < n ? *(const V *) (x + row * CI + s * 32 + lg * 8) : V{};
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) acc = Mfma<DT>::mac(a[s], b[s], acc);
+        if (colok) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t r = rb * 16 + lg * 4 + i;
+                float v = acc[i] + bv;
+                if (silu) v = v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+                if (r < n) Store<DT>::st(y, r * co + l16, v);
+            }
+        }
+    }
+}
+
+template <int DT>
+hipError_t launch_narrow_dt(const void * x, const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
+                            int silu, int cus, hipStream_t s) {
+    using T = typename Store<DT>::T;
+    const int64_t blocks16 = (n + 15) / 16;
+    int64_t grid = (blocks16 + 3) / 4;
+    if (grid > (int64_t) cus * 16) grid = (int64_t) cus * 16;
+    if (grid < 1) grid = 1;
+#define TSH_NARROW(KSV)                                                                                          \
+    k_linear_narrow<DT, KSV><<<(unsigned) grid, 256, 0, s>>>((const T *) x, (const T *) w16, bias, (T *) y, n, co, \
+                                                            silu)
+    switch (ci) {
+        case 32: TSH_NARROW(1); break;
+        case 64: TSH_NARROW(2); break;
+        case 128: TSH_NARROW(4); break;
+        case 256: TSH_NARROW(8); break;
+        case 512: TSH_NARROW(16); break;
+        default: TSH_NARROW(32); break;
+    }
+#undef TSH_NARROW
+    return hipGetLastError();
+}
 }  // namespace
+
+bool linear_narrow_supported(int dtype, int ci, int co) {
+    return (dtype == kF16 || dtype == kBF16) && co >= 1 && co <= 16 &&
+           (ci == 32 || ci == 64 || ci == 128 || ci == 256 || ci == 512 || ci == 1024);
+}
+
+hipError_t launch_linear_narrow(int dtype, const void * x, const void * w16, const float * bias, void * y, int64_t n,
+                                int ci, int co, int silu, int cus, hipStream_t s) {
+    if (!linear_narrow_supported(dtype, ci, co) || n <= 0 || cus <= 0) return hipErrorInvalidValue;
+    if (dtype == kBF16) return launch_narrow_dt<kBF16>(x, w16, bias, y, n, ci, co, silu, cus, s);
+    return launch_narrow_dt<kF16>(x, w16, bias, y, n, ci, co, silu, cus, s);
+}
 
 int linear_mfma_group(int co) { return (co % 128 == 0 ? 128 : 64) / 4 / 16; }
 

@@ -236,6 +236,11 @@ hipError_t launch_s2c_pack(int dtype, const void * x, const int32_t * child, voi
 hipError_t launch_s2c_skip_mean(int dtype, const void * x, const int32_t * child, void * y, int64_t m, int ci,
                                 int co, hipStream_t s);
 
+// Narrow MFMA linear (bf16/fp16, Co <= 16, Ci a power of two in 32..1024):
+// weights [co][ci] in the storage type.
+bool linear_narrow_supported(int dtype, int ci, int co);
+hipError_t launch_linear_narrow(int dtype, const void * x, const void * w16, const float * bias, void * y, int64_t n,
+                                int ci, int co, int silu, int cus, hipStream_t s);
 hipError_t launch_c2s_count(int dtype, const void * logits, int64_t n, int32_t * counts, hipStream_t s);
 // Exclusive scan of n int32 values; total written to *total_dev.  tmp needs scan_tmp_bytes(n).
 size_t scan_tmp_bytes(int64_t n);
