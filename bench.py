@@ -148,6 +148,10 @@ class Block:
       the host, s2c_host.c:33-120, executor.c:258-300); coarse rulebook; row_norm_silu
       -> conv(128->128) on the coarse voxels -> add(skip).  The line also carries the
       CPU oracle's S2C map time on the same voxels.
+    mesh: FlexiDualGrid mesh extraction (src/ops/mesh/flex_dual_grid.c:166-313) from
+      7-channel decoder logits on the ~1.26M config-3 children (R = 512), coordinates
+      and logits resident on the device, vertices and faces returned as host arrays
+      (the reference function's contract); the CPU oracle beside it.
     c2s: the C2S up-block on the ~0.32M config-3 parents, Ci = 256 -> Co = 128:
       linear(256->8) logits -> build_c2s_map_device -> build_rulebook_for_c2s_map;
       row_norm_silu -> conv(256->1024) on the parents -> c2s_gather_device;
@@ -182,6 +186,15 @@ class Block:
             self.slots = ["sparse_conv3d", "row_norm", "linear_silu", "linear", "add"]
             if kind == "convnext_fused":
                 self.slots = ["sparse_conv3d", "convnext_mlp"]
+        elif kind == "mesh":
+            pmap = be.upload_coords(w["parent_coords"])
+            dm = be.build_c2s_map_device(be.upload(w["logits"]), w["parent_coords"].shape[0], coords_map=pmap)
+            self.cmap, self.n = dm, dm.n
+            self.coords = be.download_c2s_coords(dm)
+            self.logits7 = rng.standard_normal((self.n, 7)).astype(np.float32) * 2
+            self.feats = be.upload(self.logits7)
+            self.faces = 0
+            self.slots = ["flex_dual_grid_mesh"]
         elif kind == "s2c":
             ci, co = 64, 128
             self.ci, self.co = ci, co
@@ -246,6 +259,11 @@ class Block:
         be = self.be
         ev = iter(range(1, 16))
         be.event(0)
+        if self.kind == "mesh":
+            _, f = be.flex_dual_grid_mesh(self.feats, self.n, 7, 512, coords_map=self.cmap)
+            self.faces = f.shape[0]
+            be.event(next(ev))
+            return
         if self.kind == "s2c":
             n, ci, co, m = self.n, self.ci, self.co, self.m
             packed, skip, norm2, conv2, out = self.bufs
@@ -319,6 +337,8 @@ class Block:
         be.free_map(dm)
 
     def flops(self):
+        if self.kind == "mesh":
+            return 0
         if self.kind == "s2c":
             return wl.conv_flops(self.fpairs, self.ci, self.co // 8) + wl.conv_flops(self.pairs, self.co, self.co)
         if self.kind in ("convnext", "convnext_fused"):
@@ -348,7 +368,20 @@ def run_block(args):
            "steps": args.steps, "warmup": args.warmup, "ms_per_block": round(dev, 4),
            "wall_ms_per_block": round(wall, 4), "effective_tflops": round(job.flops() / (dev * 1e-3) / 1e12, 2),
            "slot_ms": slots}
-    if args.block == "s2c":
+    if args.block == "mesh":
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle_lib as orc
+
+        t0 = time.perf_counter()
+        rc, _, faces = orc.fdg_mesh(job.coords, sh.storage_round(job.logits7, be.dtype), 512)
+        cpu_ms = (time.perf_counter() - t0) * 1e3
+        assert rc == 0 and faces.shape[0] == job.faces
+        out.pop("effective_tflops")
+        out.update({"voxels": int(job.n), "faces": int(job.faces),
+                    "mvoxels_per_s": round(job.n / (dev * 1e-3) / 1e6, 1), "cpu_oracle_ms": round(cpu_ms, 2),
+                    "cpu_note": "oracle/trellis_oracle.c orc_fdg_mesh (1 thread), same voxels and logits",
+                    "timed": "whole call: corner lookup map, vertices, faces, download of both arrays"})
+    elif args.block == "s2c":
         sys.path.insert(0, os.path.join(ROOT, "tests"))
         import oracle_lib as orc
 
@@ -431,7 +464,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-stride", type=int, default=16)
     ap.add_argument("--conv-algo", type=int, default=sh.CONV_AUTO)
-    ap.add_argument("--block", choices=["convnext", "convnext_fused", "c2s", "s2c"],
+    ap.add_argument("--block", choices=["convnext", "convnext_fused", "c2s", "s2c", "mesh"],
                     help="instead of the configuration step, time one decoder block composed from the backend's "
                          "slots at config-3 scale and print its own JSON line")
     ap.add_argument("--calibrate", action="store_true",

@@ -53,6 +53,16 @@ typedef enum trellis_sparse_backend_kind {
     TRELLIS_SPARSE_BACKEND_CPU = 1,
     TRELLIS_SPARSE_BACKEND_VULKAN = 2
 } trellis_sparse_backend_kind;
+
+/* include/trellis.h:790-796; arrays malloc'd, released with free() (or the
+ * reference's trellis_mesh_free). */
+typedef struct trellis_mesh_host {
+    float * vertices;      /* [n_vertices, 3] */
+    float * vertex_colors; /* optional [n_vertices, 3] in linear 0..1 RGB */
+    int32_t * faces;       /* [n_faces, 3] */
+    int64_t n_vertices;
+    int64_t n_faces;
+} trellis_mesh_host;
 #endif
 
 /* New backend kind value for this library.  A caller selects it through
@@ -311,6 +321,27 @@ trellis_status trellis_sparse_hip_s2c_skip_mean_device(trellis_sparse_backend * 
                                                        const trellis_sparse_buffer * x,
                                                        const trellis_sparse_c2s_device_map * fine_map,
                                                        trellis_sparse_buffer * y, int ci, int co);
+
+/* ------------------------------------------------------------------------ */
+/* FlexiDualGrid mesh from decoder logits on the device (no vtable          */
+/* counterpart: replaces trellis_flexible_dual_grid_mesh_from_decoder_      */
+/* logits_host, src/ops/mesh/flex_dual_grid.c:166-313, which the mesh stage */
+/* calls on the downloaded decoder output, latent_decode.c:146).            */
+/* ------------------------------------------------------------------------ */
+
+/* Same result contract as the reference function, for decoder output still
+ * on the device: coordinates as host [n][4] or a device map (coords_map wins),
+ * feats a backend buffer [n][channels] (channels >= 7).  One vertex per voxel
+ * (vertex_colors NULL), two faces per quad in the reference's (voxel, axis)
+ * order.  INVALID_ARGUMENT for NULL pointers, n < 0, channels < 7 or
+ * resolution <= 0; PARSE_ERROR for a batch index other than 0, a coordinate
+ * outside [0, resolution), a non-finite logit in channels 0..6 or a repeated
+ * coordinate; NOT_IMPLEMENTED for resolution > 65535 (the corner lookups use
+ * the kernel map's 16-bit keys).  n = 0 gives an empty mesh. */
+trellis_status trellis_sparse_hip_flex_dual_grid_mesh(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                                                     const trellis_sparse_c2s_device_map * coords_map,
+                                                     const trellis_sparse_buffer * feats, int64_t n, int channels,
+                                                     int resolution, trellis_mesh_host * mesh_out);
 
 /* ------------------------------------------------------------------------ */
 /* Fused ConvNeXt MLP tail (no counterpart in the reference vtable: it       */

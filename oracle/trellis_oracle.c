@@ -405,6 +405,141 @@ int orc_s2c_map(const int32_t * fine_coords, int64_t n, int32_t ** coarse_out, i
     return 0;
 }
 
+/* ---- FlexiDualGrid mesh (flex_dual_grid.c:166-313) ---------------------- */
+static float orc_fdg_sigmoid(float v) {
+    /* Split at 0 so that exp never overflows (flex_dual_grid.c:112-119). */
+    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+
+static float orc_fdg_softplus(float v) {
+    if (v > 20.0f) return v;
+    if (v < -20.0f) return expf(v);
+    return log1pf(expf(v));
+}
+
+/* Voxel lookup by binary search over (x, y, z) keys sorted with their rows. */
+typedef struct orc_fdg_key {
+    int64_t key;
+    int32_t row;
+} orc_fdg_key;
+
+static int orc_fdg_key_cmp(const void * a, const void * b) {
+    const int64_t u = ((const orc_fdg_key *) a)->key, v = ((const orc_fdg_key *) b)->key;
+    return u < v ? -1 : (u > v ? 1 : 0);
+}
+
+static int32_t orc_fdg_find(const orc_fdg_key * keys, int64_t n, int64_t res, int64_t x, int64_t y, int64_t z) {
+    if (x < 0 || y < 0 || z < 0 || x >= res || y >= res || z >= res) return -1;
+    const int64_t want = (x * res + y) * res + z;
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t mid = lo + (hi - lo) / 2;
+        if (keys[mid].key < want) lo = mid + 1; else hi = mid;
+    }
+    return lo < n && keys[lo].key == want ? keys[lo].row : -1;
+}
+
+int orc_fdg_mesh(const int32_t * coords, const float * feats, int64_t n, int channels, int resolution,
+                 float ** vertices_out, int32_t ** faces_out, int64_t * n_faces_out) {
+    if (coords == NULL || feats == NULL || vertices_out == NULL || faces_out == NULL || n_faces_out == NULL ||
+        n < 0 || n > INT32_MAX || channels < 7 || resolution <= 0) {
+        return 2;
+    }
+    *vertices_out = NULL;
+    *faces_out = NULL;
+    *n_faces_out = 0;
+    if (n == 0) return 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const int32_t * c = coords + 4 * i;
+        if (c[0] != 0) return 4;
+        for (int a = 1; a < 4; ++a)
+            if (c[a] < 0 || c[a] >= resolution) return 4;
+        for (int ch = 0; ch < 7; ++ch)
+            if (!isfinite(feats[i * channels + ch])) return 4;
+    }
+    const int64_t res = resolution;
+    orc_fdg_key * keys = (orc_fdg_key *) malloc((size_t) n * sizeof(orc_fdg_key));
+    float * vert = (float *) malloc((size_t) n * 3 * sizeof(float));
+    float * wgt = (float *) malloc((size_t) n * sizeof(float));
+    if (keys == NULL || vert == NULL || wgt == NULL) {
+        free(keys);
+        free(vert);
+        free(wgt);
+        return 5;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        const int32_t * c = coords + 4 * i;
+        keys[i].key = ((int64_t) c[1] * res + c[2]) * res + c[3];
+        keys[i].row = (int32_t) i;
+    }
+    qsort(keys, (size_t) n, sizeof(orc_fdg_key), orc_fdg_key_cmp);
+    for (int64_t i = 1; i < n; ++i) {
+        if (keys[i].key == keys[i - 1].key) {  /* flex_dual_grid.c:236-246 */
+            free(keys);
+            free(vert);
+            free(wgt);
+            return 4;
+        }
+    }
+    const float inv_res = 1.0f / (float) resolution;
+    for (int64_t i = 0; i < n; ++i) {
+        const float * f = feats + i * channels;
+        for (int a = 0; a < 3; ++a) {
+            const float local = 2.0f * orc_fdg_sigmoid(f[a]) - 0.5f;
+            vert[i * 3 + a] = ((float) coords[4 * i + 1 + a] + local) * inv_res - 0.5f;
+        }
+        wgt[i] = orc_fdg_softplus(f[6]);
+    }
+    /* Quad corners per axis, as (dx, dy, dz) from the voxel. */
+    static const int quad[3][4][3] = {
+        {{0, 0, 0}, {0, 0, 1}, {0, 1, 1}, {0, 1, 0}},
+        {{0, 0, 0}, {1, 0, 0}, {1, 0, 1}, {0, 0, 1}},
+        {{0, 0, 0}, {0, 1, 0}, {1, 1, 0}, {1, 0, 0}},
+    };
+    static const int quad_mut[4][3] = {{0, 0, 0}, {1, 0, 0}, {1, 1, 0}, {0, 1, 0}};
+    int32_t * faces = (int32_t *) malloc((size_t) n * 3 * 2 * 3 * sizeof(int32_t));  /* at most 3 quads per voxel */
+    if (faces == NULL) {
+        free(keys);
+        free(vert);
+        free(wgt);
+        return 5;
+    }
+    int64_t nf = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const int32_t * c = coords + 4 * i;
+        const float * f = feats + i * channels;
+        for (int a = 0; a < 3; ++a) {
+            if (!(f[3 + a] > 0.0f)) continue;
+            int32_t q[4];
+            int ok = 1;
+            for (int j = 0; j < 4 && ok; ++j) {
+                const int * d = (g_mutation == ORC_MUT_FDG_QUAD && a == 2) ? quad_mut[j] : quad[a][j];
+                q[j] = orc_fdg_find(keys, n, res, c[1] + d[0], c[2] + d[1], c[3] + d[2]);
+                ok = q[j] >= 0;
+            }
+            if (!ok) continue;
+            const float w02 = wgt[q[0]] * wgt[q[2]], w13 = wgt[q[1]] * wgt[q[3]];
+            const int first = g_mutation == ORC_MUT_FDG_SPLIT ? w02 >= w13 : w02 > w13;
+            const int32_t t[6] = {q[0], q[1], first ? q[2] : q[3], first ? q[0] : q[3], first ? q[2] : q[1],
+                                  first ? q[3] : q[2]};
+            memcpy(faces + nf * 3, t, sizeof(t));
+            nf += 2;
+        }
+    }
+    free(keys);
+    free(wgt);
+    if (nf == 0) {
+        free(faces);
+        faces = NULL;
+    }
+    *vertices_out = vert;
+    *faces_out = faces;
+    *n_faces_out = nf;
+    return 0;
+}
+
 void orc_s2c_pack(const float * x, const int32_t * parent, const int32_t * subidx, float * y, int64_t n_fine,
                   int64_t n_coarse, int co) {
     const int pc = co / 8;

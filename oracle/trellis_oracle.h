@@ -26,6 +26,10 @@
  *       subidx and the skip means it produces with zero conv weights); the map
  *       against numpy unique(axis=0) on random sets; S2C of a C2S map
  *       returns the parents.
+ *   orc_fdg_mesh - the reference's known answer (test_trellis.c:581-627:
+ *       vertices, face order, the five rejected inputs); quads against a
+ *       Python set-based corner search on random voxel sets; vertices
+ *       against numpy float64 sigmoid.
  *   orc_s2c_pack - c2s_gather (the reference's inverse index map) of the
  *       packed rows returns the input rows; all other slots are zero.
  *   orc_row_norm / orc_silu / orc_add / orc_linear - torch.nn.functional in float64.
@@ -54,7 +58,9 @@ enum {
     ORC_MUT_CROSS_BATCH = 7,     /* neighbour lookup ignores the batch index */
     ORC_MUT_SUBDIV_GE = 8,       /* subdivide keeps logits >= 0 instead of > 0 */
     ORC_MUT_S2C_ORDER = 9,       /* S2C orders coarse voxels z-major (z, y, x, b) instead of (b, x, y, z) */
-    ORC_MUT_S2C_CHANNEL = 10     /* S2C skip mean groups channel-major ((c*8 + s) / g instead of (s*ci + c) / g) */
+    ORC_MUT_S2C_CHANNEL = 10,    /* S2C skip mean groups channel-major ((c*8 + s) / g instead of (s*ci + c) / g) */
+    ORC_MUT_FDG_SPLIT = 11,      /* mesh quads split on w02 >= w13 instead of w02 > w13 */
+    ORC_MUT_FDG_QUAD = 12        /* mesh quad of axis 2 takes corners (0,0,0),(1,0,0),(1,1,0),(0,1,0) */
 };
 void orc_set_mutation(int mutation);
 int orc_get_mutation(void);
@@ -125,6 +131,19 @@ void orc_s2c_pack(const float * x, const int32_t * parent, const int32_t * subid
  * += x[f][c] / g, g = 8*ci/co, fp32 in fine-row then channel order from 0. */
 void orc_s2c_skip_mean(const float * x, const int32_t * parent, const int32_t * subidx, float * y, int64_t n_fine,
                        int64_t n_coarse, int ci, int co);
+
+/* src/ops/mesh/flex_dual_grid.c:166-313 - mesh from FlexiDualGrid decoder
+ * logits (channels >= 7).  Vertex i = ((coord + 2 sigmoid(f[a]) - 0.5) / res
+ * - 0.5) per axis a; weight softplus(f[6]); for voxel i in row order and axis
+ * a = 0, 1, 2 in order, when f[3+a] > 0 and the voxels at the quad's corners
+ * base + Q[a][0..3] all exist, two triangles split along the diagonal with
+ * the larger weight product ((q0,q1,q2),(q0,q2,q3) if w02 > w13, else
+ * (q0,q1,q3),(q3,q1,q2)).  Returns 0, 2 (bad argument) or 4 (batch != 0, a
+ * coordinate outside [0, res), a non-finite logit in channels 0..6, or a
+ * repeated coordinate); vertices [n][3] and faces [n_faces][3] are malloc'd
+ * (faces NULL when there are none). */
+int orc_fdg_mesh(const int32_t * coords, const float * feats, int64_t n, int channels, int resolution,
+                 float ** vertices_out, int32_t ** faces_out, int64_t * n_faces_out);
 
 /* trellis_sparse_cpu.c:385-409. */
 void orc_c2s_gather(const float * x, const int32_t * parent, const int32_t * subidx, float * y, int64_t n_out,

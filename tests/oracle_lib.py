@@ -44,6 +44,8 @@ def _load():
         "orc_c2s_map": (c_int, [_i32p, _f32p, c_int64, POINTER(_i32p), POINTER(_i32p), POINTER(_i32p),
                                 POINTER(c_int64)]),
         "orc_free": (None, [c_void_p]),
+        "orc_fdg_mesh": (c_int, [_i32p, _f32p, c_int64, c_int, c_int, POINTER(_f32p), POINTER(_i32p),
+                                 POINTER(c_int64)]),
         "orc_s2c_map": (c_int, [_i32p, c_int64, POINTER(_i32p), POINTER(_i32p), POINTER(_i32p), POINTER(c_int64)]),
         "orc_s2c_pack": (None, [_f32p, _i32p, _i32p, _f32p, c_int64, c_int64, c_int]),
         "orc_s2c_skip_mean": (None, [_f32p, _i32p, _i32p, _f32p, c_int64, c_int64, c_int, c_int]),
@@ -164,6 +166,25 @@ def c2s_map(coords, logits):
     finally:
         for q in (pc, pp, ps):
             L.orc_free(ctypes.cast(q, c_void_p))
+
+
+def fdg_mesh(coords, feats, resolution):
+    """(rc, vertices [n][3], faces [n_faces][3]); rc 0 ok, 2 bad argument, 4 rejected input."""
+    c = np.ascontiguousarray(coords, dtype=np.int32).reshape(-1, 4)
+    f = _f(feats).reshape(c.shape[0], -1) if c.shape[0] else np.zeros((0, 7), np.float32)
+    pv, pf, nf = _f32p(), _i32p(), c_int64()
+    rc = L.orc_fdg_mesh(_ip(c), _fp(np.ascontiguousarray(f)), c.shape[0], f.shape[1], resolution, ctypes.byref(pv),
+                        ctypes.byref(pf), ctypes.byref(nf))
+    if rc != 0:
+        return rc, None, None
+    try:
+        v = np.ctypeslib.as_array(pv, shape=(c.shape[0], 3)).copy() if c.shape[0] else np.zeros((0, 3), np.float32)
+        fc = np.ctypeslib.as_array(pf, shape=(nf.value, 3)).copy() if nf.value else np.zeros((0, 3), np.int32)
+        return 0, v, fc
+    finally:
+        for q in (pv, pf):
+            if q:
+                L.orc_free(ctypes.cast(q, c_void_p))
 
 
 def s2c_map(fine_coords):

@@ -302,6 +302,76 @@ def test_skip_repeat_matches_repeat_interleave(ci, co):
             assert not np.array_equal(orc.skip_repeat(x, parent, sub, ci, co), exp)
 
 
+# --------------------------------------------------- FlexiDualGrid mesh
+def fdg_kat():
+    """tests/test_trellis.c:581-627: four voxels of one z = 0 face, zero
+    logits except channel 5 of voxel 0 (the axis-2 quad), resolution 4."""
+    coords = np.array([[0, 0, 0, 0], [0, 0, 1, 0], [0, 1, 1, 0], [0, 1, 0, 0]], np.int32)
+    feats = np.zeros((4, 7), np.float32)
+    feats[0, 5] = 1.0
+    return coords, feats
+
+
+def test_fdg_mesh_known_answer_and_rejects():
+    coords, feats = fdg_kat()
+    rc, v, f = orc.fdg_mesh(coords, feats, 4)
+    assert rc == 0 and v.shape == (4, 3) and f.shape == (2, 3)
+    assert np.allclose(v[0], [-0.375, -0.375, -0.375], atol=1e-6)
+    assert f.tolist() == [[0, 1, 3], [3, 1, 2]]
+    with orc.mutation(11):  # ties split the other way
+        assert orc.fdg_mesh(coords, feats, 4)[2].tolist() != [[0, 1, 3], [3, 1, 2]]
+    bad = coords.copy(); bad[0, 0] = 1
+    assert orc.fdg_mesh(bad, feats, 4)[0] == 4
+    bad = coords.copy(); bad[0, 1] = -1
+    assert orc.fdg_mesh(bad, feats, 4)[0] == 4
+    bad[0, 1] = 4
+    assert orc.fdg_mesh(bad, feats, 4)[0] == 4
+    bad = coords.copy(); bad[1] = bad[0]
+    assert orc.fdg_mesh(bad, feats, 4)[0] == 4
+    nanf = feats.copy(); nanf[0, 3] = np.nan
+    assert orc.fdg_mesh(coords, nanf, 4)[0] == 4
+    assert orc.fdg_mesh(np.zeros((0, 4), np.int32), np.zeros((0, 7), np.float32), 4)[0] == 0
+
+
+def py_quads(coords, feats):
+    """Independent quad search: a Python dict of voxels, corners per axis from
+    the face the quad lies in (x-faces span y/z, y-faces z/x, z-faces x/y)."""
+    where = {tuple(c[1:]): i for i, c in enumerate(coords.tolist())}
+    corners = {0: [(0, 0, 0), (0, 0, 1), (0, 1, 1), (0, 1, 0)], 1: [(0, 0, 0), (1, 0, 0), (1, 0, 1), (0, 0, 1)],
+               2: [(0, 0, 0), (0, 1, 0), (1, 1, 0), (1, 0, 0)]}
+    out = []
+    for i, c in enumerate(coords.tolist()):
+        for a in range(3):
+            if feats[i, 3 + a] > 0:
+                q = [where.get((c[1] + d[0], c[2] + d[1], c[3] + d[2]), -1) for d in corners[a]]
+                if min(q) >= 0:
+                    out.append(q)
+    return out
+
+
+def test_fdg_mesh_quads_and_vertices_on_random_sets():
+    rng = np.random.default_rng(12)
+    res = 24
+    c = np.unique(rng.integers(0, res, (4000, 3)), axis=0)
+    coords = np.concatenate([np.zeros((c.shape[0], 1), np.int64), c], axis=1).astype(np.int32)
+    coords = coords[rng.permutation(coords.shape[0])]
+    feats = rng.standard_normal((coords.shape[0], 9)).astype(np.float32) * 3
+    rc, v, f = orc.fdg_mesh(coords, feats, res)
+    assert rc == 0
+    quads = py_quads(coords, feats)
+    assert f.shape[0] == 2 * len(quads)
+    # Each quad's two triangles use its four corners, split on one diagonal.
+    for j, q in enumerate(quads):
+        t0, t1 = f[2 * j].tolist(), f[2 * j + 1].tolist()
+        assert set(t0) | set(t1) == set(q) and t0[:2] == [q[0], q[1]]
+    sig = 1.0 / (1.0 + np.exp(-feats[:, :3].astype(np.float64)))
+    exp_v = (coords[:, 1:] + 2.0 * sig - 0.5) / res - 0.5
+    assert np.max(np.abs(v - exp_v)) < 1e-6
+    with orc.mutation(12):
+        assert orc.fdg_mesh(coords, feats, res)[2].shape != f.shape or not np.array_equal(
+            orc.fdg_mesh(coords, feats, res)[2], f)
+
+
 # ------------------------------------------------------------ S2C (encoder)
 def s2c_kat():
     """tests/test_sparse_encoder_backend.c:84-110: five fine voxels (b, x, y, z),

@@ -1252,6 +1252,128 @@ trellis_status s2c_skip_mean_impl(trellis_sparse_backend * backend, const trelli
     return hip_status(be, err, "s2c_skip_mean_device");
 }
 
+// ---- FlexiDualGrid mesh from decoder logits ------------------------------------
+trellis_status fdg_mesh_impl(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                             const trellis_sparse_c2s_device_map * coords_map, const trellis_sparse_buffer * feats,
+                             int64_t n, int channels, int resolution, trellis_mesh_host * mesh_out) {
+    if (backend == nullptr || mesh_out == nullptr || (coords_bxyz == nullptr && coords_map == nullptr) || n < 0 ||
+        n > INT32_MAX || channels < 7 || resolution <= 0) {
+        return TRELLIS_STATUS_INVALID_ARGUMENT;
+    }
+    memset(mesh_out, 0, sizeof(*mesh_out));
+    if (n == 0) return TRELLIS_STATUS_OK;
+    Backend * be = as_backend(backend);
+    if (!float_buffer_ok(be, feats, (size_t) n * (size_t) channels) || !n_ok(n) ||
+        (coords_map != nullptr && (!map_known(be, coords_map) || coords_map->n != n))) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "flex_dual_grid_mesh: bad argument");
+    }
+    if (resolution > 65535) {
+        // Corner lookups go through the kernel map, whose keys hold 16 bits per axis.
+        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, "flex_dual_grid_mesh: resolution above 65535");
+    }
+    CallScope scope(be);
+    hipStream_t s = be->stream;
+    const int dt = be->policy.compute_dtype;
+    DevMem cd, flags, vert, wgt, counts, first, total, tmp, faces;
+    trellis_status st = TRELLIS_STATUS_OK;
+    const int32_t * coords = nullptr;
+    if (coords_map != nullptr) {
+        coords = (const int32_t *) coords_map->coords.ptr;
+    } else {
+        st = upload_bytes(be, coords_bxyz, (size_t) n * 16, &cd);
+        coords = (const int32_t *) cd.ptr;
+    }
+    auto * r = new (std::nothrow) trellis_sparse_rulebook();
+    if (r == nullptr) st = TRELLIS_STATUS_OUT_OF_MEMORY;
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, 16, &flags);
+    int32_t hf[4] = {0, 0, 0, 0}, dup[2] = {0, 0};
+    if (st == TRELLIS_STATUS_OK) {
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+        hipError_t err = launch_fill_i32((int32_t *) flags.ptr, 4, 0, s);
+        if (err == hipSuccess) {
+            err = launch_fdg_check(dt, coords, feats->ptr, n, channels, resolution, (int32_t *) flags.ptr, s);
+        }
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+        st = hip_status(be, err, "flex_dual_grid_mesh check");
+    }
+    if (st == TRELLIS_STATUS_OK) st = rulebook_build_device(be, coords, n, r);
+    if (st == TRELLIS_STATUS_OK) {
+        hipError_t err = hipMemcpyAsync(hf, flags.ptr, 16, hipMemcpyDeviceToHost, s);
+        if (err == hipSuccess) err = hipMemcpyAsync(dup, r->counters.ptr, 8, hipMemcpyDeviceToHost, s);
+        if (err == hipSuccess) err = hipStreamSynchronize(s);
+        st = hip_status(be, err, "flex_dual_grid_mesh flags");
+    }
+    if (st == TRELLIS_STATUS_OK && hf[0] != 0) {
+        st = fail(be, TRELLIS_STATUS_PARSE_ERROR,
+                  "flex_dual_grid_mesh: batch index not 0, coordinate outside [0, resolution) or non-finite logit");
+    }
+    if (st == TRELLIS_STATUS_OK && dup[1] != 0) {
+        st = fail(be, TRELLIS_STATUS_PARSE_ERROR, "flex_dual_grid_mesh: repeated coordinate");
+    }
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) n * 12, &vert);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) n * 4, &wgt);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) n * 4, &counts);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, (size_t) n * 4, &first);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, 16, &total);
+    if (st == TRELLIS_STATUS_OK) st = dev_alloc(be, scan_tmp_bytes(n), &tmp);
+    int32_t quads = 0;
+    if (st == TRELLIS_STATUS_OK) {
+        stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+        const int32_t * nbr = (const int32_t *) r->nbr.ptr;
+        hipError_t err = launch_fdg_vertices(dt, coords, feats->ptr, n, channels, resolution, (float *) vert.ptr,
+                                             (float *) wgt.ptr, s);
+        if (err == hipSuccess) err = launch_fdg_count(dt, feats->ptr, nbr, n, channels, (int32_t *) counts.ptr, s);
+        if (err == hipSuccess) {
+            err = launch_scan_exclusive((const int32_t *) counts.ptr, (int32_t *) first.ptr, n, (int32_t *) total.ptr,
+                                        tmp.ptr, s);
+        }
+        stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+        if (err == hipSuccess) err = hipMemcpyAsync(&quads, total.ptr, 4, hipMemcpyDeviceToHost, s);
+        if (err == hipSuccess) err = hipStreamSynchronize(s);
+        st = hip_status(be, err, "flex_dual_grid_mesh count");
+    }
+    if (st == TRELLIS_STATUS_OK && quads > 0) {
+        st = dev_alloc(be, (size_t) quads * 24, &faces);
+        if (st == TRELLIS_STATUS_OK) {
+            stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+            st = hip_status(be,
+                            launch_fdg_faces(dt, feats->ptr, (const int32_t *) r->nbr.ptr, (const float *) wgt.ptr,
+                                             (const int32_t *) first.ptr, n, channels, (int32_t *) faces.ptr, s),
+                            "flex_dual_grid_mesh faces");
+            stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+        }
+    }
+    float * hv = nullptr;
+    int32_t * hfaces = nullptr;
+    if (st == TRELLIS_STATUS_OK) {
+        hv = (float *) malloc((size_t) n * 12);
+        hfaces = quads > 0 ? (int32_t *) malloc((size_t) quads * 24) : nullptr;
+        if (hv == nullptr || (quads > 0 && hfaces == nullptr)) {
+            st = TRELLIS_STATUS_OUT_OF_MEMORY;
+        } else {
+            hipError_t err = hipMemcpyAsync(hv, vert.ptr, (size_t) n * 12, hipMemcpyDeviceToHost, s);
+            if (err == hipSuccess && quads > 0) {
+                err = hipMemcpyAsync(hfaces, faces.ptr, (size_t) quads * 24, hipMemcpyDeviceToHost, s);
+            }
+            if (err == hipSuccess) err = hipStreamSynchronize(s);
+            st = hip_status(be, err, "flex_dual_grid_mesh download");
+        }
+    }
+    for (DevMem * d : {&cd, &flags, &vert, &wgt, &counts, &first, &total, &tmp, &faces}) dev_release(be, d);
+    if (r != nullptr) rulebook_release(be, r);
+    if (st != TRELLIS_STATUS_OK) {
+        free(hv);
+        free(hfaces);
+        return st;
+    }
+    mesh_out->vertices = hv;
+    mesh_out->vertex_colors = nullptr;
+    mesh_out->faces = hfaces;
+    mesh_out->n_vertices = n;
+    mesh_out->n_faces = (int64_t) quads * 2;
+    return TRELLIS_STATUS_OK;
+}
+
 trellis_status op_trim(trellis_sparse_backend * backend, unsigned flags, size_t * released_bytes) {
     if (released_bytes != nullptr) *released_bytes = 0;
     if (backend == nullptr || (flags & ~(unsigned) TRELLIS_SPARSE_TRIM_ALL) != 0) {
@@ -1597,6 +1719,13 @@ trellis_status trellis_sparse_hip_s2c_skip_mean_device(trellis_sparse_backend * 
                                                        const trellis_sparse_c2s_device_map * fine_map,
                                                        trellis_sparse_buffer * y, int ci, int co) {
     return tsh::s2c_skip_mean_impl(backend, x, fine_map, y, ci, co);
+}
+
+trellis_status trellis_sparse_hip_flex_dual_grid_mesh(trellis_sparse_backend * backend, const int32_t * coords_bxyz,
+                                                     const trellis_sparse_c2s_device_map * coords_map,
+                                                     const trellis_sparse_buffer * feats, int64_t n, int channels,
+                                                     int resolution, trellis_mesh_host * mesh_out) {
+    return tsh::fdg_mesh_impl(backend, coords_bxyz, coords_map, feats, n, channels, resolution, mesh_out);
 }
 
 trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,

@@ -241,6 +241,15 @@ hipError_t launch_s2c_skip_mean(int dtype, const void * x, const int32_t * child
 bool linear_narrow_supported(int dtype, int ci, int co);
 hipError_t launch_linear_narrow(int dtype, const void * x, const void * w16, const float * bias, void * y, int64_t n,
                                 int ci, int co, int silu, int cus, hipStream_t s);
+// FlexiDualGrid mesh extraction (kernels_mesh.hip).
+hipError_t launch_fdg_check(int dtype, const int32_t * coords, const void * feats, int64_t n, int channels, int res,
+                            int32_t * flags, hipStream_t s);
+hipError_t launch_fdg_vertices(int dtype, const int32_t * coords, const void * feats, int64_t n, int channels, int res,
+                               float * vert, float * wgt, hipStream_t s);
+hipError_t launch_fdg_count(int dtype, const void * feats, const int32_t * nbr, int64_t n, int channels,
+                            int32_t * counts, hipStream_t s);
+hipError_t launch_fdg_faces(int dtype, const void * feats, const int32_t * nbr, const float * wgt,
+                            const int32_t * first, int64_t n, int channels, int32_t * faces, hipStream_t s);
 hipError_t launch_c2s_count(int dtype, const void * logits, int64_t n, int32_t * counts, hipStream_t s);
 // Exclusive scan of n int32 values; total written to *total_dev.  tmp needs scan_tmp_bytes(n).
 size_t scan_tmp_bytes(int64_t n);

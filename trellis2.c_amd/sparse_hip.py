@@ -88,6 +88,12 @@ class StageTimes(Structure):
     _fields_ = [("ms", c_double * 6), ("launches", c_int64 * 6)]
 
 
+class Mesh(Structure):
+    """trellis_mesh_host (include/trellis.h:790-796)."""
+    _fields_ = [("vertices", POINTER(c_float)), ("vertex_colors", POINTER(c_float)), ("faces", _i32p),
+                ("n_vertices", c_int64), ("n_faces", c_int64)]
+
+
 # The C ABI of include/trellis_sparse_hip.h: name -> (restype, argtypes).
 ABI = {
     "trellis_sparse_hip_policy_init": (None, [POINTER(Policy)]),
@@ -111,6 +117,7 @@ ABI = {
     "trellis_sparse_hip_s2c_build_device": (c_int, [_p, _i32p, _p, c_int64, POINTER(_p), POINTER(_p), POINTER(c_int64)]),
     "trellis_sparse_hip_s2c_pack_device": (c_int, [_p, _p, _p, _p, c_int]),
     "trellis_sparse_hip_s2c_skip_mean_device": (c_int, [_p, _p, _p, _p, c_int, c_int]),
+    "trellis_sparse_hip_flex_dual_grid_mesh": (c_int, [_p, _i32p, _p, _p, c_int64, c_int, c_int, POINTER(Mesh)]),
     "trellis_sparse_hip_convnext_mlp": (c_int, [_p, _p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _p, _p, c_int64,
                                                 c_int, c_float]),
 }
@@ -433,6 +440,28 @@ class Backend:
     def s2c_skip_mean_device(self, x: Buffer, fine_map: DeviceMap, y: Buffer, ci: int, co: int):
         self._check(LIB.trellis_sparse_hip_s2c_skip_mean_device(self.ptr, x.handle, fine_map.handle, y.handle, ci, co),
                     "s2c_skip_mean_device")
+
+    # -- FlexiDualGrid mesh ------------------------------------------------------
+    def flex_dual_grid_mesh(self, feats: Buffer, n: int, channels: int, resolution: int, coords=None,
+                            coords_map: DeviceMap | None = None):
+        """(vertices [n][3] float32, faces [m][3] int32) from decoder logits on the device."""
+        c = None if coords is None else np.ascontiguousarray(coords, dtype=np.int32).reshape(-1, 4)
+        mesh = Mesh()
+        self._check(LIB.trellis_sparse_hip_flex_dual_grid_mesh(self.ptr, _ptr(c, _i32p), None if coords_map is None
+                                                               else coords_map.handle, feats.handle, n, channels,
+                                                               resolution, ctypes.byref(mesh)), "flex_dual_grid_mesh")
+        libc = ctypes.CDLL(None)
+        libc.free.argtypes = [c_void_p]
+        try:
+            v = (np.ctypeslib.as_array(mesh.vertices, shape=(mesh.n_vertices, 3)).copy() if mesh.n_vertices
+                 else np.zeros((0, 3), np.float32))
+            f = (np.ctypeslib.as_array(mesh.faces, shape=(mesh.n_faces, 3)).copy() if mesh.n_faces
+                 else np.zeros((0, 3), np.int32))
+        finally:
+            for q in (mesh.vertices, mesh.vertex_colors, mesh.faces):
+                if q:
+                    libc.free(ctypes.cast(q, c_void_p))
+        return v, f
 
     def free_map(self, dmap: DeviceMap):
         self._check(LIB.trellis_sparse_hip_free_c2s_map(self.ptr, dmap.handle), "free_c2s_map")
