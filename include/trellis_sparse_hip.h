@@ -344,6 +344,42 @@ trellis_status trellis_sparse_hip_flex_dual_grid_mesh(trellis_sparse_backend * b
                                                      int resolution, trellis_mesh_host * mesh_out);
 
 /* ------------------------------------------------------------------------ */
+/* Raw tensor dumps in trellis2.c's tool formats (no vtable counterpart:    */
+/* the readers of tools/debug/trellis_structured_latent.c:237-333 and the   */
+/* intermediate-tensor writer of src/ops/sparse/cuda/forward.cu:99-223).    */
+/* Host code; the device variants download first.                           */
+/* ------------------------------------------------------------------------ */
+
+/* A whole file of little-endian floats; *data_out malloc'd. IO_ERROR when the
+ * file cannot be read, PARSE_ERROR when its size is not a whole number of
+ * floats. */
+trellis_status trellis_sparse_hip_read_f32(const char * path, float ** data_out, size_t * count_out);
+/* Coordinates: [N,4] (b, x, y, z) when the int32 count is a multiple of 4 and
+ * force_xyz is 0, otherwise [N,3] (x, y, z) returned as [N,4] with b = 0;
+ * PARSE_ERROR when neither fits.  *coords_out malloc'd. */
+trellis_status trellis_sparse_hip_read_coords_i32(const char * path, int force_xyz, int32_t ** coords_out,
+                                                  int64_t * n_out);
+
+/* A dump directory (created if missing) with a manifest file of one line per
+ * tensor, "<name>\t<rows>x<cols>\t<f32|i32>\t<file>", files named
+ * "<index>_<name>.<f32|i32>" with a 3-digit running index. */
+typedef struct trellis_sparse_hip_dump trellis_sparse_hip_dump;
+trellis_status trellis_sparse_hip_dump_open(const char * dir, const char * manifest_name,
+                                            trellis_sparse_hip_dump ** out);
+trellis_status trellis_sparse_hip_dump_close(trellis_sparse_hip_dump * dump);
+trellis_status trellis_sparse_hip_dump_host_f32(trellis_sparse_hip_dump * dump, const char * name, const float * data,
+                                                int64_t rows, int cols);
+trellis_status trellis_sparse_hip_dump_host_i32(trellis_sparse_hip_dump * dump, const char * name,
+                                                const int32_t * data, int64_t rows, int cols);
+/* A backend buffer's first rows * cols values, downloaded as fp32. */
+trellis_status trellis_sparse_hip_dump_buffer(trellis_sparse_hip_dump * dump, trellis_sparse_backend * backend,
+                                              const char * name, const trellis_sparse_buffer * buffer, int64_t rows,
+                                              int cols);
+/* A device map's coordinates, [n][4] int32. */
+trellis_status trellis_sparse_hip_dump_map_coords(trellis_sparse_hip_dump * dump, trellis_sparse_backend * backend,
+                                                  const char * name, const trellis_sparse_c2s_device_map * map);
+
+/* ------------------------------------------------------------------------ */
 /* Fused ConvNeXt MLP tail (no counterpart in the reference vtable: it       */
 /* replaces the slot sequence row_norm -> linear_silu -> linear -> add of     */
 /* the decoder's ConvNeXt block, sparse_unet_decoder/executor.c:206-241).    */

@@ -118,6 +118,14 @@ ABI = {
     "trellis_sparse_hip_s2c_pack_device": (c_int, [_p, _p, _p, _p, c_int]),
     "trellis_sparse_hip_s2c_skip_mean_device": (c_int, [_p, _p, _p, _p, c_int, c_int]),
     "trellis_sparse_hip_flex_dual_grid_mesh": (c_int, [_p, _i32p, _p, _p, c_int64, c_int, c_int, POINTER(Mesh)]),
+    "trellis_sparse_hip_read_f32": (c_int, [c_char_p, POINTER(_f32p), POINTER(c_size_t)]),
+    "trellis_sparse_hip_read_coords_i32": (c_int, [c_char_p, c_int, POINTER(_i32p), POINTER(c_int64)]),
+    "trellis_sparse_hip_dump_open": (c_int, [c_char_p, c_char_p, POINTER(_p)]),
+    "trellis_sparse_hip_dump_close": (c_int, [_p]),
+    "trellis_sparse_hip_dump_host_f32": (c_int, [_p, c_char_p, _f32p, c_int64, c_int]),
+    "trellis_sparse_hip_dump_host_i32": (c_int, [_p, c_char_p, _i32p, c_int64, c_int]),
+    "trellis_sparse_hip_dump_buffer": (c_int, [_p, _p, c_char_p, _p, c_int64, c_int]),
+    "trellis_sparse_hip_dump_map_coords": (c_int, [_p, _p, c_char_p, _p]),
     "trellis_sparse_hip_convnext_mlp": (c_int, [_p, _p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _p, _p, c_int64,
                                                 c_int, c_float]),
 }
@@ -135,6 +143,68 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
 
 
 LIB = load_library()
+
+
+def _status(st: int, what: str):
+    if st != OK:
+        raise HipError(st, what)
+
+
+def _free(ptr):
+    libc = ctypes.CDLL(None)
+    libc.free.argtypes = [c_void_p]
+    libc.free(ctypes.cast(ptr, c_void_p))
+
+
+def read_f32(path: str) -> np.ndarray:
+    """trellis_sparse_hip_read_f32: a whole file of floats."""
+    p, n = _f32p(), c_size_t()
+    _status(LIB.trellis_sparse_hip_read_f32(path.encode(), ctypes.byref(p), ctypes.byref(n)), "read_f32")
+    try:
+        return np.ctypeslib.as_array(p, shape=(n.value,)).copy() if n.value else np.zeros(0, np.float32)
+    finally:
+        _free(p)
+
+
+def read_coords_i32(path: str, force_xyz: bool = False) -> np.ndarray:
+    """trellis_sparse_hip_read_coords_i32: [N,4] or [N,3] (batch 0 added)."""
+    p, n = _i32p(), c_int64()
+    _status(LIB.trellis_sparse_hip_read_coords_i32(path.encode(), 1 if force_xyz else 0, ctypes.byref(p),
+                                                   ctypes.byref(n)), "read_coords_i32")
+    try:
+        return np.ctypeslib.as_array(p, shape=(n.value, 4)).copy() if n.value else np.zeros((0, 4), np.int32)
+    finally:
+        _free(p)
+
+
+class Dump:
+    """trellis_sparse_hip_dump_*: a dump directory with a manifest."""
+
+    def __init__(self, directory: str, manifest: str):
+        self.h = c_void_p()
+        _status(LIB.trellis_sparse_hip_dump_open(directory.encode(), manifest.encode(), ctypes.byref(self.h)),
+                "dump_open")
+
+    def host(self, name: str, a):
+        a = np.asarray(a)
+        rows, cols = (a.shape[0], int(np.prod(a.shape[1:]))) if a.ndim > 1 else (a.size, 1)
+        if a.dtype == np.int32:
+            a = np.ascontiguousarray(a)
+            _status(LIB.trellis_sparse_hip_dump_host_i32(self.h, name.encode(), _ptr(a, _i32p), rows, cols), "dump")
+        else:
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            _status(LIB.trellis_sparse_hip_dump_host_f32(self.h, name.encode(), _ptr(a, _f32p), rows, cols), "dump")
+
+    def buffer(self, be, name: str, buf, rows: int, cols: int):
+        _status(LIB.trellis_sparse_hip_dump_buffer(self.h, be.ptr, name.encode(), buf.handle, rows, cols), "dump")
+
+    def map_coords(self, be, name: str, dmap):
+        _status(LIB.trellis_sparse_hip_dump_map_coords(self.h, be.ptr, name.encode(), dmap.handle), "dump")
+
+    def close(self):
+        if self.h:
+            _status(LIB.trellis_sparse_hip_dump_close(self.h), "dump_close")
+            self.h = c_void_p()
 
 
 class HipError(RuntimeError):
