@@ -811,15 +811,20 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
 
     // Block 0: A of steps 0 and 1 straight into LDS slots 0 and 1, steps 2 ..
     // DEPTH-1 into ring slots 2 .. DEPTH-1; weights of steps 0 .. DEPTH-1.
+    // The fetches are issued in the order the main loop issues them (step r:
+    // A piece, then weights), so that the loop's memory waits, which must
+    // hold for its first pass as for the later ones, stay those of a full
+    // DEPTH-step look-ahead.
     target(0, 0);
     load_a(ra[0], 0);
     store_a(0, ra[0]);
     load_a(ra[1], 1);
     store_a(1, ra[1]);
 #pragma unroll
-    for (int r = 2; r < DEPTH; ++r) load_a(ra[r], r);
-#pragma unroll
-    for (int r = 0; r < DEPTH; ++r) load_b(rb[r], r);
+    for (int r = 0; r < DEPTH; ++r) {
+        if (r >= 2) load_a(ra[r], r);
+        load_b(rb[r], r);
+    }
     lds_barrier();
     read_a(af[0], 0);
 
