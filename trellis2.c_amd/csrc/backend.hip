@@ -600,6 +600,21 @@ trellis_status op_add(trellis_sparse_backend * backend, const trellis_sparse_buf
 
 // ---- rulebook -------------------------------------------------------------------
 // Orders the main stream after a side-stream build (once per rulebook).
+void rulebook_wait(Backend * be, const trellis_sparse_rulebook * r);
+trellis_status map_pass(Backend * be, trellis_sparse_rulebook * r, hipStream_t s);
+
+// The neighbour table of a rulebook built without it, written on first use.
+trellis_status rulebook_ensure_nbr(Backend * be, const trellis_sparse_rulebook * rc) {
+    auto * r = const_cast<trellis_sparse_rulebook *>(rc);
+    if (r->nbr.ptr != nullptr) return TRELLIS_STATUS_OK;
+    rulebook_wait(be, r);
+    const trellis_status st = dev_alloc(be, (size_t) r->n * 27 * 4, &r->nbr);
+    if (st != TRELLIS_STATUS_OK) return st;
+    stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
+    const trellis_status mst = map_pass(be, r, be->stream);
+    stage_end(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
+    return mst;
+}
 void rulebook_wait(Backend * be, const trellis_sparse_rulebook * r) {
     auto * w = const_cast<trellis_sparse_rulebook *>(r);
     if (w == nullptr || w->ready == nullptr) return;
@@ -623,11 +638,27 @@ int64_t next_pow2(int64_t v) {
     return p;
 }
 
+// Writes the neighbour table of a built map (a second pass of the map
+// kernel, which rewrites the pair lists with the same values).
+trellis_status map_pass(Backend * be, trellis_sparse_rulebook * r, hipStream_t s) {
+    return hip_status(be,
+                      launch_map_tiles(r->coords, r->n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
+                                       r->table_slots, (const int32_t *) r->pool.ptr, (int32_t *) r->nbr.ptr,
+                                       (uint32_t *) r->mask.ptr, (int32_t *) r->tile_counts.ptr,
+                                       (int32_t *) r->tile_off.ptr, (int32_t *) r->pair_src.ptr,
+                                       (int32_t *) r->pair_dst.ptr, (int32_t *) r->counters.ptr, s),
+                      "kernel map");
+}
+
 // Builds the brick hash and the kernel map for device coordinates `coords`
-// on stream s (the main stream unless given).
+// on stream s (the main stream unless given).  The [n][27] neighbour table
+// is written only when want_nbr (fp32 backends, whose conv reads it, and the
+// mesh extraction); the compacted conv reads the pair lists, and the
+// consumers of the table build it on first use (rulebook_ensure_nbr).
 trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64_t n, trellis_sparse_rulebook * r,
-                                     hipStream_t s = nullptr) {
+                                     hipStream_t s = nullptr, bool want_nbr = false) {
     if (s == nullptr) s = be->stream;
+    want_nbr = want_nbr || be->policy.compute_dtype == kF32;
     r->n = n;
     r->coords = const_cast<int32_t *>(coords);
     r->table_slots = std::max<int64_t>(64, next_pow2(2 * n));
@@ -641,7 +672,7 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
         {&r->bidx, slots * 4},
         {&r->pool, (size_t) (kBrickGroups * brick_group_cap(n)) * kBrickCells * 4},
         {&r->counters, kCounterInts * 4},
-        {&r->nbr, (size_t) n * 27 * 4},
+        {&r->nbr, want_nbr ? (size_t) n * 27 * 4 : 0},
         {&r->mask, (size_t) n * 4},
         {&r->tile_counts, (size_t) r->n_tiles * 27 * 4},
         {&r->tile_off, (size_t) r->n_tiles * 27 * 4},
@@ -649,6 +680,7 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
         {&r->pair_dst, (size_t) r->n_tiles * kMapTile * 27 * 4},
     };
     for (const Need & q : need) {
+        if (q.bytes == 0) continue;
         const trellis_status st = dev_alloc(be, q.bytes, q.m);
         if (st != TRELLIS_STATUS_OK) return st;
     }
@@ -662,14 +694,11 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
                                     r->table_slots, (int32_t *) r->pool.ptr, (int32_t *) r->counters.ptr, s));
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_HASH);
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
-    // One pass: neighbours, per-tile counts and list starts, and each tile's
-    // pair lists in its fixed region.
-    TSH_TRY(be, launch_map_tiles(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
-                                 r->table_slots, (const int32_t *) r->pool.ptr, (int32_t *) r->nbr.ptr,
-                                 (uint32_t *) r->mask.ptr, (int32_t *) r->tile_counts.ptr, (int32_t *) r->tile_off.ptr,
-                                 (int32_t *) r->pair_src.ptr, (int32_t *) r->pair_dst.ptr,
-                                 (int32_t *) r->counters.ptr, s));
+    // One pass: neighbours (when wanted), per-tile counts and list starts,
+    // and each tile's pair lists in its fixed region.
+    const trellis_status mst = map_pass(be, r, s);
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
+    if (mst != TRELLIS_STATUS_OK) return mst;
     if (be->policy.reject_duplicates) {
         int32_t flags[4] = {0, 0, 0, 0};
         TSH_TRY(be, hipMemcpyAsync(flags, r->counters.ptr, sizeof(flags), hipMemcpyDeviceToHost, s));
@@ -746,6 +775,8 @@ trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_
                                           (const int32_t *) rulebook->tile_counts.ptr, w, (const float *) bd,
                                           out->ptr, n, ci, co, be->stream);
         } else {
+            st = rulebook_ensure_nbr(be, rulebook);
+            if (st != TRELLIS_STATUS_OK) return st;
             err = launch_conv_mfma_masked(dt, feats->ptr, (const int32_t *) rulebook->nbr.ptr,
                                           (const uint32_t *) rulebook->mask.ptr, w, (const float *) bd, out->ptr, n,
                                           ci, co, be->stream);
@@ -756,6 +787,8 @@ trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_
         st = get_weight(be, weight, wcount, kLayoutConvF32, ci, co, &w);
         if (st != TRELLIS_STATUS_OK) return st;
         stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
+        st = rulebook_ensure_nbr(be, rulebook);
+        if (st != TRELLIS_STATUS_OK) return st;
         err = launch_conv_generic(dt, feats->ptr, (const int32_t *) rulebook->nbr.ptr, (const float *) w,
                                   (const float *) bd, out->ptr, n, ci, co, be->stream);
         stage_end(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
@@ -1338,7 +1371,7 @@ trellis_status fdg_mesh_impl(trellis_sparse_backend * backend, const int32_t * c
         stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
         st = hip_status(be, err, "flex_dual_grid_mesh check");
     }
-    if (st == TRELLIS_STATUS_OK) st = rulebook_build_device(be, coords, n, r);
+    if (st == TRELLIS_STATUS_OK) st = rulebook_build_device(be, coords, n, r, nullptr, true);
     if (st == TRELLIS_STATUS_OK) {
         hipError_t err = hipMemcpyAsync(hf, flags.ptr, 16, hipMemcpyDeviceToHost, s);
         if (err == hipSuccess) err = hipMemcpyAsync(dup, r->counters.ptr, 8, hipMemcpyDeviceToHost, s);
@@ -1635,6 +1668,8 @@ trellis_status trellis_sparse_hip_download_neighbors(trellis_sparse_backend * ba
     Backend * be = tsh::as_backend(backend);
     tsh::select_device(be);
     tsh::rulebook_wait(be, rulebook);
+    const trellis_status st = tsh::rulebook_ensure_nbr(be, rulebook);
+    if (st != TRELLIS_STATUS_OK) return st;
     hipError_t err = hipMemcpyAsync(nbr_out, rulebook->nbr.ptr, (size_t) n * 27 * 4, hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
     return tsh::hip_status(be, err, "download_neighbors");

@@ -298,10 +298,10 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
     __syncthreads();
     const int64_t base = tile * kBlock * 27;
     if (t < 27) tile_off[tile * 27 + t] = (int32_t) (base + s_koff[t]);
-    // Coalesced copy of the tile's neighbour table.
+    // Coalesced copy of the tile's neighbour table (when the caller wants it).
     const int64_t rows = (n - row0) < kBlock ? (n - row0) : kBlock;
-    const int64_t words = rows * 27;
-    int32_t * dst = nbr + row0 * 27;
+    const int64_t words = nbr != nullptr ? rows * 27 : 0;
+    int32_t * dst = nbr != nullptr ? nbr + row0 * 27 : nullptr;
     if ((words & 3) == 0) {
         for (int64_t w = (int64_t) t * 4; w < words; w += kBlock * 4) {
             *(int4 *) (dst + w) = *(const int4 *) (s_nbr + w);
