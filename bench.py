@@ -157,7 +157,10 @@ class Block:
       row_norm_silu -> conv(256->1024) on the parents -> c2s_gather_device;
       skip_repeat_device; row_norm_silu -> conv(128->128) on the children -> add
       (executor.c:257-554).
-    Slot times come from HIP events on the backend stream between slots.
+    Slot times come from HIP events on the backend stream between slots.  A
+    rulebook built from a device map runs on the backend's second stream, so
+    its time shows up in the slot that first waits for it (the next conv),
+    and work queued between the two overlaps it.
     """
 
     def __init__(self, be, kind):

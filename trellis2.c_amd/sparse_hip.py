@@ -186,7 +186,10 @@ class Dump:
                 "dump_open")
 
     def host(self, name: str, a):
+        """int32 arrays as .i32, floating arrays as .f32 (other dtypes are refused)."""
         a = np.asarray(a)
+        if a.dtype != np.int32 and not np.issubdtype(a.dtype, np.floating):
+            raise TypeError(f"dump {name}: int32 or floating data, not {a.dtype}")
         rows, cols = (a.shape[0], int(np.prod(a.shape[1:]))) if a.ndim > 1 else (a.size, 1)
         if a.dtype == np.int32:
             a = np.ascontiguousarray(a)
