@@ -111,10 +111,15 @@ class ConvOnly:
 
 
 class Cfg2(ConvOnly):
-    """Residual block: conv -> LayerNorm -> SiLU -> conv -> + skip (fp16)."""
+    """Residual block: conv -> LayerNorm -> SiLU -> conv -> + skip (fp16).
 
-    def __init__(self, be, w):
+    By default the two slot pairs run as the fused entry points
+    trellis_sparse_hip_conv_norm and trellis_sparse_hip_conv_add (the norm and
+    the add happen in the convs' epilogues); --slots runs the four slots."""
+
+    def __init__(self, be, w, slots=False):
         super().__init__(be, w)
+        self.slots = slots
         self.weight2 = be.keep(np.ascontiguousarray(w["weight2"], np.float32))
         self.gamma = be.keep(w["gamma"])
         self.beta = be.keep(w["beta"])
@@ -124,11 +129,22 @@ class Cfg2(ConvOnly):
     def step(self):
         be = self.be
         rb = be.build_rulebook_for_c2s_map(self.cmap)
-        be.conv(rb, self.x, self.weight, None, self.y, self.ci, self.co)
-        be.row_norm(self.y, self.gamma, self.beta, self.h, self.n, self.co, 1e-6, silu=True)
-        be.conv(rb, self.h, self.weight2, None, self.y, self.co, self.co)
-        be.add(self.y, self.x, self.out, self.n * self.co)
+        if self.slots:
+            be.conv(rb, self.x, self.weight, None, self.y, self.ci, self.co)
+            be.row_norm(self.y, self.gamma, self.beta, self.h, self.n, self.co, 1e-6, silu=True)
+            be.conv(rb, self.h, self.weight2, None, self.y, self.co, self.co)
+            be.add(self.y, self.x, self.out, self.n * self.co)
+        else:
+            be.conv_norm(rb, self.x, self.weight, None, self.gamma, self.beta, 1e-6, self.h, self.ci, self.co,
+                         silu=True)
+            be.conv_add(rb, self.h, self.weight2, None, self.x, self.out, self.co, self.co)
         rb.free()
+
+    def describe(self):
+        d = super().describe()
+        d["block"] = ("conv -> row_norm_silu -> conv -> add (slots)" if self.slots else
+                      "conv_norm(silu) -> conv_add (fused epilogues)")
+        return d
 
     def flops(self):
         return 2 * wl.conv_flops(self.pairs, self.ci, self.co)
@@ -157,14 +173,16 @@ class Block:
       row_norm_silu -> conv(256->1024) on the parents -> c2s_gather_device;
       skip_repeat_device; row_norm_silu -> conv(128->128) on the children -> add
       (executor.c:257-554).
+    In c2s and s2c the closing conv -> add runs as one trellis_sparse_hip_conv_add
+    (slot "conv_add_post") unless --slots is given.
     Slot times come from HIP events on the backend stream between slots.  A
     rulebook built from a device map runs on the backend's second stream, so
     its time shows up in the slot that first waits for it (the next conv),
     and work queued between the two overlaps it.
     """
 
-    def __init__(self, be, kind):
-        self.be, self.kind = be, kind
+    def __init__(self, be, kind, slots=False):
+        self.be, self.kind, self.fuse_add = be, kind, not slots
         w = wl.workload(3)
         rng = np.random.default_rng(11)
         f32 = lambda a: np.ascontiguousarray(a, np.float32)
@@ -227,6 +245,8 @@ class Block:
             self.slots = ["row_norm_silu_pre", "sparse_conv3d_pre", "s2c_build_device", "s2c_pack_device",
                           "s2c_skip_mean_device", "build_rulebook_for_c2s_map", "row_norm_silu_post",
                           "sparse_conv3d_post", "add"]
+            if self.fuse_add:
+                self.slots[-2:] = ["conv_add_post"]
         else:
             ci, co = 256, 128
             self.ci, self.co = ci, co
@@ -257,6 +277,8 @@ class Block:
             self.slots = ["linear_subdiv", "build_c2s_map_device", "build_rulebook_for_c2s_map", "row_norm_silu_pre",
                           "sparse_conv3d_pre", "c2s_gather_device", "skip_repeat_device", "row_norm_silu_post",
                           "sparse_conv3d_post", "add"]
+            if self.fuse_add:
+                self.slots[-2:] = ["conv_add_post"]
 
     def step(self):
         be = self.be
@@ -284,10 +306,14 @@ class Block:
             be.event(next(ev))
             be.row_norm(packed, None, None, norm2, m, co, 1e-6, silu=True)
             be.event(next(ev))
-            be.conv(rb, norm2, self.w2, self.c2b, conv2, co, co)
-            be.event(next(ev))
-            be.add(conv2, skip, out, m * co)
-            be.event(next(ev))
+            if self.fuse_add:
+                be.conv_add(rb, norm2, self.w2, self.c2b, skip, out, co, co)
+                be.event(next(ev))
+            else:
+                be.conv(rb, norm2, self.w2, self.c2b, conv2, co, co)
+                be.event(next(ev))
+                be.add(conv2, skip, out, m * co)
+                be.event(next(ev))
             rb.free()
             be.free_map(fmap)
             be.free_map(cmap)
@@ -332,10 +358,14 @@ class Block:
         be.event(next(ev))
         be.row_norm(h_up, None, None, norm2, self.m, co, 1e-6, silu=True)
         be.event(next(ev))
-        be.conv(rb, norm2, self.w2, self.c2b, conv2, co, co)
-        be.event(next(ev))
-        be.add(conv2, skip, out, self.m * co)
-        be.event(next(ev))
+        if self.fuse_add:
+            be.conv_add(rb, norm2, self.w2, self.c2b, skip, out, co, co)
+            be.event(next(ev))
+        else:
+            be.conv(rb, norm2, self.w2, self.c2b, conv2, co, co)
+            be.event(next(ev))
+            be.add(conv2, skip, out, self.m * co)
+            be.event(next(ev))
         rb.free()
         be.free_map(dm)
 
@@ -353,7 +383,7 @@ class Block:
 
 def run_block(args):
     be = sh.Backend(0, sh.BF16)
-    job = Block(be, args.block)
+    job = Block(be, args.block, slots=args.slots)
     for _ in range(args.warmup):
         job.step()
     be.synchronize()
@@ -367,7 +397,8 @@ def run_block(args):
     wall = (time.perf_counter() - t0) * 1e3 / args.steps
     slots = {name: round(ms / args.steps, 4) for name, ms in zip(job.slots, slot_ms)}
     dev = sum(slots.values())
-    out = {"block": args.block, "dtype": "bf16", "data": "synthetic (config-3 voxel sets, seeded random weights)",
+    out = {"block": args.block, "epilogues": "slots" if args.slots else "fused where they apply",
+           "dtype": "bf16", "data": "synthetic (config-3 voxel sets, seeded random weights)",
            "steps": args.steps, "warmup": args.warmup, "ms_per_block": round(dev, 4),
            "wall_ms_per_block": round(wall, 4), "effective_tflops": round(job.flops() / (dev * 1e-3) / 1e12, 2),
            "slot_ms": slots}
@@ -470,6 +501,9 @@ def main():
     ap.add_argument("--block", choices=["convnext", "convnext_fused", "c2s", "s2c", "mesh"],
                     help="instead of the configuration step, time one decoder block composed from the backend's "
                          "slots at config-3 scale and print its own JSON line")
+    ap.add_argument("--slots", action="store_true",
+                    help="config 2 and the c2s / s2c blocks: run conv -> row_norm_silu and conv -> add as separate "
+                         "slots instead of the convs with fused epilogues")
     ap.add_argument("--calibrate", action="store_true",
                     help="run one fp32 add over 2 x 64Mi-element inputs (512 MiB read, 256 MiB written) so PMC "
                          "byte counters can be scaled against a streaming kernel of known traffic")
@@ -504,7 +538,7 @@ def main():
     log(f"bench: generating cfg{cfg} ({spec['name']})")
     w = wl.workload(cfg)
     be = sh.Backend(0, spec["dtype"], conv_algo=args.conv_algo)
-    job = {3: Cfg3, 2: Cfg2}.get(cfg, ConvOnly)(be, w)
+    job = Cfg2(be, w, slots=args.slots) if cfg == 2 else {3: Cfg3}.get(cfg, ConvOnly)(be, w)
     log(f"bench: {job.describe()}")
     for _ in range(args.warmup):
         job.step()

@@ -399,6 +399,34 @@ trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend,
                                                int64_t n, int c, float eps);
 
 /* ------------------------------------------------------------------------ */
+/* Convs with a fused epilogue (no counterpart in the reference vtable: each */
+/* replaces a slot pair of the residual blocks, sparse_unet_decoder/         */
+/* executor.c:176-255 and sparse_unet_encoder/executor.c:160-360).           */
+/* ------------------------------------------------------------------------ */
+
+/* out = row_norm(_silu)(sparse_conv3d(feats)) with gamma, beta (NULL allowed)
+ * and eps as trellis_sparse_backend_ops.row_norm(_silu) take them; the conv
+ * output is rounded to the storage type before the norm, as the slot pair
+ * stores it, and is not written anywhere.  out must not be feats.
+ * TRELLIS_STATUS_NOT_IMPLEMENTED unless compute_dtype is F16 or BF16, the
+ * conv policy is AUTO or COMPACT, Ci is 64 or a multiple of 128 and
+ * Co == 128; callers then run the slot pair. */
+trellis_status trellis_sparse_hip_conv_norm(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                                            const trellis_sparse_buffer * feats, const float * weight,
+                                            const float * bias, const float * gamma, const float * beta, float eps,
+                                            int silu, trellis_sparse_buffer * out, int64_t n, int ci, int co);
+
+/* out = sparse_conv3d(feats) + residual (the conv output rounded to the
+ * storage type first, as the slot pair conv -> add computes it); residual
+ * [n][co] may be out itself (each element is read before it is written) or
+ * feats, but out must not be feats.  Same conditions as conv_norm, with Co a
+ * multiple of 128. */
+trellis_status trellis_sparse_hip_conv_add(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                                           const trellis_sparse_buffer * feats, const float * weight,
+                                           const float * bias, const trellis_sparse_buffer * residual,
+                                           trellis_sparse_buffer * out, int64_t n, int ci, int co);
+
+/* ------------------------------------------------------------------------ */
 /* Stage timing with HIP events recorded on the backend's own stream.        */
 /* ------------------------------------------------------------------------ */
 typedef enum trellis_sparse_hip_stage {

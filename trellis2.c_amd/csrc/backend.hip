@@ -732,18 +732,36 @@ trellis_status op_build_rulebook(trellis_sparse_backend * backend, const int32_t
     return TRELLIS_STATUS_OK;
 }
 
-trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
-                                const trellis_sparse_buffer * feats, const float * weight, const float * bias,
-                                trellis_sparse_buffer * out, int64_t n, int ci, int co) {
+// The conv, optionally with a fused epilogue (fused_epi != nullptr: row
+// norm (+ SiLU) or residual add, compacted schedule only).  epi's gamma and
+// beta are host pointers here; they go through the weight cache.
+trellis_status conv_impl(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                         const trellis_sparse_buffer * feats, const float * weight, const float * bias,
+                         trellis_sparse_buffer * out, int64_t n, int ci, int co, const ConvEpilogue * fused_epi,
+                         const char * what) {
     if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
     Backend * be = as_backend(backend);
     if (rulebook == nullptr || weight == nullptr || n <= 0 || ci <= 0 || co <= 0 || n != rulebook->n ||
-        !float_buffer_ok(be, feats, (size_t) n * ci) || !float_buffer_ok(be, out, (size_t) n * co)) {
-        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "sparse_conv3d: bad argument");
+        !float_buffer_ok(be, feats, (size_t) n * ci) || !float_buffer_ok(be, out, (size_t) n * co) ||
+        feats->ptr == out->ptr) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, (std::string(what) + ": bad argument").c_str());
+    }
+    const int dt = be->policy.compute_dtype;
+    ConvEpilogue epi;
+    if (fused_epi != nullptr) {
+        const bool algo_ok = be->policy.conv_algo == TRELLIS_SPARSE_HIP_CONV_AUTO ||
+                             be->policy.conv_algo == TRELLIS_SPARSE_HIP_CONV_COMPACT;
+        const bool shape_ok = fused_epi->mode == kEpiNorm ? co == 128 : co % 128 == 0;
+        if (!algo_ok || !conv_stream_supported(dt, ci, co) || !shape_ok) {
+            const std::string msg = std::string(what) +
+                                    ": needs the compacted conv (16-bit, Ci 64 or a multiple of 128) and " +
+                                    (fused_epi->mode == kEpiNorm ? "Co == 128" : "Co a multiple of 128");
+            return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, msg.c_str());
+        }
+        epi = *fused_epi;
     }
     CallScope scope(be);
     rulebook_wait(be, rulebook);
-    const int dt = be->policy.compute_dtype;
     int algo = be->policy.conv_algo;
     if (algo == TRELLIS_SPARSE_HIP_CONV_AUTO) {
         // The streamed compacted schedule multiplies valid pairs only; where it
@@ -759,6 +777,15 @@ trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_
     const void * bd = nullptr;
     trellis_status st = get_weight(be, bias, (size_t) co, kLayoutVector, 0, co, &bd);
     if (st != TRELLIS_STATUS_OK) return st;
+    if (epi.mode == kEpiNorm) {
+        const void * g = nullptr;
+        const void * b = nullptr;
+        st = get_weight(be, epi.gamma, (size_t) co, kLayoutVector, 0, co, &g);
+        if (st == TRELLIS_STATUS_OK) st = get_weight(be, epi.beta, (size_t) co, kLayoutVector, 0, co, &b);
+        if (st != TRELLIS_STATUS_OK) return st;
+        epi.gamma = (const float *) g;
+        epi.beta = (const float *) b;
+    }
     const size_t wcount = (size_t) co * 27 * ci;
     hipError_t err;
     if (algo == TRELLIS_SPARSE_HIP_CONV_MASKED || algo == TRELLIS_SPARSE_HIP_CONV_COMPACT) {
@@ -773,7 +800,7 @@ trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_
                                           (const int32_t *) rulebook->pair_dst.ptr,
                                           (const int32_t *) rulebook->tile_off.ptr,
                                           (const int32_t *) rulebook->tile_counts.ptr, w, (const float *) bd,
-                                          out->ptr, n, ci, co, be->stream);
+                                          out->ptr, n, ci, co, be->stream, epi);
         } else {
             st = rulebook_ensure_nbr(be, rulebook);
             if (st != TRELLIS_STATUS_OK) return st;
@@ -793,7 +820,43 @@ trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_
                                   (const float *) bd, out->ptr, n, ci, co, be->stream);
         stage_end(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
     }
-    return hip_status(be, err, "sparse_conv3d");
+    return hip_status(be, err, what);
+}
+
+trellis_status op_sparse_conv3d(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                                const trellis_sparse_buffer * feats, const float * weight, const float * bias,
+                                trellis_sparse_buffer * out, int64_t n, int ci, int co) {
+    return conv_impl(backend, rulebook, feats, weight, bias, out, n, ci, co, nullptr, "sparse_conv3d");
+}
+
+trellis_status conv_norm_impl(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                              const trellis_sparse_buffer * feats, const float * weight, const float * bias,
+                              const float * gamma, const float * beta, float eps, int silu,
+                              trellis_sparse_buffer * out, int64_t n, int ci, int co) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    if (!(eps > 0.0f)) return fail(as_backend(backend), TRELLIS_STATUS_INVALID_ARGUMENT, "conv_norm: bad argument");
+    ConvEpilogue epi;
+    epi.mode = kEpiNorm;
+    epi.silu = silu != 0;
+    epi.eps = eps;
+    epi.gamma = gamma;
+    epi.beta = beta;
+    return conv_impl(backend, rulebook, feats, weight, bias, out, n, ci, co, &epi, "conv_norm");
+}
+
+trellis_status conv_add_impl(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                             const trellis_sparse_buffer * feats, const float * weight, const float * bias,
+                             const trellis_sparse_buffer * residual, trellis_sparse_buffer * out, int64_t n, int ci,
+                             int co) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (n <= 0 || co <= 0 || !float_buffer_ok(be, residual, (size_t) n * co)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "conv_add: bad argument");
+    }
+    ConvEpilogue epi;
+    epi.mode = kEpiAdd;
+    epi.residual = residual->ptr;
+    return conv_impl(backend, rulebook, feats, weight, bias, out, n, ci, co, &epi, "conv_add");
 }
 
 void op_free_rulebook(trellis_sparse_backend * backend, trellis_sparse_rulebook * rulebook) {
@@ -1825,6 +1888,20 @@ trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend,
                                                const trellis_sparse_buffer * residual, trellis_sparse_buffer * y,
                                                int64_t n, int c, float eps) {
     return tsh::mlp_impl(backend, x, gamma, beta, mlp0_w, mlp0_b, mlp2_w, mlp2_b, residual, y, n, c, eps);
+}
+
+trellis_status trellis_sparse_hip_conv_norm(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                                            const trellis_sparse_buffer * feats, const float * weight,
+                                            const float * bias, const float * gamma, const float * beta, float eps,
+                                            int silu, trellis_sparse_buffer * out, int64_t n, int ci, int co) {
+    return tsh::conv_norm_impl(backend, rulebook, feats, weight, bias, gamma, beta, eps, silu, out, n, ci, co);
+}
+
+trellis_status trellis_sparse_hip_conv_add(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                                           const trellis_sparse_buffer * feats, const float * weight,
+                                           const float * bias, const trellis_sparse_buffer * residual,
+                                           trellis_sparse_buffer * out, int64_t n, int ci, int co) {
+    return tsh::conv_add_impl(backend, rulebook, feats, weight, bias, residual, out, n, ci, co);
 }
 
 trellis_status trellis_sparse_hip_profile_enable(trellis_sparse_backend * backend, int enable) {

@@ -636,7 +636,7 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
                                                         const typename Store<DT>::T * __restrict__ w16,
                                                         const float * __restrict__ bias,
                                                         typename Store<DT>::T * __restrict__ y, int64_t n, int ci,
-                                                        int co, int64_t n_col_tiles) {
+                                                        int co, int64_t n_col_tiles, ConvEpilogue epi) {
     using T = typename Store<DT>::T;
     using V = typename Mfma<DT>::V;
     constexpr int NW = 8;            // wavefronts
@@ -882,27 +882,76 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
         } while (s0 < KS);
         if constexpr (UPB == 1) flush(cb);
     }
-    lds_barrier();
+    // Epilogue: bias, one rounding to the storage type; then the optional
+    // row norm (+ SiLU) or residual add on the rounded values, rounded again.
+    // A row's CHUNKS 16-byte chunks sit in CHUNKS consecutive lanes (each
+    // thread keeps its chunk column on every pass), so the norm's sums are
+    // shuffle reductions inside those lanes; every thread takes part in them
+    // (rows past n are computed and not stored).  The residual chunks, bias,
+    // scale and shift are fetched before the barrier, all passes at once, so
+    // their latency overlaps the last accumulator flush.
     constexpr int CHUNKS = BN / 8;
-    for (int e = t; e < TM * CHUNKS; e += NTHR) {
-        const int rr = e / CHUNKS, cc = (e % CHUNKS) * 8;
+    constexpr int PASSES = TM * CHUNKS / NTHR;
+    static_assert(NTHR % CHUNKS == 0 && 64 % CHUNKS == 0 && (TM * CHUNKS) % NTHR == 0, "whole rows per wavefront");
+    const int cc = (t % CHUNKS) * 8;
+    const int rr0 = t / CHUNKS;
+    union Chunk {
+        int4 v;
+        T h[8];
+    };
+    Chunk res[PASSES];
+    if (epi.mode == kEpiAdd) {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int64_t row = row0 + rr0 + p * (NTHR / CHUNKS);
+            res[p].v = row < n ? *(const int4 *) ((const T *) epi.residual + row * co + col0 + cc) : int4{0, 0, 0, 0};
+        }
+    }
+    float bv[8], gv[8], sv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        bv[u] = bias != nullptr ? bias[col0 + cc + u] : 0.0f;
+        gv[u] = epi.gamma != nullptr ? epi.gamma[col0 + cc + u] : 1.0f;
+        sv[u] = epi.beta != nullptr ? epi.beta[col0 + cc + u] : 0.0f;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int rr = rr0 + p * (NTHR / CHUNKS);
         const int64_t row = row0 + rr;
-        if (row >= n) continue;
-        union {
-            int4 v;
-            T h[8];
-        } o;
+        Chunk o;
+        float v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const float bv = bias != nullptr ? bias[col0 + cc + u] : 0.0f;
-            const float v = s_acc[rr * BN + cc + u] + bv;
-            if constexpr (DT == kBF16) {
-                o.h[u] = f32_to_bf16(v);
-            } else {
-                o.h[u] = (T) v;
-            }
+            Store<DT>::st(o.h, u, s_acc[rr * BN + cc + u] + bv[u]);
+            v[u] = Store<DT>::ld(o.h, u);
         }
-        *(int4 *) (y + row * co + col0 + cc) = o.v;
+        if (epi.mode == kEpiNorm) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) sum += v[u];
+#pragma unroll
+            for (int d = CHUNKS / 2; d >= 1; d >>= 1) sum += __shfl_xor(sum, d);
+            const float mean = sum / (float) BN;
+            float q = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) q += (v[u] - mean) * (v[u] - mean);
+#pragma unroll
+            for (int d = CHUNKS / 2; d >= 1; d >>= 1) q += __shfl_xor(q, d);
+            const float inv = 1.0f / sqrtf(q / (float) BN + epi.eps);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                float r = (v[u] - mean) * inv;
+                if (epi.gamma != nullptr) r *= gv[u];
+                if (epi.beta != nullptr) r += sv[u];
+                if (epi.silu) r = r * __builtin_amdgcn_rcpf(1.0f + __expf(-r));
+                Store<DT>::st(o.h, u, r);
+            }
+        } else if (epi.mode == kEpiAdd) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) Store<DT>::st(o.h, u, v[u] + Store<DT>::ld(res[p].h, u));
+        }
+        if (row < n) *(int4 *) (y + row * co + col0 + cc) = o.v;
     }
 }
 
@@ -985,7 +1034,8 @@ namespace {
 template <int DT, int BN, int DEPTH, int NW, int RG, int UPB>
 hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
                            const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
-                           const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
+                           const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
+                           const ConvEpilogue & epi) {
     using T = typename Store<DT>::T;
     const int64_t tiles = (n + kMapTile - 1) / kMapTile;
     const int64_t col_tiles = co / BN;
@@ -999,13 +1049,14 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32
         if (UPB == 1 && ci % 256 == 0) {
             k_conv_mfma_wreg<DT, BN, 2, UPB, UPB == 1 ? 8 : 4><<<(unsigned) grid, 512, 0, s>>>(
                 (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co,
-                col_tiles);
+                col_tiles, epi);
         } else {
             k_conv_mfma_wreg<DT, BN, 2, UPB, 4><<<(unsigned) grid, 512, 0, s>>>(
                 (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co,
-                col_tiles);
+                col_tiles, epi);
         }
     } else {
+        if (epi.mode != kEpiNone) return hipErrorInvalidValue;  // 64-channel blocks: plain epilogue only
         k_conv_mfma_stream<DT, BN, DEPTH, NW, RG, UPB><<<(unsigned) grid, 64 * NW, 0, s>>>(
             (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co,
             col_tiles);
@@ -1016,12 +1067,14 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32
 template <int DT>
 hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
                             const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
-                            const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
+                            const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
+                            const ConvEpilogue & epi) {
     const bool wide = co % 128 == 0;
     const bool pair = ci == 64;  // two 2-step units per 4-step block
 #define TSH_STREAM(BNV, UV)                                                                                       \
     launch_stream_t<DT, BNV, 4, TSH_STREAM_WAVES, TSH_STREAM_ROW_GROUPS, UV>(x, pair_src, pair_dst, tile_off,      \
-                                                                           tile_counts, w16, bias, y, n, ci, co, s)
+                                                                           tile_counts, w16, bias, y, n, ci, co, s, \
+                                                                           epi)
     if (wide) return pair ? TSH_STREAM(128, 2) : TSH_STREAM(128, 1);
     return pair ? TSH_STREAM(64, 2) : TSH_STREAM(64, 1);
 #undef TSH_STREAM
@@ -1030,14 +1083,16 @@ hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int3
 
 hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const int32_t * pair_dst,
                                    const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
-                                   const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s) {
-    if (!conv_stream_supported(dtype, ci, co)) {
+                                   const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
+                                   const ConvEpilogue & epi) {
+    if (!conv_stream_supported(dtype, ci, co) || (epi.mode == kEpiNorm && co != 128) ||
+        (epi.mode != kEpiNone && co % 128 != 0)) {
         return hipErrorInvalidValue;
     }
     if (dtype == kBF16) {
-        return launch_stream_dt<kBF16>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
+        return launch_stream_dt<kBF16>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s, epi);
     }
-    return launch_stream_dt<kF16>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s);
+    return launch_stream_dt<kF16>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s, epi);
 }
 
 }  // namespace tsh

@@ -181,6 +181,21 @@ bool conv_mfma_supported(int dtype, int ci, int co);
 hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nbr, const uint32_t * mask,
                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
                                    hipStream_t s);
+// Epilogue of the 128-channel compacted conv: after bias and the rounding to
+// the storage type, optionally a row norm (+ SiLU) over whole rows (co ==
+// 128, one block holds every channel of its rows) or a residual add
+// (rounded again), as the slot sequences conv -> row_norm(_silu) and
+// conv -> add compute them.
+struct ConvEpilogue {
+    int mode = 0;  // kEpiNone, kEpiNorm, kEpiAdd
+    int silu = 0;
+    float eps = 0.0f;
+    const float * gamma = nullptr;
+    const float * beta = nullptr;
+    const void * residual = nullptr;  // storage type [n][co]
+};
+enum { kEpiNone = 0, kEpiNorm = 1, kEpiAdd = 2 };
+
 // Streamed compacted schedule over the tile-major pair lists (needs ci == 64 or ci % 128 == 0).
 // Its weights use the grouped packing: [27][ci/8][co][8] whose packed column
 // b*16g + nt*16 + l holds channel b*16g + l*g + nt, g = conv_stream_group(co).
@@ -188,7 +203,8 @@ int conv_stream_group(int co);
 bool conv_stream_supported(int dtype, int ci, int co);
 hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const int32_t * pair_dst,
                                    const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
-                                   const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s);
+                                   const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
+                                   const ConvEpilogue & epi = ConvEpilogue());
 
 // Everything else (kernels_misc.hip).
 hipError_t launch_convert_from_f32(int dtype, const float * src, void * dst, int64_t count, hipStream_t s);

@@ -128,6 +128,9 @@ ABI = {
     "trellis_sparse_hip_dump_map_coords": (c_int, [_p, _p, c_char_p, _p]),
     "trellis_sparse_hip_convnext_mlp": (c_int, [_p, _p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _p, _p, c_int64,
                                                 c_int, c_float]),
+    "trellis_sparse_hip_conv_norm": (c_int, [_p, _p, _p, _f32p, _f32p, _f32p, _f32p, c_float, c_int, _p, c_int64,
+                                             c_int, c_int]),
+    "trellis_sparse_hip_conv_add": (c_int, [_p, _p, _p, _f32p, _f32p, _p, _p, c_int64, c_int, c_int]),
 }
 
 
@@ -415,6 +418,22 @@ class Backend:
                                                         _ptr(w0a, _f32p), _ptr(b0a, _f32p), _ptr(w2a, _f32p),
                                                         _ptr(b2a, _f32p), residual.handle, y.handle, n, c, eps),
                     "convnext_mlp")
+
+    def conv_norm(self, rb: Rulebook, x: Buffer, weight, bias, gamma, beta, eps: float, out: Buffer, ci: int,
+                  co: int, silu: bool = False):
+        """Fused sparse_conv3d -> row_norm(_silu); raises HipError(NOT_IMPLEMENTED) where it does not apply."""
+        w = self.keep(_f32(weight))
+        b, g, bt = (None if a is None else self.keep(_f32(a)) for a in (bias, gamma, beta))
+        self._check(LIB.trellis_sparse_hip_conv_norm(self.ptr, rb.handle, x.handle, _ptr(w, _f32p), _ptr(b, _f32p),
+                                                     _ptr(g, _f32p), _ptr(bt, _f32p), eps, int(silu), out.handle,
+                                                     rb.n, ci, co), "conv_norm")
+
+    def conv_add(self, rb: Rulebook, x: Buffer, weight, bias, residual: Buffer, out: Buffer, ci: int, co: int):
+        """Fused sparse_conv3d -> add(residual); raises HipError(NOT_IMPLEMENTED) where it does not apply."""
+        w = self.keep(_f32(weight))
+        b = None if bias is None else self.keep(_f32(bias))
+        self._check(LIB.trellis_sparse_hip_conv_add(self.ptr, rb.handle, x.handle, _ptr(w, _f32p), _ptr(b, _f32p),
+                                                    residual.handle, out.handle, rb.n, ci, co), "conv_add")
 
     def silu_inplace(self, x: Buffer, count: int):
         self._check(self.ops.silu_inplace(self.ptr, x.handle, count), "silu_inplace")
