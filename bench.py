@@ -158,6 +158,8 @@ class Block:
       (src/architectures/sparse_unet_decoder/executor.c:176-255).
     convnext_fused: the same block with its tail (row_norm .. add) in the one
       fused entry point trellis_sparse_hip_convnext_mlp.
+    convnext_block: the whole block in trellis_sparse_hip_convnext_block (the
+      conv with the norm in its epilogue, then the MLP kernel without the norm).
     s2c: the encoder's S2C down-block on the ~1.26M config-3 children, Ci = 64 -> Co = 128
       (sparse_unet_encoder/executor.c:160-360): row_norm_silu -> conv(64->16) on the fine
       rulebook; S2C map, pack and skip mean on the device (the reference does these on
@@ -186,7 +188,7 @@ class Block:
         w = wl.workload(3)
         rng = np.random.default_rng(11)
         f32 = lambda a: np.ascontiguousarray(a, np.float32)
-        if kind in ("convnext", "convnext_fused"):
+        if kind in ("convnext", "convnext_fused", "convnext_block"):
             c = 128
             pmap = be.upload_coords(w["parent_coords"])
             dm = be.build_c2s_map_device(be.upload(w["logits"]), w["parent_coords"].shape[0], coords_map=pmap)
@@ -207,6 +209,8 @@ class Block:
             self.slots = ["sparse_conv3d", "row_norm", "linear_silu", "linear", "add"]
             if kind == "convnext_fused":
                 self.slots = ["sparse_conv3d", "convnext_mlp"]
+            if kind == "convnext_block":
+                self.slots = ["convnext_block"]
         elif kind == "mesh":
             pmap = be.upload_coords(w["parent_coords"])
             dm = be.build_c2s_map_device(be.upload(w["logits"]), w["parent_coords"].shape[0], coords_map=pmap)
@@ -318,6 +322,11 @@ class Block:
             be.free_map(fmap)
             be.free_map(cmap)
             return
+        if self.kind == "convnext_block":
+            be.convnext_block(self.rb, self.h, self.conv_w, self.conv_b, self.gamma, self.beta, self.w0, self.b0,
+                              self.w2, self.b2, self.bufs[4], self.c, 1e-6)
+            be.event(next(ev))
+            return
         if self.kind == "convnext_fused":
             conv, out = self.bufs[0], self.bufs[4]
             be.conv(self.rb, self.h, self.conv_w, self.conv_b, conv, self.c, self.c)
@@ -374,7 +383,7 @@ class Block:
             return 0
         if self.kind == "s2c":
             return wl.conv_flops(self.fpairs, self.ci, self.co // 8) + wl.conv_flops(self.pairs, self.co, self.co)
-        if self.kind in ("convnext", "convnext_fused"):
+        if self.kind in ("convnext", "convnext_fused", "convnext_block"):
             n, c = self.n, self.c
             return wl.conv_flops(self.pairs, c, c) + 2 * (2 * n * c * 4 * c)
         return (wl.conv_flops(self.ppairs, self.ci, 8 * self.co) + wl.conv_flops(self.pairs, self.co, self.co)
@@ -429,7 +438,7 @@ def run_block(args):
                     "s2c_map_mvoxels_per_s": round(job.n / (map_ms * 1e-3) / 1e6, 1),
                     "s2c_map_cpu_oracle_ms": round(cpu_ms, 2),
                     "s2c_map_cpu_note": "oracle/trellis_oracle.c orc_s2c_map (qsort, 1 thread), same fine voxels"})
-    elif args.block in ("convnext", "convnext_fused"):
+    elif args.block in ("convnext", "convnext_fused", "convnext_block"):
         out.update({"voxels": int(job.n), "pairs": int(job.pairs), "channels": job.c})
     else:
         out.update({"parents": int(job.n), "children": int(job.m), "parent_pairs": int(job.ppairs),
@@ -498,7 +507,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-stride", type=int, default=16)
     ap.add_argument("--conv-algo", type=int, default=sh.CONV_AUTO)
-    ap.add_argument("--block", choices=["convnext", "convnext_fused", "c2s", "s2c", "mesh"],
+    ap.add_argument("--block", choices=["convnext", "convnext_fused", "convnext_block", "c2s", "s2c", "mesh"],
                     help="instead of the configuration step, time one decoder block composed from the backend's "
                          "slots at config-3 scale and print its own JSON line")
     ap.add_argument("--slots", action="store_true",

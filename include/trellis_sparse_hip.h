@@ -398,6 +398,23 @@ trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend,
                                                const trellis_sparse_buffer * residual, trellis_sparse_buffer * y,
                                                int64_t n, int c, float eps);
 
+/* The whole ConvNeXt block (sparse_unet_decoder/executor.c:176-255):
+ * out = h + mlp2(SiLU(mlp0(row_norm(sparse_conv3d(h), gamma, beta, eps)))),
+ * h and out [n][c] (out must not be h), conv_w fp32 [c][27][c], conv_b [c],
+ * the rest as in trellis_sparse_hip_convnext_mlp.  At c = 128 with the
+ * compacted conv the norm runs in the conv's epilogue and the MLP kernel
+ * takes the normalised rows; otherwise the conv is plain and the MLP kernel
+ * normalises.  Storage roundings where the slot sequence stores.
+ * TRELLIS_STATUS_NOT_IMPLEMENTED unless compute_dtype is F16 or BF16 and c is
+ * 64 or 128. */
+trellis_status trellis_sparse_hip_convnext_block(trellis_sparse_backend * backend,
+                                                 const trellis_sparse_rulebook * rulebook,
+                                                 const trellis_sparse_buffer * h, const float * conv_w,
+                                                 const float * conv_b, const float * gamma, const float * beta,
+                                                 const float * mlp0_w, const float * mlp0_b, const float * mlp2_w,
+                                                 const float * mlp2_b, trellis_sparse_buffer * out, int64_t n, int c,
+                                                 float eps);
+
 /* ------------------------------------------------------------------------ */
 /* Convs with a fused epilogue (no counterpart in the reference vtable: each */
 /* replaces a slot pair of the residual blocks, sparse_unet_decoder/         */

@@ -199,6 +199,105 @@ def test_convnext_mlp_rejects_unsupported(backends):
         assert ei.value.status == sh.NOT_IMPLEMENTED
 
 
+def convnext_block_params(rng, c, dtype):
+    conv_w = weights(rng, c, 27, c, dtype)
+    conv_b = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    return (conv_w, conv_b) + mlp_params(rng, c, dtype)
+
+
+def oracle_convnext_block(coords, h, params, c, dtype):
+    """The slot chain row by row on the oracle, rounded where the slots store."""
+    rnd = lambda a: sh.storage_round(a, dtype)
+    conv_w, conv_b, gamma, beta, w0, b0, w2, b2 = params
+    n = h.shape[0]
+    e = rnd(orc.Rulebook(coords).conv(h, conv_w, conv_b, c, c))
+    e = rnd(orc.row_norm(e, gamma, beta, n, c, 1e-6))
+    e = rnd(orc.linear(e, w0, b0, n, c, 4 * c, silu=True))
+    e = rnd(orc.linear(e, w2, b2, n, 4 * c, c))
+    return rnd(orc.add(h, e))
+
+
+@pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
+@pytest.mark.parametrize("c", [64, 128])
+@pytest.mark.parametrize("n", [1, 300, 6000])
+def test_convnext_block_entry_vs_oracle(backends, dtype, c, n):
+    """trellis_sparse_hip_convnext_block (conv with the norm epilogue at c =
+    128, the norm in the MLP kernel at c = 64) against the oracle's slot chain
+    from the block input; the tolerance is the end-to-end one of the slot
+    sequence above (each slot within the storage tolerance, compounded)."""
+    be = backends[dtype]
+    rnd = lambda a: sh.storage_round(a, dtype)
+    rng = np.random.default_rng(500 + c + n + dtype)
+    coords = shell_coords(n)
+    say(f"convnext_block entry dtype={dtype} c={c} n={n}")
+    h = rnd(rng.standard_normal((n, c)))
+    params = convnext_block_params(rng, c, dtype)
+    rb = be.build_rulebook(coords)
+    hb, out = be.upload(h), be.alloc(n * c)
+    be.convnext_block(rb, hb, *params, out, c, 1e-6)
+    got = be.download(out).reshape(n, c)
+    err = max_rel_err(got, oracle_convnext_block(coords, h, params, c, dtype))
+    say(f"convnext_block entry dtype={dtype} c={c} n={n} max_rel_err={err:.3e}")
+    assert err <= 5e-2
+    rb.free()
+
+
+@pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
+@pytest.mark.parametrize("c", [64, 128])
+def test_convnext_block_entry_vs_slots(backends, dtype, c):
+    """On the config-2 voxels: the block entry against the five slots on the
+    same inputs, to the storage tolerance (the norm's sums follow the row_norm
+    slot's order; the MLP's as in the fused tail)."""
+    be = backends[dtype]
+    rnd = lambda a: sh.storage_round(a, dtype)
+    rng = np.random.default_rng(900 + c + dtype)
+    coords = np.ascontiguousarray(wl.make_coords(2))
+    n = coords.shape[0]
+    say(f"convnext_block entry vs slots dtype={dtype} c={c} n={n}")
+    h = rnd(rng.standard_normal((n, c)))
+    conv_w, conv_b, gamma, beta, w0, b0, w2, b2 = convnext_block_params(rng, c, dtype)
+    rb = be.build_rulebook(coords)
+    hb = be.upload(h)
+    conv, norm, mlp1, mlp2, ref = (be.alloc(n * c), be.alloc(n * c), be.alloc(n * 4 * c), be.alloc(n * c),
+                                   be.alloc(n * c))
+    be.conv(rb, hb, conv_w, conv_b, conv, c, c)
+    be.row_norm(conv, gamma, beta, norm, n, c, 1e-6)
+    be.linear(norm, w0, b0, mlp1, n, c, 4 * c, silu=True)
+    be.linear(mlp1, w2, b2, mlp2, n, 4 * c, c)
+    be.add(hb, mlp2, ref, n * c)
+    out = be.alloc(n * c)
+    be.convnext_block(rb, hb, conv_w, conv_b, gamma, beta, w0, b0, w2, b2, out, c, 1e-6)
+    got, exp = be.download(out), be.download(ref)
+    err = max_rel_err(got, exp)
+    say(f"convnext_block entry vs slots dtype={dtype} c={c} max_rel_err={err:.3e}")
+    assert err <= TOL[dtype]
+    rb.free()
+
+
+def test_convnext_block_entry_rejects(backends):
+    """fp32 storage, c other than 64 / 128, and out aliasing h are refused
+    before anything is launched."""
+    rng = np.random.default_rng(6)
+    coords = shell_coords(50)
+    n = coords.shape[0]
+    for dtype, c, status in ((sh.F32, 64, sh.NOT_IMPLEMENTED), (sh.BF16, 96, sh.NOT_IMPLEMENTED),
+                             (sh.F16, 256, sh.NOT_IMPLEMENTED)):
+        be = backends[dtype]
+        rb = be.build_rulebook(coords)
+        hb, out = be.upload(np.zeros((n, c), np.float32)), be.alloc(n * c)
+        with pytest.raises(sh.HipError) as ei:
+            be.convnext_block(rb, hb, *convnext_block_params(rng, c, sh.F32), out, c, 1e-6)
+        assert ei.value.status == status
+        rb.free()
+    be = backends[sh.BF16]
+    rb = be.build_rulebook(coords)
+    hb = be.upload(np.zeros((n, 128), np.float32))
+    with pytest.raises(sh.HipError) as ei:
+        be.convnext_block(rb, hb, *convnext_block_params(rng, 128, sh.F32), hb, 128, 1e-6)
+    assert ei.value.status == sh.INVALID_ARGUMENT
+    rb.free()
+
+
 @pytest.mark.parametrize("dtype", [sh.F32, sh.BF16])
 def test_c2s_upblock_vs_oracle(backends, dtype):
     be = backends[dtype]

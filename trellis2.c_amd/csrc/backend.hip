@@ -509,10 +509,11 @@ trellis_status op_linear_silu(trellis_sparse_backend * backend, const trellis_sp
 }
 
 // The ConvNeXt block's MLP tail fused: y = residual + W2 SiLU(W0 LN(x) + b0) + b2.
+// norm = 0: x is already the normalised LN output (gamma, beta and eps unused).
 trellis_status mlp_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * gamma,
                         const float * beta, const float * w0, const float * b0, const float * w2, const float * b2,
                         const trellis_sparse_buffer * residual, trellis_sparse_buffer * y, int64_t n, int c,
-                        float eps) {
+                        float eps, int norm = 1) {
     if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
     Backend * be = as_backend(backend);
     if (w0 == nullptr || w2 == nullptr || n <= 0 || c <= 0 || !(eps >= 0.0f) ||
@@ -525,8 +526,11 @@ trellis_status mlp_impl(trellis_sparse_backend * backend, const trellis_sparse_b
     }
     CallScope scope(be);
     const void *g = nullptr, *bt = nullptr, *pw0 = nullptr, *pb0 = nullptr, *pw2 = nullptr, *pb2 = nullptr;
-    trellis_status st = get_weight(be, gamma, (size_t) c, kLayoutVector, 0, c, &g);
-    if (st == TRELLIS_STATUS_OK) st = get_weight(be, beta, (size_t) c, kLayoutVector, 0, c, &bt);
+    trellis_status st = TRELLIS_STATUS_OK;
+    if (norm) {
+        st = get_weight(be, gamma, (size_t) c, kLayoutVector, 0, c, &g);
+        if (st == TRELLIS_STATUS_OK) st = get_weight(be, beta, (size_t) c, kLayoutVector, 0, c, &bt);
+    }
     if (st == TRELLIS_STATUS_OK) st = get_weight(be, w0, (size_t) c * 4 * c, kLayoutMlp0, c, 4 * c, &pw0);
     if (st == TRELLIS_STATUS_OK) st = get_weight(be, b0, (size_t) 4 * c, kLayoutVector, 0, 4 * c, &pb0);
     if (st == TRELLIS_STATUS_OK) st = get_weight(be, w2, (size_t) 4 * c * c, kLayoutMlp2, 4 * c, c, &pw2);
@@ -535,8 +539,8 @@ trellis_status mlp_impl(trellis_sparse_backend * backend, const trellis_sparse_b
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
     const hipError_t err =
         launch_convnext_mlp(be->policy.compute_dtype, x->ptr, (const float *) g, (const float *) bt, pw0,
-                            (const float *) pb0, pw2, (const float *) pb2, residual->ptr, y->ptr, n, c, eps, be->cus,
-                            be->stream);
+                            (const float *) pb0, pw2, (const float *) pb2, residual->ptr, y->ptr, n, c, eps, norm,
+                            be->cus, be->stream);
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
     return hip_status(be, err, "convnext_mlp");
 }
@@ -857,6 +861,48 @@ trellis_status conv_add_impl(trellis_sparse_backend * backend, const trellis_spa
     epi.mode = kEpiAdd;
     epi.residual = residual->ptr;
     return conv_impl(backend, rulebook, feats, weight, bias, out, n, ci, co, &epi, "conv_add");
+}
+
+// The whole ConvNeXt block: out = h + MLP(LN(conv(h))).  Where the conv's
+// norm epilogue applies (C = 128, compacted conv) the LN runs there and the
+// MLP kernel takes the normalised rows; otherwise the conv is plain and the
+// MLP kernel normalises.  One n x C intermediate either way.
+trellis_status block_impl(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
+                          const trellis_sparse_buffer * h, const float * conv_w, const float * conv_b,
+                          const float * gamma, const float * beta, const float * w0, const float * b0,
+                          const float * w2, const float * b2, trellis_sparse_buffer * out, int64_t n, int c,
+                          float eps) {
+    if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = as_backend(backend);
+    if (rulebook == nullptr || conv_w == nullptr || w0 == nullptr || w2 == nullptr || n <= 0 || c <= 0 ||
+        n != rulebook->n || !(eps > 0.0f) || !float_buffer_ok(be, h, (size_t) n * c) ||
+        !float_buffer_ok(be, out, (size_t) n * c) || h->ptr == out->ptr) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "convnext_block: bad argument");
+    }
+    const int dt = be->policy.compute_dtype;
+    if (!convnext_mlp_supported(dt, c)) {
+        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, "convnext_block: needs bf16/fp16 storage and c = 64 or 128");
+    }
+    const bool fused_norm = c == 128 && conv_stream_supported(dt, c, c) &&
+                            (be->policy.conv_algo == TRELLIS_SPARSE_HIP_CONV_AUTO ||
+                             be->policy.conv_algo == TRELLIS_SPARSE_HIP_CONV_COMPACT);
+    trellis_sparse_buffer * tmp = nullptr;
+    trellis_status st = op_alloc_f32(backend, (size_t) n * c, &tmp);
+    if (st != TRELLIS_STATUS_OK) return st;
+    if (fused_norm) {
+        ConvEpilogue epi;
+        epi.mode = kEpiNorm;
+        epi.eps = eps;
+        epi.gamma = gamma;
+        epi.beta = beta;
+        st = conv_impl(backend, rulebook, h, conv_w, conv_b, tmp, n, c, c, &epi, "convnext_block");
+        if (st == TRELLIS_STATUS_OK) st = mlp_impl(backend, tmp, nullptr, nullptr, w0, b0, w2, b2, h, out, n, c, eps, 0);
+    } else {
+        st = conv_impl(backend, rulebook, h, conv_w, conv_b, tmp, n, c, c, nullptr, "convnext_block");
+        if (st == TRELLIS_STATUS_OK) st = mlp_impl(backend, tmp, gamma, beta, w0, b0, w2, b2, h, out, n, c, eps, 1);
+    }
+    op_free_buffer(backend, tmp);
+    return st;
 }
 
 void op_free_rulebook(trellis_sparse_backend * backend, trellis_sparse_rulebook * rulebook) {
@@ -1888,6 +1934,17 @@ trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend,
                                                const trellis_sparse_buffer * residual, trellis_sparse_buffer * y,
                                                int64_t n, int c, float eps) {
     return tsh::mlp_impl(backend, x, gamma, beta, mlp0_w, mlp0_b, mlp2_w, mlp2_b, residual, y, n, c, eps);
+}
+
+trellis_status trellis_sparse_hip_convnext_block(trellis_sparse_backend * backend,
+                                                 const trellis_sparse_rulebook * rulebook,
+                                                 const trellis_sparse_buffer * h, const float * conv_w,
+                                                 const float * conv_b, const float * gamma, const float * beta,
+                                                 const float * mlp0_w, const float * mlp0_b, const float * mlp2_w,
+                                                 const float * mlp2_b, trellis_sparse_buffer * out, int64_t n, int c,
+                                                 float eps) {
+    return tsh::block_impl(backend, rulebook, h, conv_w, conv_b, gamma, beta, mlp0_w, mlp0_b, mlp2_w, mlp2_b, out, n,
+                           c, eps);
 }
 
 trellis_status trellis_sparse_hip_conv_norm(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,

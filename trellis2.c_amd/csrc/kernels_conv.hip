@@ -626,6 +626,15 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
 // between fetch and use.
 // ---------------------------------------------------------------------------
 
+// Sum over the 16 lanes of a DPP row, left in every lane of the row:
+// rotations by 8, 4, 2 and 1 within the row (row_ror), each one VALU add.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
+    return v;
+}
 
 template <int DT, int BN, int RG, int UPB, int DEPTH>
 __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,
@@ -675,6 +684,29 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     const int col0 = (int) (logical % n_col_tiles) * BN;
     const int ci8 = ci >> 3;
     const int KS = ci / BK;
+
+    // Epilogue operands fetched now, so that their latency hides under the
+    // main loop: this thread's residual chunks (add epilogue).  Thread t
+    // handles chunk column cc of rows rr0 + p * (NTHR / CHUNKS) in the
+    // epilogue; a block reads these residual rows before it writes the same
+    // rows of y, so y may be the residual buffer.
+    constexpr int CHUNKS = BN / 8;
+    constexpr int PASSES = TM * CHUNKS / NTHR;
+    static_assert(NTHR % CHUNKS == 0 && 64 % CHUNKS == 0 && (TM * CHUNKS) % NTHR == 0, "whole rows per wavefront");
+    const int cc = (t % CHUNKS) * 8;
+    const int rr0 = t / CHUNKS;
+    union Chunk {
+        int4 v;
+        T h[8];
+    };
+    Chunk res[PASSES];
+    if (epi.mode == kEpiAdd) {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int64_t row = row0 + rr0 + p * (NTHR / CHUNKS);
+            res[p].v = row < n ? *(const int4 *) ((const T *) epi.residual + row * co + col0 + cc) : int4{0, 0, 0, 0};
+        }
+    }
 
     for (int i = t; i < (TM + 1) * BN; i += NTHR) s_acc[i] = 0.0f;
     if (t < 27) {
@@ -886,27 +918,12 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     // row norm (+ SiLU) or residual add on the rounded values, rounded again.
     // A row's CHUNKS 16-byte chunks sit in CHUNKS consecutive lanes (each
     // thread keeps its chunk column on every pass), so the norm's sums are
-    // shuffle reductions inside those lanes; every thread takes part in them
-    // (rows past n are computed and not stored).  The residual chunks, bias,
-    // scale and shift are fetched before the barrier, all passes at once, so
-    // their latency overlaps the last accumulator flush.
-    constexpr int CHUNKS = BN / 8;
-    constexpr int PASSES = TM * CHUNKS / NTHR;
-    static_assert(NTHR % CHUNKS == 0 && 64 % CHUNKS == 0 && (TM * CHUNKS) % NTHR == 0, "whole rows per wavefront");
-    const int cc = (t % CHUNKS) * 8;
-    const int rr0 = t / CHUNKS;
-    union Chunk {
-        int4 v;
-        T h[8];
-    };
-    Chunk res[PASSES];
-    if (epi.mode == kEpiAdd) {
-#pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const int64_t row = row0 + rr0 + p * (NTHR / CHUNKS);
-            res[p].v = row < n ? *(const int4 *) ((const T *) epi.residual + row * co + col0 + cc) : int4{0, 0, 0, 0};
-        }
-    }
+    // DPP row reductions over those lanes (a DPP row is 16 lanes); every
+    // thread takes part in them (rows past n are computed and not stored).
+    // Bias, scale and shift are fetched before the barrier so that their
+    // latency overlaps the last accumulator flush; the residual chunks were
+    // fetched at the start.
+    static_assert(CHUNKS == 16 || BN != 128, "a row's chunks fill one DPP row");
     float bv[8], gv[8], sv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -919,39 +936,40 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     for (int p = 0; p < PASSES; ++p) {
         const int rr = rr0 + p * (NTHR / CHUNKS);
         const int64_t row = row0 + rr;
-        Chunk o;
+        // Whole 16-byte chunks through the packed conversions: sum + bias,
+        // rounded to the storage type and widened again.
         float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            Store<DT>::st(o.h, u, s_acc[rr * BN + cc + u] + bv[u]);
-            v[u] = Store<DT>::ld(o.h, u);
-        }
+        for (int u = 0; u < 8; ++u) v[u] = s_acc[rr * BN + cc + u] + bv[u];
+        int4 o = pack_chunk<DT>(v);
         if (epi.mode == kEpiNorm) {
+            unpack_chunk<DT>(o, v);
             float sum = 0.0f;
 #pragma unroll
             for (int u = 0; u < 8; ++u) sum += v[u];
-#pragma unroll
-            for (int d = CHUNKS / 2; d >= 1; d >>= 1) sum += __shfl_xor(sum, d);
-            const float mean = sum / (float) BN;
+            const float mean = row16_sum(sum) / (float) BN;
             float q = 0.0f;
 #pragma unroll
             for (int u = 0; u < 8; ++u) q += (v[u] - mean) * (v[u] - mean);
-#pragma unroll
-            for (int d = CHUNKS / 2; d >= 1; d >>= 1) q += __shfl_xor(q, d);
-            const float inv = 1.0f / sqrtf(q / (float) BN + epi.eps);
+            const float inv = 1.0f / sqrtf(row16_sum(q) / (float) BN + epi.eps);
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 float r = (v[u] - mean) * inv;
                 if (epi.gamma != nullptr) r *= gv[u];
                 if (epi.beta != nullptr) r += sv[u];
                 if (epi.silu) r = r * __builtin_amdgcn_rcpf(1.0f + __expf(-r));
-                Store<DT>::st(o.h, u, r);
+                v[u] = r;
             }
+            o = pack_chunk<DT>(v);
         } else if (epi.mode == kEpiAdd) {
+            float rv[8];
+            unpack_chunk<DT>(o, v);
+            unpack_chunk<DT>(res[p].v, rv);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) Store<DT>::st(o.h, u, v[u] + Store<DT>::ld(res[p].h, u));
+            for (int u = 0; u < 8; ++u) v[u] += rv[u];
+            o = pack_chunk<DT>(v);
         }
-        if (row < n) *(int4 *) (y + row * co + col0 + cc) = o.v;
+        if (row < n) *(int4 *) (y + row * co + col0 + cc) = o;
     }
 }
 

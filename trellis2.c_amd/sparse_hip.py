@@ -128,6 +128,8 @@ ABI = {
     "trellis_sparse_hip_dump_map_coords": (c_int, [_p, _p, c_char_p, _p]),
     "trellis_sparse_hip_convnext_mlp": (c_int, [_p, _p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _p, _p, c_int64,
                                                 c_int, c_float]),
+    "trellis_sparse_hip_convnext_block": (c_int, [_p, _p, _p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                                  _p, c_int64, c_int, c_float]),
     "trellis_sparse_hip_conv_norm": (c_int, [_p, _p, _p, _f32p, _f32p, _f32p, _f32p, c_float, c_int, _p, c_int64,
                                              c_int, c_int]),
     "trellis_sparse_hip_conv_add": (c_int, [_p, _p, _p, _f32p, _f32p, _p, _p, c_int64, c_int, c_int]),
@@ -418,6 +420,17 @@ class Backend:
                                                         _ptr(w0a, _f32p), _ptr(b0a, _f32p), _ptr(w2a, _f32p),
                                                         _ptr(b2a, _f32p), residual.handle, y.handle, n, c, eps),
                     "convnext_mlp")
+
+    def convnext_block(self, rb: Rulebook, h: Buffer, conv_w, conv_b, gamma, beta, w0, b0, w2, b2, out: Buffer,
+                       c: int, eps: float):
+        """The whole ConvNeXt block: out = h + MLP(row_norm(conv(h)))."""
+        cw, w0a, w2a = self.keep(_f32(conv_w)), self.keep(_f32(w0)), self.keep(_f32(w2))
+        cb, g, bt, b0a, b2a = (None if a is None else self.keep(_f32(a)) for a in (conv_b, gamma, beta, b0, b2))
+        self._check(LIB.trellis_sparse_hip_convnext_block(self.ptr, rb.handle, h.handle, _ptr(cw, _f32p),
+                                                          _ptr(cb, _f32p), _ptr(g, _f32p), _ptr(bt, _f32p),
+                                                          _ptr(w0a, _f32p), _ptr(b0a, _f32p), _ptr(w2a, _f32p),
+                                                          _ptr(b2a, _f32p), out.handle, rb.n, c, eps),
+                    "convnext_block")
 
     def conv_norm(self, rb: Rulebook, x: Buffer, weight, bias, gamma, beta, eps: float, out: Buffer, ci: int,
                   co: int, silu: bool = False):
