@@ -586,21 +586,10 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
         const int rr = e / CHUNKS, cc = (e % CHUNKS) * 8;
         const int64_t row = row0 + rr;
         if (row >= n) continue;
-        union {
-            int4 v;
-            T h[8];
-        } o;
+        float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const float bv = bias != nullptr ? bias[col0 + cc + u] : 0.0f;
-            const float v = s_acc[rr * BN + cc + u] + bv;
-            if constexpr (DT == kBF16) {
-                o.h[u] = f32_to_bf16(v);
-            } else {
-                o.h[u] = (T) v;
-            }
-        }
-        *(int4 *) (y + row * co + col0 + cc) = o.v;
+        for (int u = 0; u < 8; ++u) v[u] = s_acc[rr * BN + cc + u] + (bias != nullptr ? bias[col0 + cc + u] : 0.0f);
+        *(int4 *) (y + row * co + col0 + cc) = pack_chunk<DT>(v);
     }
 }
 

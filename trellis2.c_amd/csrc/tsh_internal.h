@@ -48,7 +48,8 @@ template <> struct Store<kF16> {
 template <> struct Store<kBF16> {
     using T = uint16_t;
     __device__ static float ld(const T * p, int64_t i) { return bf16_to_f32(p[i]); }
-    __device__ static void st(T * p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+    // Round to nearest even with the hardware conversion (NaN stays NaN).
+    __device__ static void st(T * p, int64_t i, float v) { p[i] = __builtin_bit_cast(uint16_t, (__bf16) v); }
 };
 
 // A 16-byte chunk of 16-bit storage values (8 of them) to fp32 and back,
