@@ -158,8 +158,8 @@ class Block:
       (src/architectures/sparse_unet_decoder/executor.c:176-255).
     convnext_fused: the same block with its tail (row_norm .. add) in the one
       fused entry point trellis_sparse_hip_convnext_mlp.
-    convnext_block: the whole block in trellis_sparse_hip_convnext_block (the
-      conv with the norm in its epilogue, then the MLP kernel without the norm).
+    convnext_block: the whole block in one call, trellis_sparse_hip_convnext_block
+      (the conv into one intermediate, then the fused tail).
     s2c: the encoder's S2C down-block on the ~1.26M config-3 children, Ci = 64 -> Co = 128
       (sparse_unet_encoder/executor.c:160-360): row_norm_silu -> conv(64->16) on the fine
       rulebook; S2C map, pack and skip mean on the device (the reference does these on

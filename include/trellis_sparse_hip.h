@@ -401,10 +401,9 @@ trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend,
 /* The whole ConvNeXt block (sparse_unet_decoder/executor.c:176-255):
  * out = h + mlp2(SiLU(mlp0(row_norm(sparse_conv3d(h), gamma, beta, eps)))),
  * h and out [n][c] (out must not be h), conv_w fp32 [c][27][c], conv_b [c],
- * the rest as in trellis_sparse_hip_convnext_mlp.  At c = 128 with the
- * compacted conv the norm runs in the conv's epilogue and the MLP kernel
- * takes the normalised rows; otherwise the conv is plain and the MLP kernel
- * normalises.  Storage roundings where the slot sequence stores.
+ * the rest as in trellis_sparse_hip_convnext_mlp: the conv into one n x c
+ * intermediate, then the fused tail.  Storage roundings where the slot
+ * sequence stores.
  * TRELLIS_STATUS_NOT_IMPLEMENTED unless compute_dtype is F16 or BF16 and c is
  * 64 or 128. */
 trellis_status trellis_sparse_hip_convnext_block(trellis_sparse_backend * backend,

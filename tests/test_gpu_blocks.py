@@ -221,10 +221,10 @@ def oracle_convnext_block(coords, h, params, c, dtype):
 @pytest.mark.parametrize("c", [64, 128])
 @pytest.mark.parametrize("n", [1, 300, 6000])
 def test_convnext_block_entry_vs_oracle(backends, dtype, c, n):
-    """trellis_sparse_hip_convnext_block (conv with the norm epilogue at c =
-    128, the norm in the MLP kernel at c = 64) against the oracle's slot chain
-    from the block input; the tolerance is the end-to-end one of the slot
-    sequence above (each slot within the storage tolerance, compounded)."""
+    """trellis_sparse_hip_convnext_block (the conv, then the fused tail)
+    against the oracle's slot chain from the block input; the tolerance is the
+    end-to-end one of the slot sequence above (each slot within the storage
+    tolerance, compounded)."""
     be = backends[dtype]
     rnd = lambda a: sh.storage_round(a, dtype)
     rng = np.random.default_rng(500 + c + n + dtype)
@@ -246,8 +246,8 @@ def test_convnext_block_entry_vs_oracle(backends, dtype, c, n):
 @pytest.mark.parametrize("c", [64, 128])
 def test_convnext_block_entry_vs_slots(backends, dtype, c):
     """On the config-2 voxels: the block entry against the five slots on the
-    same inputs, to the storage tolerance (the norm's sums follow the row_norm
-    slot's order; the MLP's as in the fused tail)."""
+    same inputs, to the storage tolerance (the MLP's sums run in another order
+    than the linear slots')."""
     be = backends[dtype]
     rnd = lambda a: sh.storage_round(a, dtype)
     rng = np.random.default_rng(900 + c + dtype)

@@ -509,11 +509,10 @@ trellis_status op_linear_silu(trellis_sparse_backend * backend, const trellis_sp
 }
 
 // The ConvNeXt block's MLP tail fused: y = residual + W2 SiLU(W0 LN(x) + b0) + b2.
-// norm = 0: x is already the normalised LN output (gamma, beta and eps unused).
 trellis_status mlp_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * gamma,
                         const float * beta, const float * w0, const float * b0, const float * w2, const float * b2,
                         const trellis_sparse_buffer * residual, trellis_sparse_buffer * y, int64_t n, int c,
-                        float eps, int norm = 1) {
+                        float eps) {
     if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
     Backend * be = as_backend(backend);
     if (w0 == nullptr || w2 == nullptr || n <= 0 || c <= 0 || !(eps >= 0.0f) ||
@@ -526,11 +525,8 @@ trellis_status mlp_impl(trellis_sparse_backend * backend, const trellis_sparse_b
     }
     CallScope scope(be);
     const void *g = nullptr, *bt = nullptr, *pw0 = nullptr, *pb0 = nullptr, *pw2 = nullptr, *pb2 = nullptr;
-    trellis_status st = TRELLIS_STATUS_OK;
-    if (norm) {
-        st = get_weight(be, gamma, (size_t) c, kLayoutVector, 0, c, &g);
-        if (st == TRELLIS_STATUS_OK) st = get_weight(be, beta, (size_t) c, kLayoutVector, 0, c, &bt);
-    }
+    trellis_status st = get_weight(be, gamma, (size_t) c, kLayoutVector, 0, c, &g);
+    if (st == TRELLIS_STATUS_OK) st = get_weight(be, beta, (size_t) c, kLayoutVector, 0, c, &bt);
     if (st == TRELLIS_STATUS_OK) st = get_weight(be, w0, (size_t) c * 4 * c, kLayoutMlp0, c, 4 * c, &pw0);
     if (st == TRELLIS_STATUS_OK) st = get_weight(be, b0, (size_t) 4 * c, kLayoutVector, 0, 4 * c, &pb0);
     if (st == TRELLIS_STATUS_OK) st = get_weight(be, w2, (size_t) 4 * c * c, kLayoutMlp2, 4 * c, c, &pw2);
@@ -539,7 +535,7 @@ trellis_status mlp_impl(trellis_sparse_backend * backend, const trellis_sparse_b
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
     const hipError_t err =
         launch_convnext_mlp(be->policy.compute_dtype, x->ptr, (const float *) g, (const float *) bt, pw0,
-                            (const float *) pb0, pw2, (const float *) pb2, residual->ptr, y->ptr, n, c, eps, norm,
+                            (const float *) pb0, pw2, (const float *) pb2, residual->ptr, y->ptr, n, c, eps,
                             be->cus, be->stream);
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
     return hip_status(be, err, "convnext_mlp");
@@ -863,10 +859,10 @@ trellis_status conv_add_impl(trellis_sparse_backend * backend, const trellis_spa
     return conv_impl(backend, rulebook, feats, weight, bias, out, n, ci, co, &epi, "conv_add");
 }
 
-// The whole ConvNeXt block: out = h + MLP(LN(conv(h))).  Where the conv's
-// norm epilogue applies (C = 128, compacted conv) the LN runs there and the
-// MLP kernel takes the normalised rows; otherwise the conv is plain and the
-// MLP kernel normalises.  One n x C intermediate either way.
+// The whole ConvNeXt block: out = h + MLP(LN(conv(h))): the conv into one
+// n x C intermediate, then the fused tail, whose LN overlaps its second GEMM
+// (measured faster than the LN in the conv's epilogue, which runs after the
+// block's last MFMAs).
 trellis_status block_impl(trellis_sparse_backend * backend, const trellis_sparse_rulebook * rulebook,
                           const trellis_sparse_buffer * h, const float * conv_w, const float * conv_b,
                           const float * gamma, const float * beta, const float * w0, const float * b0,
@@ -883,24 +879,11 @@ trellis_status block_impl(trellis_sparse_backend * backend, const trellis_sparse
     if (!convnext_mlp_supported(dt, c)) {
         return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, "convnext_block: needs bf16/fp16 storage and c = 64 or 128");
     }
-    const bool fused_norm = c == 128 && conv_stream_supported(dt, c, c) &&
-                            (be->policy.conv_algo == TRELLIS_SPARSE_HIP_CONV_AUTO ||
-                             be->policy.conv_algo == TRELLIS_SPARSE_HIP_CONV_COMPACT);
     trellis_sparse_buffer * tmp = nullptr;
     trellis_status st = op_alloc_f32(backend, (size_t) n * c, &tmp);
     if (st != TRELLIS_STATUS_OK) return st;
-    if (fused_norm) {
-        ConvEpilogue epi;
-        epi.mode = kEpiNorm;
-        epi.eps = eps;
-        epi.gamma = gamma;
-        epi.beta = beta;
-        st = conv_impl(backend, rulebook, h, conv_w, conv_b, tmp, n, c, c, &epi, "convnext_block");
-        if (st == TRELLIS_STATUS_OK) st = mlp_impl(backend, tmp, nullptr, nullptr, w0, b0, w2, b2, h, out, n, c, eps, 0);
-    } else {
-        st = conv_impl(backend, rulebook, h, conv_w, conv_b, tmp, n, c, c, nullptr, "convnext_block");
-        if (st == TRELLIS_STATUS_OK) st = mlp_impl(backend, tmp, gamma, beta, w0, b0, w2, b2, h, out, n, c, eps, 1);
-    }
+    st = conv_impl(backend, rulebook, h, conv_w, conv_b, tmp, n, c, c, nullptr, "convnext_block");
+    if (st == TRELLIS_STATUS_OK) st = mlp_impl(backend, tmp, gamma, beta, w0, b0, w2, b2, h, out, n, c, eps);
     op_free_buffer(backend, tmp);
     return st;
 }

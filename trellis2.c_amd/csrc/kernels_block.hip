@@ -34,9 +34,7 @@
 namespace tsh {
 namespace {
 
-// NORM false: x is already the normalised (and rounded) LN output, as the
-// conv's norm epilogue writes it; it goes to s_x unchanged.
-template <int DT, int C, bool NORM>
+template <int DT, int C>
 __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::T * __restrict__ x,
                                                       const float * __restrict__ gamma,
                                                       const float * __restrict__ beta,
@@ -125,10 +123,6 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
 #pragma unroll
         for (int p = 0; p < LNP; ++p) {
             const int rloc = wave * 8 + p * RPP + lane / LPR;
-            if constexpr (!NORM) {
-                *(int4 *) (&s_x[opnd(li / 4, rloc / 16, rloc % 16, li % 4)]) = xr[p];
-                continue;
-            }
             float v[8];
             unpack_chunk<DT>(xr[p], v);
             float s = 0.0f;
@@ -274,21 +268,15 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
 
 template <int DT, int C>
 hipError_t launch_mlp_t(const void * x, const float * gamma, const float * beta, const void * w0, const float * b0,
-                        const void * w2, const float * b2, const void * res, void * y, int64_t n, float eps, int norm,
-                        int cus, hipStream_t s) {
+                        const void * w2, const float * b2, const void * res, void * y, int64_t n, float eps, int cus,
+                        hipStream_t s) {
     using T = typename Store<DT>::T;
     const int64_t tiles = (n + 63) / 64;
     if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
     const int64_t grid = tiles < cus ? tiles : cus;
-    if (norm) {
-        k_convnext_mlp<DT, C, true><<<(unsigned) grid, 512, 0, s>>>((const T *) x, gamma, beta, (const T *) w0, b0,
-                                                                   (const T *) w2, b2, (const T *) res, (T *) y, n,
-                                                                   eps, (int) tiles);
-    } else {
-        k_convnext_mlp<DT, C, false><<<(unsigned) grid, 512, 0, s>>>((const T *) x, nullptr, nullptr,
-                                                                    (const T *) w0, b0, (const T *) w2, b2,
-                                                                    (const T *) res, (T *) y, n, eps, (int) tiles);
-    }
+    k_convnext_mlp<DT, C><<<(unsigned) grid, 512, 0, s>>>((const T *) x, gamma, beta, (const T *) w0, b0,
+                                                         (const T *) w2, b2, (const T *) res, (T *) y, n, eps,
+                                                         (int) tiles);
     return hipGetLastError();
 }
 }  // namespace
@@ -302,14 +290,14 @@ void convnext_mlp_groups(int c, int * g0, int * g2) {
 
 hipError_t launch_convnext_mlp(int dtype, const void * x, const float * gamma, const float * beta, const void * w0,
                                const float * b0, const void * w2, const float * b2, const void * res, void * y,
-                               int64_t n, int c, float eps, int norm, int cus, hipStream_t s) {
+                               int64_t n, int c, float eps, int cus, hipStream_t s) {
     if (!convnext_mlp_supported(dtype, c) || n <= 0 || cus <= 0) return hipErrorInvalidValue;
     if (dtype == kBF16) {
-        return c == 128 ? launch_mlp_t<kBF16, 128>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, norm, cus, s)
-                        : launch_mlp_t<kBF16, 64>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, norm, cus, s);
+        return c == 128 ? launch_mlp_t<kBF16, 128>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, cus, s)
+                        : launch_mlp_t<kBF16, 64>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, cus, s);
     }
-    return c == 128 ? launch_mlp_t<kF16, 128>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, norm, cus, s)
-                    : launch_mlp_t<kF16, 64>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, norm, cus, s);
+    return c == 128 ? launch_mlp_t<kF16, 128>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, cus, s)
+                    : launch_mlp_t<kF16, 64>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, cus, s);
 }
 
 }  // namespace tsh

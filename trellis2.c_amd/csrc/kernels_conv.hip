@@ -27,6 +27,8 @@
 //               of 128 output channels run k_conv_mfma_wreg (weights in
 //               registers, feature rows shared through LDS), blocks of 64
 //               k_conv_mfma_stream (weights shared through LDS).
+#include <type_traits>
+
 #include "tsh_internal.h"
 #include "mfma_common.h"
 
@@ -913,6 +915,7 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     // latency overlaps the last accumulator flush; the residual chunks were
     // fetched at the start.
     static_assert(CHUNKS == 16 || BN != 128, "a row's chunks fill one DPP row");
+    // Missing scale / shift are 1 and 0 (exact in r * g + b).
     float bv[8], gv[8], sv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -921,44 +924,63 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
         sv[u] = epi.beta != nullptr ? epi.beta[col0 + cc + u] : 0.0f;
     }
     lds_barrier();
+    // One copy of the pass loop per epilogue kind, so that no kind pays for
+    // another's arithmetic.
+    auto passes = [&](auto mode_c, auto silu_c) {
+        constexpr int MODE = decltype(mode_c)::value;
+        constexpr bool SILU = decltype(silu_c)::value;
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-        const int rr = rr0 + p * (NTHR / CHUNKS);
-        const int64_t row = row0 + rr;
-        // Whole 16-byte chunks through the packed conversions: sum + bias,
-        // rounded to the storage type and widened again.
-        float v[8];
+        for (int p = 0; p < PASSES; ++p) {
+            const int rr = rr0 + p * (NTHR / CHUNKS);
+            const int64_t row = row0 + rr;
+            // Whole 16-byte chunks through the packed conversions: sum +
+            // bias, rounded to the storage type (and widened again).
+            float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = s_acc[rr * BN + cc + u] + bv[u];
-        int4 o = pack_chunk<DT>(v);
-        if (epi.mode == kEpiNorm) {
-            unpack_chunk<DT>(o, v);
-            float sum = 0.0f;
+            for (int u = 0; u < 8; ++u) v[u] = s_acc[rr * BN + cc + u] + bv[u];
+            int4 o = pack_chunk<DT>(v);
+            if constexpr (MODE == kEpiNorm) {
+                unpack_chunk<DT>(o, v);
+                float sum = 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) sum += v[u];
-            const float mean = row16_sum(sum) / (float) BN;
-            float q = 0.0f;
+                for (int u = 0; u < 8; ++u) sum += v[u];
+                const float mean = row16_sum(sum) / (float) BN;
+                float q = 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) q += (v[u] - mean) * (v[u] - mean);
-            const float inv = 1.0f / sqrtf(row16_sum(q) / (float) BN + epi.eps);
+                for (int u = 0; u < 8; ++u) q += (v[u] - mean) * (v[u] - mean);
+                const float inv = 1.0f / sqrtf(row16_sum(q) / (float) BN + epi.eps);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                float r = (v[u] - mean) * inv;
-                if (epi.gamma != nullptr) r *= gv[u];
-                if (epi.beta != nullptr) r += sv[u];
-                if (epi.silu) r = r * __builtin_amdgcn_rcpf(1.0f + __expf(-r));
-                v[u] = r;
+                for (int u = 0; u < 8; ++u) {
+                    float r = (v[u] - mean) * inv;
+                    r = r * gv[u] + sv[u];
+                    if constexpr (SILU) r = r * __builtin_amdgcn_rcpf(1.0f + __expf(-r));
+                    v[u] = r;
+                }
+                o = pack_chunk<DT>(v);
+            } else if constexpr (MODE == kEpiAdd) {
+                float rv[8];
+                unpack_chunk<DT>(o, v);
+                unpack_chunk<DT>(res[p].v, rv);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] += rv[u];
+                o = pack_chunk<DT>(v);
             }
-            o = pack_chunk<DT>(v);
-        } else if (epi.mode == kEpiAdd) {
-            float rv[8];
-            unpack_chunk<DT>(o, v);
-            unpack_chunk<DT>(res[p].v, rv);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] += rv[u];
-            o = pack_chunk<DT>(v);
+            if (row < n) *(int4 *) (y + row * co + col0 + cc) = o;
         }
-        if (row < n) *(int4 *) (y + row * co + col0 + cc) = o;
+    };
+    using kNone = std::integral_constant<int, kEpiNone>;
+    using kNorm = std::integral_constant<int, kEpiNorm>;
+    using kAdd = std::integral_constant<int, kEpiAdd>;
+    if (epi.mode == kEpiNorm) {
+        if (epi.silu) {
+            passes(kNorm(), std::true_type());
+        } else {
+            passes(kNorm(), std::false_type());
+        }
+    } else if (epi.mode == kEpiAdd) {
+        passes(kAdd(), std::false_type());
+    } else {
+        passes(kNone(), std::false_type());
     }
 }
 

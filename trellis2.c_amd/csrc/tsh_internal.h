@@ -224,15 +224,14 @@ int linear_mfma_group(int co);
 bool linear_mfma_supported(int dtype, int ci, int co);
 hipError_t launch_linear_mfma(int dtype, const void * x, const void * w16, const float * bias, void * y, int64_t n,
                               int ci, int co, int silu, int cus, hipStream_t s);
-// Fused ConvNeXt MLP tail (kernels_block.hip): bf16/fp16, C = 64 or 128;
-// norm = 0 takes x as the already normalised LN output.
+// Fused ConvNeXt MLP tail (kernels_block.hip): bf16/fp16, C = 64 or 128.
 // w0 [C/8][4C][8] and w2 [4C/8][C][8] in the storage type with the grouped
 // column packing of the MFMA linear, groups g0 and g2 from convnext_mlp_groups.
 bool convnext_mlp_supported(int dtype, int c);
 void convnext_mlp_groups(int c, int * g0, int * g2);
 hipError_t launch_convnext_mlp(int dtype, const void * x, const float * gamma, const float * beta, const void * w0,
                                const float * b0, const void * w2, const float * b2, const void * res, void * y,
-                               int64_t n, int c, float eps, int norm, int cus, hipStream_t s);
+                               int64_t n, int c, float eps, int cus, hipStream_t s);
 // Spatial-to-channel downsample (kernels_s2c.hip).  flags: int32[8]; prep
 // (scratch part of s2c_prep_part_bytes()) sets flags[0] to 1 or 0 (a
 // negative coordinate) and flags[1..4] to the field maxima; heads sets
