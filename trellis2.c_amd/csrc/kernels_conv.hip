@@ -699,17 +699,45 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
         }
     }
 
-    for (int i = t; i < (TM + 1) * BN; i += NTHR) s_acc[i] = 0.0f;
+    // The centre offset pairs every row of the tile with exactly one row
+    // (itself, or the last duplicate of its coordinates), and the kernel map
+    // packs its list first in the tile's region, dst ascending.  So the
+    // first CU units are the centre's: their lists sit at known places, and
+    // together they write every row of the tile once, which is why their
+    // flushes store instead of adding and the tile sums need no clearing.
+    const int tile_rows = (int) ((n - row0) < TM ? (n - row0) : TM);
+    const int CU = (tile_rows + PASS - 1) / PASS;
+    const int64_t region = tile * TM * 27;
+    const int le = t & (PASS - 1);
+    const int32_t * list = t < PASS ? pair_src : pair_dst;
+    const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
+    // One round trip for the tile's counts and starts and the centre units'
+    // lists among the first 2 UPB units (the ring fill below).
+    int32_t cnt_v = 0, off_v = 0;
     if (t < 27) {
-        s_cnt[t] = tile_counts[tile * 27 + t];
-        s_start[t] = tile_off[tile * 27 + t];
+        cnt_v = tile_counts[tile * 27 + t];
+        off_v = tile_off[tile * 27 + t];
+    }
+    int32_t ring_v[2 * UPB];
+#pragma unroll
+    for (int j = 0; j < 2 * UPB; ++j) {
+        const int cj = tile_rows - j * PASS < PASS ? tile_rows - j * PASS : PASS;
+        ring_v[j] = (t < 2 * PASS && j < CU) ? list[region + j * PASS + (le < cj ? le : cj - 1)] : 0;
+    }
+    if (t < 27) {
+        s_cnt[t] = cnt_v;
+        s_start[t] = off_v;
     }
     lds_barrier();
-    // Unit table: offset k contributes ceil(count / PASS) units, in k order.
+    // Unit table: offset k contributes ceil(count / PASS) units, the centre
+    // offset's first, then the others in k order.
     if (t < 27) {
         int u = 0;
+        if (t != 13) {
+            u = (s_cnt[13] + PASS - 1) / PASS;
 #pragma unroll 1
-        for (int k = 0; k < t; ++k) u += (s_cnt[k] + PASS - 1) / PASS;
+            for (int k = 0; k < t; ++k) u += k == 13 ? 0 : (s_cnt[k] + PASS - 1) / PASS;
+        }
         const int c = s_cnt[t];
 #pragma unroll 1
         for (int p = 0; p < c; p += PASS, ++u) {
@@ -727,9 +755,6 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     // 0..127 carry src entries, 128..255 dst entries).  Padding entries
     // repeat the unit's last pair, so every gather stays in range; past the
     // last unit the last unit is loaded again (never used).
-    const int le = t & (PASS - 1);
-    const int32_t * list = t < PASS ? pair_src : pair_dst;
-    const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
     auto list_load = [&](int u) -> int32_t {
         if (t >= 2 * PASS) return 0;
         const int lu = u < U ? u : U - 1;
@@ -745,7 +770,7 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
         }
     };
 #pragma unroll
-    for (int j = 0; j < 2 * UPB; ++j) list_store(j, list_load(j));
+    for (int j = 0; j < 2 * UPB; ++j) list_store(j, j < CU ? ring_v[j] : list_load(j));
     int32_t lv[UPB];
 #pragma unroll
     for (int j = 0; j < UPB; ++j) lv[j] = list_load(2 * UPB + j);
@@ -801,6 +826,7 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     // into the spare row TM, reads batched ahead of the writes).
     auto flush = [&](int unit) {
         const int slot = unit & (RING - 1);
+        const bool first = unit < CU;  // a centre unit: its rows' first sums
         using Row = float __attribute__((ext_vector_type(NT)));
 #pragma unroll
         for (int q0 = 0; q0 < QB; q0 += QF) {
@@ -813,10 +839,17 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
 #pragma unroll
                 for (int i = 0; i < 4; ++i) dst[qq][i] = (Row *) (s_acc + rows[i] * BN + ch * WN + l16 * NT);
             }
+            if (first) {
 #pragma unroll
-            for (int qq = 0; qq < QF; ++qq)
+                for (int qq = 0; qq < QF; ++qq)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[qq][i] = *dst[qq][i];
+                    for (int i = 0; i < 4; ++i) v[qq][i] = (Row) 0.0f;
+            } else {
+#pragma unroll
+                for (int qq = 0; qq < QF; ++qq)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[qq][i] = *dst[qq][i];
+            }
 #pragma unroll
             for (int qq = 0; qq < QF; ++qq)
 #pragma unroll

@@ -199,7 +199,11 @@ __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict
 // Tile t owns the fixed region [t * 256 * 27, (t + 1) * 256 * 27) of the
 // pair arrays (the most pairs 256 rows can have), so no tile waits for the
 // counts of the tiles before it; the lists of a tile are packed from the
-// region's start, offsets in order.
+// region's start, the centre offset (k = 13) first, then the others in
+// order.  Every row has exactly one centre neighbour (itself, or the last
+// duplicate of its coordinates), so the centre list holds the tile's rows in
+// order, starting at the region's start: a consumer can find it without the
+// tile's counts.
 __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ coords, int64_t n,
                                                       const uint64_t * __restrict__ bkeys,
                                                       const int32_t * __restrict__ bidx, uint64_t hmask,
@@ -280,12 +284,14 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
     }
     __syncthreads();
     if (t < 64) {
-        // Tile counts per offset (lanes 0..26), their exclusive scan, the total.
+        // Tile counts per offset and their exclusive scan in packing order:
+        // lane 0 takes the centre offset, lanes 1..26 the others in order.
+        const int k = t == 0 ? 13 : (t <= 13 ? t - 1 : t);
         int32_t cnt = 0;
         if (t < 27) {
 #pragma unroll
-            for (int w = 0; w < kBlock / 64; ++w) cnt += s_wave_cnt[t][w];
-            tile_counts[tile * 27 + t] = cnt;
+            for (int w = 0; w < kBlock / 64; ++w) cnt += s_wave_cnt[k][w];
+            tile_counts[tile * 27 + k] = cnt;
         }
         int32_t incl = cnt;
 #pragma unroll
@@ -293,7 +299,7 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
             const int32_t o = __shfl_up(incl, d);
             if (lane >= d) incl += o;
         }
-        if (t < 27) s_koff[t] = incl - cnt;
+        if (t < 27) s_koff[k] = incl - cnt;
     }
     __syncthreads();
     const int64_t base = tile * kBlock * 27;
