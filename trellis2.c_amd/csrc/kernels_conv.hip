@@ -730,22 +730,27 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     }
     lds_barrier();
     // Unit table: offset k contributes ceil(count / PASS) units, the centre
-    // offset's first, then the others in k order.
-    if (t < 27) {
-        int u = 0;
-        if (t != 13) {
-            u = (s_cnt[13] + PASS - 1) / PASS;
-#pragma unroll 1
-            for (int k = 0; k < t; ++k) u += k == 13 ? 0 : (s_cnt[k] + PASS - 1) / PASS;
+    // offset's first, then the others in k order (the packing order): lane p
+    // of wavefront 0 takes the p-th offset of that order, and a scan of the
+    // unit counts gives each offset's first unit.
+    if (t < 64) {
+        const int k = t == 0 ? 13 : (t <= 13 ? t - 1 : t);
+        const int c = t < 27 ? s_cnt[k] : 0;
+        const int nu = (c + PASS - 1) / PASS;
+        int incl = nu;
+#pragma unroll
+        for (int d = 1; d < 32; d <<= 1) {
+            const int o = __shfl_up(incl, d);
+            if (lane >= d) incl += o;
         }
-        const int c = s_cnt[t];
+        int u = incl - nu;
 #pragma unroll 1
         for (int p = 0; p < c; p += PASS, ++u) {
-            s_uk[u] = t;
-            s_ustart[u] = s_start[t] + p;
+            s_uk[u] = k;
+            s_ustart[u] = s_start[k] + p;
             s_ucnt[u] = c - p < PASS ? c - p : PASS;
         }
-        if (t == 26) s_units = u;
+        if (t == 26) s_units = incl;
     }
     lds_barrier();
     const int U = s_units;
@@ -865,22 +870,19 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
         }
     };
 
-    // Block 0: A of steps 0 and 1 straight into LDS slots 0 and 1, steps 2 ..
-    // DEPTH-1 into ring slots 2 .. DEPTH-1; weights of steps 0 .. DEPTH-1.
-    // The fetches are issued in the order the main loop issues them (step r:
-    // A piece, then weights), so that the loop's memory waits, which must
-    // hold for its first pass as for the later ones, stay those of a full
-    // DEPTH-step look-ahead.
+    // Block 0: every fetch of its DEPTH steps issued first, in the order the
+    // main loop issues them (step r: A piece, then weights), so that the
+    // loop's memory waits, which must hold for its first pass as for the
+    // later ones, stay those of a full DEPTH-step look-ahead; then the A of
+    // steps 0 and 1 into LDS slots 0 and 1 (one round trip for the block).
     target(0, 0);
-    load_a(ra[0], 0);
-    store_a(0, ra[0]);
-    load_a(ra[1], 1);
-    store_a(1, ra[1]);
 #pragma unroll
     for (int r = 0; r < DEPTH; ++r) {
-        if (r >= 2) load_a(ra[r], r);
+        load_a(ra[r], r);
         load_b(rb[r], r);
     }
+    store_a(0, ra[0]);
+    store_a(1, ra[1]);
     lds_barrier();
     read_a(af[0], 0);
 
