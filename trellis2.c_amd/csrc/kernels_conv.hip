@@ -348,37 +348,67 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     const int ci8 = ci >> 3;
     const int KS = ci / BK;
 
-    for (int i = t; i < (TM + 1) * BN; i += NTHR) s_acc[i] = 0.0f;
+    // The centre offset pairs every row of the tile with exactly one row
+    // (itself, or the last duplicate of its coordinates), and the kernel map
+    // packs its list first in the tile's region, dst ascending.  So the
+    // first CU units are the centre's: their lists sit at known places, and
+    // together they write every row of the tile once, which is why their
+    // flushes store instead of adding and the tile sums need no clearing.
+    const int tile_rows = (int) ((n - row0) < TM ? (n - row0) : TM);
+    const int CU = (tile_rows + PASS - 1) / PASS;
+    const int64_t region = tile * TM * 27;
+    const int le = t & (PASS - 1);
+    const int32_t * list = t < PASS ? pair_src : pair_dst;
+    const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
+    // One round trip for the tile's counts and starts and the centre units'
+    // lists among the first 2 UPB units (the ring fill below).
+    int32_t cnt_v = 0, off_v = 0;
     if (t < 27) {
-        s_cnt[t] = tile_counts[tile * 27 + t];
-        s_start[t] = tile_off[tile * 27 + t];
+        cnt_v = tile_counts[tile * 27 + t];
+        off_v = tile_off[tile * 27 + t];
+    }
+    int32_t ring_v[2 * UPB];
+#pragma unroll
+    for (int j = 0; j < 2 * UPB; ++j) {
+        const int cj = tile_rows - j * PASS < PASS ? tile_rows - j * PASS : PASS;
+        ring_v[j] = (t < 2 * PASS && j < CU) ? list[region + j * PASS + (le < cj ? le : cj - 1)] : 0;
+    }
+    if (t < 27) {
+        s_cnt[t] = cnt_v;
+        s_start[t] = off_v;
     }
     lds_barrier();
-    // Unit table: offset k contributes ceil(count / PASS) units, in k order.
-    if (t < 27) {
-        int u = 0;
-#pragma unroll 1
-        for (int k = 0; k < t; ++k) u += (s_cnt[k] + PASS - 1) / PASS;
-        const int c = s_cnt[t];
+    // Unit table: offset k contributes ceil(count / PASS) units, the centre
+    // offset's first, then the others in k order (the packing order): lane p
+    // of wavefront 0 takes the p-th offset of that order, and a scan of the
+    // unit counts gives each offset's first unit.
+    if (t < 64) {
+        const int k = t == 0 ? 13 : (t <= 13 ? t - 1 : t);
+        const int c = t < 27 ? s_cnt[k] : 0;
+        const int nu = (c + PASS - 1) / PASS;
+        int incl = nu;
+#pragma unroll
+        for (int d = 1; d < 32; d <<= 1) {
+            const int o = __shfl_up(incl, d);
+            if (lane >= d) incl += o;
+        }
+        int u = incl - nu;
 #pragma unroll 1
         for (int p = 0; p < c; p += PASS, ++u) {
-            s_uk[u] = t;
-            s_ustart[u] = s_start[t] + p;
+            s_uk[u] = k;
+            s_ustart[u] = s_start[k] + p;
             s_ucnt[u] = c - p < PASS ? c - p : PASS;
         }
-        if (t == 26) s_units = u;
+        if (t == 26) s_units = incl;
     }
     lds_barrier();
     const int U = s_units;
     if (U == 0) return;  // unreachable for a tile with rows: the centre offset pairs every row with itself
 
-    // Unit lists, staged two blocks ahead in a ring of RING slots: threads
-    // 0..127 carry src entries, 128..255 dst entries.  Padding entries
+    // Unit lists, staged two blocks ahead in a ring of RING slots (threads
+    // 0..127 carry src entries, 128..255 dst entries).  Padding entries
     // repeat the unit's last pair, so every gather stays in range; past the
     // last unit the last unit is loaded again (never used).
-    const int le = t & (PASS - 1);
-    const int32_t * list = t < PASS ? pair_src : pair_dst;
-    const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
     auto list_load = [&](int u) -> int32_t {
         if (t >= 2 * PASS) return 0;
         const int lu = u < U ? u : U - 1;
@@ -394,7 +424,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
         }
     };
 #pragma unroll
-    for (int j = 0; j < 2 * UPB; ++j) list_store(j, list_load(j));
+    for (int j = 0; j < 2 * UPB; ++j) list_store(j, j < CU ? ring_v[j] : list_load(j));
     int32_t lv[UPB];
 #pragma unroll
     for (int j = 0; j < UPB; ++j) lv[j] = list_load(2 * UPB + j);
@@ -472,6 +502,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     // equal row).
     auto flush = [&](int unit) {
         const int slot = unit & (RING - 1);
+        const bool first = unit < CU;  // a centre unit: its rows' first sums
         using Row = float __attribute__((ext_vector_type(NT)));
 #pragma unroll
         for (int q0 = 0; q0 < QB; q0 += QF) {
@@ -484,10 +515,17 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
 #pragma unroll
                 for (int i = 0; i < 4; ++i) dst[qq][i] = (Row *) (s_acc + rows[i] * BN + ch * WN + l16 * NT);
             }
+            if (first) {
 #pragma unroll
-            for (int qq = 0; qq < QF; ++qq)
+                for (int qq = 0; qq < QF; ++qq)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[qq][i] = *dst[qq][i];
+                    for (int i = 0; i < 4; ++i) v[qq][i] = (Row) 0.0f;
+            } else {
+#pragma unroll
+                for (int qq = 0; qq < QF; ++qq)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[qq][i] = *dst[qq][i];
+            }
 #pragma unroll
             for (int qq = 0; qq < QF; ++qq)
 #pragma unroll
@@ -503,17 +541,19 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
         }
     };
 
-    // Block 0: weights of steps 0 and 1 straight into LDS slots 0 and 1,
-    // steps 2 .. DEPTH-1 into ring slots 2 .. DEPTH-1; A of steps 0 .. DEPTH-1.
+    // Block 0: every fetch of its DEPTH steps issued first, in the order the
+    // main loop issues them (step r: weights, then A), so that the loop's
+    // memory waits, which must hold for its first pass as for the later
+    // ones, stay those of a full DEPTH-step look-ahead; then the weights of
+    // steps 0 and 1 into LDS slots 0 and 1 (one round trip for the block).
     target(0, 0);
-    load_b(rw[0], 0);
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) {
+        load_b(rw[r], r);
+        load_a(ra[r], r);
+    }
     store_b(0, rw[0]);
-    load_b(rw[1], 1);
     store_b(1, rw[1]);
-#pragma unroll
-    for (int r = 2; r < DEPTH; ++r) load_b(rw[r], r);
-#pragma unroll
-    for (int r = 0; r < DEPTH; ++r) load_a(ra[r], r);
     lds_barrier();
     {
         const T * bs = &s_b[0][(lg * BN + ch * WN + l16) * 8];
