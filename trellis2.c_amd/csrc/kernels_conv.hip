@@ -243,7 +243,9 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
 // A block owns one 256-row map tile x BN output channels; the fp32 sums of
 // those rows live in LDS.  The kernel map's tile-major pair lists give, for
 // each offset k, the tile's valid (src, dst) pairs in destination order.  The
-// block walks "units" (offset k, up to 128 of its pairs) in k order; each unit
+// block walks "units" (offset k, up to 128 of its pairs): the centre offset's
+// first, whose flushes store (every row of the tile has one centre pair, so
+// the sums need no clearing), then the others in k order; each unit
 // is Ci/32 K steps of MFMA work over 16-pair row blocks, so the MFMA row
 // dimension runs over valid pairs only.  NW wavefronts (8: two per SIMD, so
 // one's VALU and LDS work overlaps the other's MFMAs) are split into RG row
