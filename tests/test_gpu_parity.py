@@ -110,6 +110,31 @@ def test_rulebook_rejects_bad_arguments(be32):
     assert e.value.status == sh.INVALID_ARGUMENT
 
 
+@pytest.mark.parametrize("name", ["duplicates", "wrap", "single", "ragged", "batches"])
+@pytest.mark.parametrize("ci,co", [(128, 128), (256, 128), (64, 64)])
+def test_compact_conv_edge_cases_vs_oracle(be_sched, name, ci, co):
+    """The compacted conv on the map's edge cases.  Each tile starts with the
+    centre offset's pairs, which with duplicate coordinates point at the last
+    duplicate rather than the row itself; wrapped coordinates, a one-voxel
+    input, a ragged last tile and several batches exercise the tile
+    bookkeeping of both compacted kernels (128-channel and 64-channel blocks).
+    Against the oracle's conv on the same rounded inputs, to the storage
+    tolerance."""
+    be = be_sched[("compact", sh.BF16)]
+    c = edge_coord_sets()[name]
+    n = c.shape[0]
+    say(f"compact conv edge case {name}: n={n} ci={ci} co={co}")
+    rng = np.random.default_rng(ci + co + n)
+    x = sh.storage_round(rng.standard_normal((n, ci)), sh.BF16)
+    w = sh.storage_round(rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci), sh.BF16)
+    bias = (0.1 * rng.standard_normal(co)).astype(np.float32)
+    got = run_conv(be, c, x, w, bias, ci, co)
+    exp = orc.Rulebook(c).conv(x, w, bias, ci, co)
+    err = max_rel_err(got, sh.storage_round(exp, sh.BF16))
+    say(f"compact conv edge case {name} ci={ci} co={co} max_rel_err={err:.3e}")
+    assert err <= 2e-2
+
+
 def test_reject_duplicates_policy():
     b = sh.Backend(0, sh.F32, reject_duplicates=True)
     c = np.array([[0, 1, 1, 1], [0, 2, 2, 2], [0, 1, 1, 1]], np.int32)
