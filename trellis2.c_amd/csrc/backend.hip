@@ -17,6 +17,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <thread>
 
 #include "tsh_internal.h"
 
@@ -74,6 +75,10 @@ struct Backend {
     std::vector<DevMem> transient;  // uncached weights of the current call
     // Device C2S maps (valid until destroy).
     std::vector<trellis_sparse_c2s_device_map *> maps;
+    // Pinned host staging for downloads into caller-owned pageable arrays
+    // (grown on demand; released by trim(FREE_BUFFERS) and destroy).
+    void * pinned = nullptr;
+    size_t pinned_bytes = 0;
     // Timing.
     bool profiling = false;
     std::vector<StageMark> pending;
@@ -162,6 +167,45 @@ void dev_release(Backend * be, DevMem * m) {
 }
 
 void select_device(Backend * be) { (void) hipSetDevice(be->device); }
+
+// memcpy split over up to 8 host threads (at least 2 MiB each): copying into
+// freshly allocated pageable memory is bound by first-touch page faults,
+// which threads take in parallel.
+void parallel_copy(void * dst, const void * src, size_t bytes) {
+    constexpr size_t kMinChunk = (size_t) 2 << 20;
+    const size_t parts = std::min<size_t>(8, std::max<size_t>(1, bytes / kMinChunk));
+    if (parts <= 1) {
+        memcpy(dst, src, bytes);
+        return;
+    }
+    const size_t chunk = (bytes + parts - 1) / parts;
+    std::vector<std::thread> pool;
+    for (size_t i = 1; i < parts; ++i) {
+        const size_t off = i * chunk, len = std::min(chunk, bytes - off);
+        pool.emplace_back([=] { memcpy((char *) dst + off, (const char *) src + off, len); });
+    }
+    memcpy(dst, src, chunk);
+    for (auto & th : pool) th.join();
+}
+
+// Pinned staging of at least `bytes` (the stream has no transfer pending on
+// the old buffer when this is called: every user synchronizes before
+// returning).
+trellis_status pinned_reserve(Backend * be, size_t bytes) {
+    if (bytes <= be->pinned_bytes) return TRELLIS_STATUS_OK;
+    if (be->pinned != nullptr) (void) hipHostFree(be->pinned);
+    be->pinned = nullptr;
+    be->pinned_bytes = 0;
+    const size_t want = std::max<size_t>(bytes, (size_t) 1 << 20);
+    void * p = nullptr;
+    if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) {
+        (void) hipGetLastError();
+        return fail(be, TRELLIS_STATUS_OUT_OF_MEMORY, "pinned staging buffer");
+    }
+    be->pinned = p;
+    be->pinned_bytes = want;
+    return TRELLIS_STATUS_OK;
+}
 
 // ---- stage timing -----------------------------------------------------------
 hipEvent_t take_event(Backend * be) {
@@ -1518,12 +1562,24 @@ trellis_status fdg_mesh_impl(trellis_sparse_backend * backend, const int32_t * c
         if (hv == nullptr || (quads > 0 && hfaces == nullptr)) {
             st = TRELLIS_STATUS_OUT_OF_MEMORY;
         } else {
-            hipError_t err = hipMemcpyAsync(hv, vert.ptr, (size_t) n * 12, hipMemcpyDeviceToHost, s);
-            if (err == hipSuccess && quads > 0) {
-                err = hipMemcpyAsync(hfaces, faces.ptr, (size_t) quads * 24, hipMemcpyDeviceToHost, s);
+            // Both arrays through the pinned staging buffer (full-rate
+            // transfers), then copied into the caller's malloc-owned arrays.
+            const size_t vbytes = (size_t) n * 12, voff = (vbytes + 255) / 256 * 256;
+            const size_t fbytes = (size_t) quads * 24;
+            st = pinned_reserve(be, voff + fbytes);
+            if (st == TRELLIS_STATUS_OK) {
+                char * stage = (char *) be->pinned;
+                hipError_t err = hipMemcpyAsync(stage, vert.ptr, vbytes, hipMemcpyDeviceToHost, s);
+                if (err == hipSuccess && quads > 0) {
+                    err = hipMemcpyAsync(stage + voff, faces.ptr, fbytes, hipMemcpyDeviceToHost, s);
+                }
+                if (err == hipSuccess) err = hipStreamSynchronize(s);
+                st = hip_status(be, err, "flex_dual_grid_mesh download");
+                if (st == TRELLIS_STATUS_OK) {
+                    parallel_copy(hv, stage, vbytes);
+                    if (quads > 0) parallel_copy(hfaces, stage + voff, fbytes);
+                }
             }
-            if (err == hipSuccess) err = hipStreamSynchronize(s);
-            st = hip_status(be, err, "flex_dual_grid_mesh download");
         }
     }
     for (DevMem * d : {&cd, &flags, &vert, &wgt, &counts, &first, &total, &tmp, &faces}) dev_release(be, d);
@@ -1567,6 +1623,12 @@ trellis_status op_trim(trellis_sparse_backend * backend, unsigned flags, size_t 
             }
         }
         be->free_blocks.clear();
+        if (be->pinned != nullptr) {
+            (void) hipHostFree(be->pinned);
+            released += be->pinned_bytes;
+            be->pinned = nullptr;
+            be->pinned_bytes = 0;
+        }
         be->pooled_bytes = 0;
     }
     if (released_bytes != nullptr) *released_bytes = released;
@@ -1629,6 +1691,7 @@ void op_destroy(trellis_sparse_backend * backend) {
     for (hipEvent_t e : be->spare_events) (void) hipEventDestroy(e);
     for (hipEvent_t e : be->user_events)
         if (e != nullptr) (void) hipEventDestroy(e);
+    if (be->pinned != nullptr) (void) hipHostFree(be->pinned);
     if (be->side != nullptr) (void) hipStreamDestroy(be->side);
     (void) hipStreamDestroy(be->stream);
     delete be;
