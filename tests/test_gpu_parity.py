@@ -258,8 +258,9 @@ def test_conv_mfma_ragged_rows(be_sched, algo, n):
                                      (64, 16, 1), (64, 32, 129)])
 def test_conv_narrow_output_vs_oracle(be_sched, algo, dtype, ci, co, n):
     """16 and 32 output channels (the encoder's S2C conv to co/8 channels):
-    the masked MFMA schedule with all four wavefronts on rows (the compacted
-    one needs 64-channel multiples and hands these over); ragged row counts."""
+    the compacted schedule with one 16/32-channel block (Ci = 64 or a
+    multiple of 128; Ci = 32 falls back to the masked one) and the masked one
+    with all four wavefronts on rows; ragged row counts and a single row."""
     be = be_sched[(algo, dtype)]
     c = wl.make_coords(1)[:n]
     rng = np.random.default_rng(ci * 3 + co + n + dtype)

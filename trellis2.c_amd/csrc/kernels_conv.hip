@@ -20,13 +20,14 @@
 //               and read pre-packed weight fragments; row groups of 16 with no
 //               valid neighbour skip the offset, others multiply zeros for
 //               their missing neighbours.
-//  * compact  - bf16/fp16 storage, Ci = 64 or Ci % 128 == 0, Co % 64 == 0.  The same MFMA
+//  * compact  - bf16/fp16 storage, Ci = 64 or Ci % 128 == 0, Co % 64 == 0 or
+//               Co = 16 / 32 (one 16/32-channel block).  The same MFMA
 //               tiles driven by the kernel map's compacted per-tile pair
 //               lists, so the MFMA rows are valid (src, dst) pairs only; sums
 //               of a 256-row tile stay in LDS until one final store.  Blocks
 //               of 128 output channels run k_conv_mfma_wreg (weights in
-//               registers, feature rows shared through LDS), blocks of 64
-//               k_conv_mfma_stream (weights shared through LDS).
+//               registers, feature rows shared through LDS), blocks of 64,
+//               32 or 16 k_conv_mfma_stream (weights shared through LDS).
 #include <type_traits>
 
 #include "tsh_internal.h"
@@ -1125,15 +1126,18 @@ hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nb
 
 int conv_stream_group(int co) {
     // 128-channel blocks run k_conv_mfma_wreg (2 row groups x 4 channel
-    // groups of 32), 64-channel blocks k_conv_mfma_stream.
+    // groups of 32), 64-channel blocks k_conv_mfma_stream; 16- and
+    // 32-channel outputs are one block of co channels there.
     if (co % 128 == 0) return 128 / 4 / 16;
+    if (co == 16 || co == 32) return co / (TSH_STREAM_WAVES / TSH_STREAM_ROW_GROUPS) / 16;
     return 64 / (TSH_STREAM_WAVES / TSH_STREAM_ROW_GROUPS) / 16;
 }
 
 bool conv_stream_supported(int dtype, int ci, int co) {
     // A unit (Ci/32 K steps) spans a whole number of 4-step blocks, or two
     // units (Ci = 64) make one block.
-    return conv_mfma_supported(dtype, ci, co) && co % 64 == 0 && (ci % 128 == 0 || ci == 64);
+    return conv_mfma_supported(dtype, ci, co) && (co % 64 == 0 || co == 16 || co == 32) &&
+           (ci % 128 == 0 || ci == 64);
 }
 
 namespace {
@@ -1182,6 +1186,8 @@ hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int3
                                                                            tile_counts, w16, bias, y, n, ci, co, s, \
                                                                            epi)
     if (wide) return pair ? TSH_STREAM(128, 2) : TSH_STREAM(128, 1);
+    if (co == 16) return pair ? TSH_STREAM(16, 2) : TSH_STREAM(16, 1);
+    if (co == 32) return pair ? TSH_STREAM(32, 2) : TSH_STREAM(32, 1);
     return pair ? TSH_STREAM(64, 2) : TSH_STREAM(64, 1);
 #undef TSH_STREAM
 }
