@@ -552,9 +552,9 @@ def main():
     for _ in range(args.warmup):
         job.step()
     be.synchronize()
-    be.profile(True)
-    be.profile_read(reset=True)
-    be.synchronize()
+    # Timed steps: the production path, without stage events (rulebooks built
+    # from device maps run on the backend's second stream, overlapping the
+    # broadcast).
     t0 = time.perf_counter()
     be.event(0)
     for _ in range(args.steps):
@@ -563,6 +563,14 @@ def main():
     be.synchronize()
     wall = (time.perf_counter() - t0) * 1e3
     dev_ms = be.elapsed(0, 1)
+    # Stage breakdown and the conv's launch time (the roofline's denominator):
+    # a second pass of as many steps with stage events, which keep every
+    # stage on the backend stream.
+    be.profile(True)
+    be.profile_read(reset=True)
+    for _ in range(args.steps):
+        job.step()
+    be.synchronize()
     stages = be.profile_read(reset=True)
     be.profile(False)
     ms_per_step = max(dev_ms, wall) / args.steps
@@ -624,7 +632,9 @@ def main():
             "schedule": algo_name,
             "avg_launch_ms": round(conv_avg, 4),
         },
-        "timing": {"device_event_ms": round(dev_ms, 3), "wall_ms": round(wall, 3)},
+        "timing": {"device_event_ms": round(dev_ms, 3), "wall_ms": round(wall, 3),
+                   "stages": "stage_ms_per_step and the conv launch time come from a second pass of as many steps "
+                             "with stage events (every stage on the backend stream)"},
     }
     if not args.no_cpu_baseline:
         log("bench: timing the CPU oracle baseline")
