@@ -228,6 +228,18 @@ const char * trellis_sparse_hip_last_error(const trellis_sparse_backend * backen
 /* Waits for all work queued by this backend. */
 trellis_status trellis_sparse_hip_synchronize(trellis_sparse_backend * backend);
 
+/* Forced allocation failure, for tests of the out-of-memory paths (no
+ * counterpart in the reference, whose Vulkan backend only reacts to real
+ * failures by trimming and retrying, trellis_sparse_vulkan.c:533-561).
+ * From this call on, device allocation attempts number after .. after +
+ * count - 1 (counted from 0) fail as if the device were full; after < 0
+ * switches the hook off.  Every slot then returns
+ * TRELLIS_STATUS_OUT_OF_MEMORY with its outputs NULL / 0, and an allocation
+ * that fails while the backend's pool holds free blocks releases the pool and
+ * tries once more.  The environment variable TRELLIS_HIP_FAIL_ALLOC_AFTER=N[,K]
+ * sets the same hook at creation (K defaults to all later attempts). */
+trellis_status trellis_sparse_hip_fail_alloc(trellis_sparse_backend * backend, int64_t after, int64_t count);
+
 /* ------------------------------------------------------------------------ */
 /* Inspection (no counterpart in the reference vtable; used by parity tests */
 /* and the benchmark).  All downloads are synchronous.                       */

@@ -1,0 +1,195 @@
+"""GPU parity of the convs at the benchmark configurations' own sizes, and of
+the deep-channel schedules (a 128-pair unit spanning several blocks of K
+steps).
+
+At full size the oracle (trellis_sparse_cpu.c:324-373 restated) runs on a
+strided sample of output rows, from the same rounded inputs the backend
+reads; the sampled rows are compared to the storage tolerance of
+tests/test_sparse_decoder_backend.c:16-24 (|a-b| <= 2e-2 max(1,|a|,|b|)).
+
+  config 2  conv(128->128) -> LayerNorm -> SiLU -> conv(128->128) + skip, fp16,
+            419,340 voxels: each fused launch against the oracle, the second
+            from the backend's own intermediate rows
+  config 4  conv 64->64 bf16 on the 3,788,747-voxel R=1024 shell set
+  config 5  conv 512->512 bf16 on the four batched structures (327,680 voxels)
+
+The deep-channel cases run Ci = 384, 512 and 1024 with 64- and 128-channel
+output blocks on ragged row counts: with Ci >= 512 (or Ci = 384) one unit of
+128 pairs takes more than one block of 8 (or 4) K steps, so the kernels'
+mid-unit block prefetch is executed.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+import sparse_hip as sh
+import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+TOL = {sh.F16: 2e-2, sh.BF16: 2e-2}
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def max_rel_err(got, exp):
+    got = np.asarray(got, dtype=np.float64).ravel()
+    exp = np.asarray(exp, dtype=np.float64).ravel()
+    assert got.shape == exp.shape
+    scale = np.maximum(1.0, np.maximum(np.abs(got), np.abs(exp)))
+    return float(np.max(np.abs(got - exp) / scale)) if got.size else 0.0
+
+
+@pytest.fixture(scope="module")
+def backends():
+    bes = {dt: sh.Backend(0, dt) for dt in (sh.F16, sh.BF16)}
+    yield bes
+    for b in bes.values():
+        b.destroy()
+
+
+def sample_rows(n, want):
+    step = max(1, n // want)
+    return (min(3, n - 1), n, step)
+
+
+@pytest.mark.parametrize("cfg", [4, 5])
+def test_config_conv_full_size_vs_oracle_sample(backends, cfg):
+    be = backends[sh.BF16]
+    w = wl.workload(cfg)
+    coords, ci, co = w["coords"], w["ci"], w["co"]
+    n = coords.shape[0]
+    x = sh.bf16_round(w["feats"])
+    wr = sh.bf16_round(w["weight"])
+    rng = np.random.default_rng(cfg)
+    bias = (0.1 * rng.standard_normal(co)).astype(np.float32)
+    say(f"cfg{cfg} full conv {ci}->{co} bf16 n={n}")
+    rb = be.build_rulebook(coords)
+    stats = be.rulebook_stats(rb)
+    xb, yb = be.upload(x), be.alloc(n * co)
+    be.conv(rb, xb, w["weight"], bias, yb, ci, co)
+    got = be.download(yb).reshape(n, co)
+    del xb, yb
+    assert np.all(np.isfinite(got))
+    rows = sample_rows(n, 5000 if ci * co <= 8192 else 900)
+    orb = orc.Rulebook(coords)
+    exp = orb.conv(x, wr, bias, ci, co, rows=rows)
+    err = max_rel_err(got[rows[0]:rows[1]:rows[2]], exp)
+    say(f"cfg{cfg} full conv pairs={stats['pairs']} sampled rows={exp.shape[0]} max_rel_err={err:.3e}")
+    assert err <= 2e-2
+    rb.free()
+
+
+def test_config2_fused_block_full_size_vs_oracle_sample(backends):
+    """Config 2 at full size: conv_norm (SiLU) and conv_add, each checked on a
+    row sample against the oracle's conv -> round -> row_norm_silu -> round
+    and conv -> round -> add -> round, the second from the backend's own
+    intermediate (already in the storage type)."""
+    dtype = sh.F16
+    be = backends[dtype]
+    rnd = lambda a: sh.storage_round(a, dtype)
+    w = wl.workload(2)
+    coords, c = w["coords"], 128
+    n = coords.shape[0]
+    x = rnd(w["feats"])
+    w1, w2 = rnd(w["weight"]), rnd(w["weight2"])
+    rng = np.random.default_rng(22)
+    b1 = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    b2 = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    say(f"cfg2 fused block fp16 n={n}")
+    rb = be.build_rulebook(coords)
+    xb, hb, ob = be.upload(x), be.alloc(n * c), be.alloc(n * c)
+    be.conv_norm(rb, xb, w1, b1, gamma, beta, 1e-6, hb, c, c, silu=True)
+    be.conv_add(rb, hb, w2, b2, xb, ob, c, c)
+    h = be.download(hb).reshape(n, c)
+    out = be.download(ob).reshape(n, c)
+    rows = sample_rows(n, 4000)
+    sl = slice(rows[0], rows[1], rows[2])
+    orb = orc.Rulebook(coords)
+    e_conv1 = rnd(orb.conv(x, w1, b1, c, c, rows=rows))
+    e_h = rnd(orc.row_norm(e_conv1, gamma, beta, e_conv1.shape[0], c, 1e-6, silu=True))
+    err_h = max_rel_err(h[sl], e_h)
+    e_out = rnd(orc.add(rnd(orb.conv(h, w2, b2, c, c, rows=rows)), x[sl]))
+    err_o = max_rel_err(out[sl], e_out)
+    say(f"cfg2 fused block sampled rows={e_h.shape[0]} err_conv_norm={err_h:.3e} err_conv_add={err_o:.3e}")
+    assert err_h <= TOL[dtype]
+    assert err_o <= TOL[dtype]
+    rb.free()
+
+
+DEEP_CASES = [(512, 128, 3001), (384, 128, 2000), (1024, 128, 1200), (512, 64, 2500), (1024, 64, 1777),
+              (512, 512, 1300)]
+
+
+@pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])
+@pytest.mark.parametrize("ci,co,n", DEEP_CASES)
+def test_conv_deep_channels_vs_oracle(backends, dtype, ci, co, n):
+    be = backends[dtype]
+    coords = np.ascontiguousarray(wl.make_coords(1)[:n])
+    rng = np.random.default_rng(ci + 3 * co + n + dtype)
+    x = sh.storage_round(rng.standard_normal((n, ci)), dtype)
+    w = sh.storage_round(rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci), dtype)
+    bias = (0.1 * rng.standard_normal(co)).astype(np.float32)
+    say(f"deep conv dtype={dtype} ci={ci} co={co} n={n}")
+    rb = be.build_rulebook(coords)
+    xb, yb = be.upload(x), be.alloc(n * co)
+    be.conv(rb, xb, w, bias, yb, ci, co)
+    got = be.download(yb).reshape(n, co)
+    rows = sample_rows(n, 400)
+    exp = orc.Rulebook(coords).conv(x, w, bias, ci, co, rows=rows)
+    err = max_rel_err(got[rows[0]:rows[1]:rows[2]], exp)
+    say(f"deep conv dtype={dtype} ci={ci} co={co} n={n} rows={exp.shape[0]} max_rel_err={err:.3e}")
+    assert err <= TOL[dtype]
+    # Fused epilogues on the multi-block path (128-channel blocks only).
+    if co % 128 == 0:
+        res = sh.storage_round(rng.standard_normal((n, co)), dtype)
+        rs = be.upload(res)
+        be.conv_add(rb, xb, w, bias, rs, yb, ci, co)
+        got_add = be.download(yb).reshape(n, co)
+        e_add = sh.storage_round(orc.add(sh.storage_round(exp, dtype), res[rows[0]:rows[1]:rows[2]]), dtype)
+        err_add = max_rel_err(got_add[rows[0]:rows[1]:rows[2]], e_add)
+        say(f"deep conv_add dtype={dtype} ci={ci} co={co} max_rel_err={err_add:.3e}")
+        assert err_add <= TOL[dtype]
+    if co == 128:
+        gamma = (1 + 0.1 * rng.standard_normal(co)).astype(np.float32)
+        beta = (0.1 * rng.standard_normal(co)).astype(np.float32)
+        be.conv_norm(rb, xb, w, bias, gamma, beta, 1e-6, yb, ci, co, silu=True)
+        got_n = be.download(yb).reshape(n, co)
+        e_n = sh.storage_round(orc.row_norm(sh.storage_round(exp, dtype), gamma, beta, exp.shape[0], co, 1e-6,
+                                            silu=True), dtype)
+        err_n = max_rel_err(got_n[rows[0]:rows[1]:rows[2]], e_n)
+        say(f"deep conv_norm dtype={dtype} ci={ci} max_rel_err={err_n:.3e}")
+        assert err_n <= TOL[dtype]
+    rb.free()
+
+
+@pytest.mark.parametrize("ci,co,n", [(512, 128, 2100), (384, 64, 1500)])
+def test_conv_deep_channels_masked_vs_oracle(ci, co, n):
+    """The masked schedule on the same deep shapes (it walks K in 32-channel
+    steps per offset; no unit blocks)."""
+    be = sh.Backend(0, sh.BF16, conv_algo=sh.CONV_MASKED)
+    try:
+        coords = np.ascontiguousarray(wl.make_coords(1)[:n])
+        rng = np.random.default_rng(ci * 5 + co + n)
+        x = sh.bf16_round(rng.standard_normal((n, ci)))
+        w = sh.bf16_round(rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci))
+        rb = be.build_rulebook(coords)
+        xb, yb = be.upload(x), be.alloc(n * co)
+        be.conv(rb, xb, w, None, yb, ci, co)
+        got = be.download(yb).reshape(n, co)
+        rows = sample_rows(n, 300)
+        exp = orc.Rulebook(coords).conv(x, w, None, ci, co, rows=rows)
+        err = max_rel_err(got[rows[0]:rows[1]:rows[2]], exp)
+        say(f"deep masked ci={ci} co={co} n={n} max_rel_err={err:.3e}")
+        assert err <= 2e-2
+        rb.free()
+    finally:
+        be.destroy()

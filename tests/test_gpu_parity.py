@@ -353,6 +353,96 @@ def test_c2s_known_answer_host_and_device(be32):
     assert np.array_equal(c3, e2c) and np.array_equal(p3, e2p) and np.array_equal(s3, e2s)
 
 
+@pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
+def test_c2s_exact_on_fp32_logits_with_16bit_storage(be16, bebf, dtype):
+    """The voxel set of a 16-bit backend equals the reference's on the same
+    fp32 logits (executor.c:119-150: child s exists iff logit > 0), also for
+    positives too small for the storage type (fp16 keeps nothing below
+    ~3e-8, so round-to-nearest would give +0 and drop the child), +-0.0 and
+    tiny negatives.  Both producers of logits are covered: upload_f32 of
+    host fp32 values, and the linear slot (the decoder's to_subdiv Ci -> 8),
+    here with zero weights so that every row's logits are the bias exactly."""
+    be = backend_for(dtype, None, be16, bebf)
+    rng = np.random.default_rng(17 + dtype)
+    n = 2500
+    coords = np.unique(np.stack([rng.integers(0, 2, n), rng.integers(0, 40, n), rng.integers(0, 40, n),
+                                 rng.integers(0, 40, n)], 1), axis=0).astype(np.int32)
+    n = coords.shape[0]
+    special = np.array([1e-7, 6e-8, 3e-8, 2.9e-8, 1e-9, 1e-12, 1e-30, 1.5e-38, -0.0, 0.0, -1e-30, -1e-9, -3e-8,
+                        1.0, -1.0, 7e4, -7e4], np.float32)
+    logits = np.where(rng.random((n, 8)) < 0.7, special[rng.integers(0, special.size, (n, 8))],
+                      rng.standard_normal((n, 8))).astype(np.float32)
+    rc, ec, ep, es = orc.c2s_map(coords, logits)
+    assert rc == 0
+    lg = be.upload(logits)
+    dm = be.build_c2s_map_device(lg, n, coords=coords)
+    c2, p2, s2 = be.download_c2s_map(dm)
+    say(f"c2s fp32 logits dtype={dtype}: {ec.shape[0]} children of {n} parents, got {dm.n}")
+    assert np.array_equal(c2, ec) and np.array_equal(p2, ep) and np.array_equal(s2, es)
+    hc, hp, hs = be.build_c2s_map(coords, lg)
+    assert np.array_equal(hc, ec) and np.array_equal(hp, ep) and np.array_equal(hs, es)
+    # Through the linear slot.
+    ci = 64
+    h = be.upload(sh.storage_round(rng.standard_normal((n, ci)), dtype))
+    w = np.zeros((8, ci), np.float32)
+    bias = np.array([1e-9, -1e-9, 0.0, -0.0, 2e-8, 1e-30, 1.0, -1.0], np.float32)
+    sub = be.alloc(n * 8)
+    be.linear(h, w, bias, sub, n, ci, 8)
+    rc, ec2, ep2, es2 = orc.c2s_map(coords, np.tile(bias, (n, 1)))
+    dm2 = be.build_c2s_map_device(sub, n, coords=coords)
+    c3, p3, s3 = be.download_c2s_map(dm2)
+    assert dm2.n == 4 * n
+    assert np.array_equal(c3, ec2) and np.array_equal(p3, ep2) and np.array_equal(s3, es2)
+
+
+@pytest.mark.parametrize("dtype", [sh.F32, sh.BF16])
+def test_device_map_survives_trim(be32, be16, bebf, dtype):
+    """Device C2S maps and guides stay valid across trim (the vtable contract,
+    trellis_sparse_backend.h:183-188; the texture decode reuses the shape
+    decode's guides, executor.c:304-320): build a map, its rulebook, and the
+    gather / broadcast / conv results over it; trim FREE_BUFFERS | WEIGHTS;
+    then the map downloads unchanged and the same calls on the same map (and a
+    rulebook rebuilt from it) give bit-identical results."""
+    be = backend_for(dtype, be32, be16, bebf)
+    w = wl.workload(3)
+    pc, logits = w["parent_coords"][:40000], w["logits"][:40000]
+    npar = pc.shape[0]
+    rng = np.random.default_rng(5)
+    ci, co = 128, 64
+    h = be.upload(sh.storage_round(rng.standard_normal((npar, ci)), dtype))
+    up = be.upload(sh.storage_round(rng.standard_normal((npar, 8 * co)), dtype))
+    wt = sh.storage_round(rng.standard_normal((co, 27, co)) / math.sqrt(27 * co), dtype)
+    dm = be.build_c2s_map_device(be.upload(logits), npar, coords=pc)
+    m = dm.n
+    rb = be.build_rulebook_for_c2s_map(dm)
+
+    def run_all(rulebook):
+        g, s, y = be.alloc(m * co), be.alloc(m * co), be.alloc(m * co)
+        be.c2s_gather_device(up, dm, g, co)
+        be.skip_repeat_device(h, dm, s, ci, co)
+        be.conv(rulebook, g, wt, None, y, co, co)
+        return [be.download(b) for b in (g, s, y)]
+
+    before = run_all(rb)
+    maps_before = be.download_c2s_map(dm)
+    released = be.trim(sh.TRIM_FREE_BUFFERS | sh.TRIM_WEIGHTS)
+    say(f"device map survives trim dtype={dtype}: {m} children, trim released {released} bytes")
+    assert released > 0
+    maps_after = be.download_c2s_map(dm)
+    for a, b in zip(maps_before, maps_after):
+        assert np.array_equal(a, b)
+    rc, ec, ep, es = orc.c2s_map(pc, logits)
+    assert np.array_equal(maps_after[0], ec) and np.array_equal(maps_after[1], ep)
+    after = run_all(rb)
+    for a, b in zip(before, after):
+        assert np.array_equal(a, b)
+    rb2 = be.build_rulebook_for_c2s_map(dm)
+    again = run_all(rb2)
+    assert np.array_equal(before[2], again[2])
+    rb.free()
+    rb2.free()
+
+
 def test_c2s_no_children_is_error(be32):
     lg = be32.upload(-np.ones((3, 8), np.float32))
     with pytest.raises(sh.HipError) as e:

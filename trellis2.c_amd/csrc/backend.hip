@@ -70,6 +70,13 @@ struct Backend {
     // Pool: size class -> free device blocks.
     std::map<size_t, std::vector<void *>> free_blocks;
     size_t pooled_bytes = 0;
+    // Forced allocation failures (tests of the out-of-memory paths): device
+    // allocation attempts fail_after .. fail_after + fail_count - 1 (counted
+    // from 0 since the hook was set) report hipErrorOutOfMemory without
+    // calling hipMalloc.  fail_after < 0: off.
+    int64_t fail_after = -1;
+    int64_t fail_count = 0;
+    int64_t alloc_attempts = 0;
     // Weight cache.
     std::unordered_map<WeightKey, DevMem, WeightKeyHash> weights;
     std::vector<DevMem> transient;  // uncached weights of the current call
@@ -122,6 +129,15 @@ size_t size_class(size_t bytes) {
     return (bytes + step - 1) / step * step;
 }
 
+hipError_t device_malloc(Backend * be, void ** p, size_t bytes) {
+    *p = nullptr;
+    if (be->fail_after >= 0) {
+        const int64_t attempt = be->alloc_attempts++;
+        if (attempt >= be->fail_after && attempt - be->fail_after < be->fail_count) return hipErrorOutOfMemory;
+    }
+    return hipMalloc(p, bytes);
+}
+
 trellis_status dev_alloc(Backend * be, size_t bytes, DevMem * out) {
     out->ptr = nullptr;
     out->bytes = 0;
@@ -136,7 +152,7 @@ trellis_status dev_alloc(Backend * be, size_t bytes, DevMem * out) {
         return TRELLIS_STATUS_OK;
     }
     void * p = nullptr;
-    hipError_t err = hipMalloc(&p, cls);
+    hipError_t err = device_malloc(be, &p, cls);
     if (err == hipErrorOutOfMemory && be->pooled_bytes > 0) {
         // Release cached blocks and retry once.
         (void) hipGetLastError();
@@ -146,7 +162,7 @@ trellis_status dev_alloc(Backend * be, size_t bytes, DevMem * out) {
             kv.second.clear();
         }
         be->pooled_bytes = 0;
-        err = hipMalloc(&p, cls);
+        err = device_malloc(be, &p, cls);
     }
     if (err != hipSuccess) {
         return hip_status(be, err, "hipMalloc");
@@ -1765,7 +1781,28 @@ trellis_status trellis_sparse_hip_backend_create_ex(int device, const trellis_sp
     be->base.device = device;
     be->device = device;
     be->policy = p;
+    // TRELLIS_HIP_FAIL_ALLOC_AFTER=N[,K]: the device allocation attempts after
+    // the first N fail (K of them, default all), for out-of-memory tests.
+    if (const char * env = getenv("TRELLIS_HIP_FAIL_ALLOC_AFTER")) {
+        char * end = nullptr;
+        const long long after = strtoll(env, &end, 10);
+        long long count = INT64_MAX;
+        if (end != nullptr && *end == ',') count = strtoll(end + 1, nullptr, 10);
+        if (end != env && after >= 0 && count > 0) {
+            be->fail_after = after;
+            be->fail_count = count;
+        }
+    }
     *out = &be->base;
+    return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_fail_alloc(trellis_sparse_backend * backend, int64_t after, int64_t count) {
+    if (backend == nullptr || (after >= 0 && count <= 0)) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    Backend * be = tsh::as_backend(backend);
+    be->fail_after = after < 0 ? -1 : after;
+    be->fail_count = after < 0 ? 0 : count;
+    be->alloc_attempts = 0;
     return TRELLIS_STATUS_OK;
 }
 

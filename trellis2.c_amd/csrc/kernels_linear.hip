@@ -293,7 +293,7 @@ __global__ void __launch_bounds__(256) k_linear_narrow(const typename Store<DT>:
                 const int64_t r = rb * 16 + lg * 4 + i;
                 float v = acc[i] + bv;
                 if (silu) v = v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
-                if (r < n) Store<DT>::st(y, r * co + l16, v);
+                if (r < n) Store<DT>::st_signed(y, r * co + l16, v);
             }
         }
     }

@@ -26,7 +26,7 @@ int blocks_for(int64_t count, int block, int cap = 65536) {
 
 template <int DT>
 __global__ void k_from_f32(const float * __restrict__ src, typename Store<DT>::T * __restrict__ dst, int64_t count) {
-    TSH_GRID_STRIDE(i, count) { Store<DT>::st(dst, i, src[i]); }
+    TSH_GRID_STRIDE(i, count) { Store<DT>::st_signed(dst, i, src[i]); }
 }
 
 template <int DT>
@@ -145,7 +145,7 @@ __global__ void __launch_bounds__(256) k_linear(const typename Store<DT>::T * __
             if (col >= co) continue;
             float v = acc[i][j];
             if (silu) v = v / (1.0f + expf(-v));
-            Store<DT>::st(y, r * co + col, v);
+            Store<DT>::st_signed(y, r * co + col, v);
         }
     }
 }

@@ -39,17 +39,31 @@ template <> struct Store<kF32> {
     using T = float;
     __device__ static float ld(const T * p, int64_t i) { return p[i]; }
     __device__ static void st(T * p, int64_t i, float v) { p[i] = v; }
+    __device__ static void st_signed(T * p, int64_t i, float v) { p[i] = v; }
 };
+// st_signed: the same rounding, except that a positive value which rounds to
+// +0 is stored as the smallest positive subnormal, so that v > 0 holds for
+// the stored value exactly when it held for v.  Used where a sign decides
+// something downstream (uploads and the linear slot, whose 8-wide output is
+// the subdivide logits: child s exists iff logit > 0).
 template <> struct Store<kF16> {
     using T = _Float16;
     __device__ static float ld(const T * p, int64_t i) { return (float) p[i]; }
     __device__ static void st(T * p, int64_t i, float v) { p[i] = (_Float16) v; }
+    __device__ static void st_signed(T * p, int64_t i, float v) {
+        const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16) v);
+        p[i] = __builtin_bit_cast(_Float16, (uint16_t) ((v > 0.0f && h == 0) ? 1 : h));
+    }
 };
 template <> struct Store<kBF16> {
     using T = uint16_t;
     __device__ static float ld(const T * p, int64_t i) { return bf16_to_f32(p[i]); }
     // Round to nearest even with the hardware conversion (NaN stays NaN).
     __device__ static void st(T * p, int64_t i, float v) { p[i] = __builtin_bit_cast(uint16_t, (__bf16) v); }
+    __device__ static void st_signed(T * p, int64_t i, float v) {
+        const uint16_t h = __builtin_bit_cast(uint16_t, (__bf16) v);
+        p[i] = (v > 0.0f && h == 0) ? (uint16_t) 1 : h;
+    }
 };
 
 // A 16-byte chunk of 16-bit storage values (8 of them) to fp32 and back,

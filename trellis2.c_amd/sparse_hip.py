@@ -102,6 +102,7 @@ ABI = {
     "trellis_sparse_hip_device_count": (c_int, []),
     "trellis_sparse_hip_last_error": (c_char_p, [_p]),
     "trellis_sparse_hip_synchronize": (c_int, [_p]),
+    "trellis_sparse_hip_fail_alloc": (c_int, [_p, c_int64, c_int64]),
     "trellis_sparse_hip_rulebook_stats": (c_int, [_p, _p, POINTER(c_int64), POINTER(c_int64), POINTER(c_int64),
                                                   POINTER(c_int64)]),
     "trellis_sparse_hip_download_neighbors": (c_int, [_p, _p, _i32p, c_int64]),
@@ -323,6 +324,10 @@ class Backend:
     def synchronize(self):
         self._check(LIB.trellis_sparse_hip_synchronize(self.ptr), "synchronize")
 
+    def fail_alloc(self, after: int, count: int = 1 << 62):
+        """Device allocation attempts after .. after + count - 1 fail from now on (after < 0: off)."""
+        self._check(LIB.trellis_sparse_hip_fail_alloc(self.ptr, after, count), "fail_alloc")
+
     def trim(self, flags: int) -> int:
         rel = c_size_t(0)
         self._check(self.ops.trim(self.ptr, flags, ctypes.byref(rel)), "trim")
@@ -355,6 +360,19 @@ class Backend:
         count = buf.count if count is None else count
         out = np.empty(count, dtype=np.float32)
         self._check(self.ops.download_f32(self.ptr, buf.handle, _ptr(out, _f32p), count), "download_f32")
+        return out
+
+    def upload_i32(self, arr) -> Buffer:
+        a = np.ascontiguousarray(arr, dtype=np.int32).ravel()
+        h = c_void_p()
+        self._check(self.ops.upload_i32(self.ptr, _ptr(a, _i32p), a.size, ctypes.byref(h)), "upload_i32")
+        return Buffer(self, h, a.size)
+
+    def download_i32(self, buf: Buffer, count: int | None = None) -> np.ndarray:
+        """An int32 buffer (upload_i32) back to the host; download_f32 copies its bits unchanged."""
+        count = buf.count if count is None else count
+        out = np.empty(count, dtype=np.int32)
+        self._check(self.ops.download_f32(self.ptr, buf.handle, out.ctypes.data_as(_f32p), count), "download_f32")
         return out
 
     def download_raw(self, buf: Buffer, count: int | None = None) -> np.ndarray:
