@@ -293,6 +293,34 @@ trellis_status trellis_sparse_hip_upload_coords(trellis_sparse_backend * backend
 trellis_status trellis_sparse_hip_free_c2s_map(trellis_sparse_backend * backend,
                                                trellis_sparse_c2s_device_map * map);
 
+/* Allocation-free subdivide: build_c2s_map_device's result written into
+ * caller-owned buffers.  No counterpart in the reference; it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  It calls no hipMalloc,
+ * hipFree or other allocating routine: its working memory (per-parent child
+ * counts and their scan) is a fixed device array of about 8 MB per GPU,
+ * held until the process ends and shared by every call on that GPU, so calls
+ * that overlap on one GPU (e.g. two backends on different streams) race.
+ *   coords      int32 buffer (upload_i32) of the n parents' (b, x, y, z)
+ *   logits      [n][8] buffer in the backend's compute_dtype; child s of
+ *               parent p exists iff logits[p][s] > 0 (executor.c:108-154)
+ *   coords_out  int32 buffer of >= 4 m entries, parent_out / subidx_out
+ *               int32 buffers of >= m entries; children parent-major,
+ *               subidx ascending, coordinates (b, 2x+(s&1), 2y+((s>>1)&1),
+ *               2z+((s>>2)&1)) - the same arrays download_c2s_map returns
+ *   n_out       m, the number of children (set also when the outputs are too
+ *               small, so the caller can size them)
+ * n > 1048576 -> INVALID_ARGUMENT (the scratch limit); outputs smaller than m
+ * -> INVALID_ARGUMENT with *n_out = m and nothing written; no child ->
+ * TRELLIS_STATUS_ERROR, as build_c2s_map_device.  The fill is queued on the
+ * backend's stream; the child count is read back synchronously. */
+trellis_status trellis_sparse_hip_build_c2s_map_into(trellis_sparse_backend * backend,
+                                                     const trellis_sparse_buffer * coords,
+                                                     const trellis_sparse_buffer * logits, int64_t n,
+                                                     trellis_sparse_buffer * coords_out,
+                                                     trellis_sparse_buffer * parent_out,
+                                                     trellis_sparse_buffer * subidx_out, int64_t * n_out);
+
 /* ------------------------------------------------------------------------ */
 /* Spatial-to-channel downsample of the encoder on the device (no vtable     */
 /* counterpart: the reference runs it on the host, replacing                 */

@@ -17,6 +17,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <thread>
 
 #include "tsh_internal.h"
@@ -77,6 +78,9 @@ struct Backend {
     int64_t fail_after = -1;
     int64_t fail_count = 0;
     int64_t alloc_attempts = 0;
+    // Device address of this device's copy of `scratch` (the allocation-free
+    // subdivide's working memory), or null when it could not be resolved.
+    unsigned char * scratch_dev = nullptr;
     // Weight cache.
     std::unordered_map<WeightKey, DevMem, WeightKeyHash> weights;
     std::vector<DevMem> transient;  // uncached weights of the current call
@@ -94,6 +98,41 @@ struct Backend {
     hipEvent_t user_events[16] = {};
     StageMark open[TRELLIS_SPARSE_HIP_STAGE_COUNT];
 };
+
+// Working memory of trellis_sparse_hip_build_c2s_map_into, which allocates
+// nothing: per-parent child counts, their exclusive scan, the scan total and
+// the scan's tile sums, for at most kIntoMaxParents parents.  Each device
+// holds its own copy until the process ends.  Host code uses the device
+// address from hipGetSymbolAddress (resolved once per device at backend
+// creation), never the array's name: in host code the name is a host-side
+// stand-in, not a device address.
+constexpr int64_t kIntoMaxParents = int64_t(1) << 20;
+constexpr size_t kIntoCounts = 0;                                        // int32 [kIntoMaxParents]
+constexpr size_t kIntoOffsets = kIntoCounts + 4 * kIntoMaxParents;       // int32 [kIntoMaxParents]
+constexpr size_t kIntoTotal = kIntoOffsets + 4 * kIntoMaxParents;        // int32, own 256-byte line
+constexpr size_t kIntoSums = kIntoTotal + 256;                           // scan tile sums
+constexpr size_t kIntoScratchBytes = kIntoSums + 16384;
+static __device__ __align__(256) unsigned char scratch[kIntoScratchBytes];
+
+// Resolves this device's copy of `scratch` once per device (the caller has
+// made `device` current).  Returns null on failure.
+unsigned char * scratch_address(int device) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static unsigned char * addr[kMaxDevices] = {};
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (addr[device] == nullptr) {
+        void * p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || p == nullptr) {
+            (void) hipGetLastError();
+            return nullptr;
+        }
+        addr[device] = (unsigned char *) p;
+    }
+    return addr[device];
+}
 
 namespace {
 
@@ -1781,6 +1820,7 @@ trellis_status trellis_sparse_hip_backend_create_ex(int device, const trellis_sp
     be->base.device = device;
     be->device = device;
     be->policy = p;
+    be->scratch_dev = tsh::scratch_address(device);
     // TRELLIS_HIP_FAIL_ALLOC_AFTER=N[,K]: the device allocation attempts after
     // the first N fail (K of them, default all), for out-of-memory tests.
     if (const char * env = getenv("TRELLIS_HIP_FAIL_ALLOC_AFTER")) {
@@ -1980,6 +2020,54 @@ trellis_status trellis_sparse_hip_free_c2s_map(trellis_sparse_backend * backend,
     tsh::select_device(be);
     tsh::map_release(be, map);
     return TRELLIS_STATUS_OK;
+}
+
+trellis_status trellis_sparse_hip_build_c2s_map_into(trellis_sparse_backend * backend,
+                                                     const trellis_sparse_buffer * coords,
+                                                     const trellis_sparse_buffer * logits, int64_t n,
+                                                     trellis_sparse_buffer * coords_out,
+                                                     trellis_sparse_buffer * parent_out,
+                                                     trellis_sparse_buffer * subidx_out, int64_t * n_out) {
+    using namespace tsh;
+    if (backend == nullptr || n_out == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
+    *n_out = 0;
+    Backend * be = as_backend(backend);
+    const bool int_bufs = coords != nullptr && coords_out != nullptr && parent_out != nullptr &&
+                          subidx_out != nullptr && coords->dtype < 0 && coords_out->dtype < 0 &&
+                          parent_out->dtype < 0 && subidx_out->dtype < 0;
+    if (n <= 0 || !int_bufs || coords->count < (size_t) n * 4 || !float_buffer_ok(be, logits, (size_t) n * 8)) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "build_c2s_map_into: bad argument");
+    }
+    if (n > kIntoMaxParents) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT,
+                    "build_c2s_map_into: more than 1048576 parents (the size of its fixed scratch)");
+    }
+    if (be->scratch_dev == nullptr) {
+        return fail(be, TRELLIS_STATUS_ERROR, "build_c2s_map_into: scratch address unavailable on this device");
+    }
+    select_device(be);
+    hipStream_t s = be->stream;
+    int32_t * counts = (int32_t *) (be->scratch_dev + kIntoCounts);
+    int32_t * offsets = (int32_t *) (be->scratch_dev + kIntoOffsets);
+    int32_t * total = (int32_t *) (be->scratch_dev + kIntoTotal);
+    void * sums = be->scratch_dev + kIntoSums;
+    static_assert(kIntoSums + (kIntoMaxParents / 2048 + 2) * 4 <= kIntoScratchBytes, "scan sums fit");
+    // Every counts and offsets entry below n, the total and the tile sums
+    // are written before they are read, so nothing needs clearing.
+    hipError_t err = launch_c2s_count(be->policy.compute_dtype, logits->ptr, n, counts, s);
+    if (err == hipSuccess) err = launch_scan_exclusive(counts, offsets, n, total, sums, s);
+    int32_t m = 0;
+    if (err == hipSuccess) err = hipMemcpyAsync(&m, total, 4, hipMemcpyDeviceToHost, s);
+    if (err == hipSuccess) err = hipStreamSynchronize(s);
+    if (err != hipSuccess) return hip_status(be, err, "build_c2s_map_into: count/scan");
+    if (m <= 0) return fail(be, TRELLIS_STATUS_ERROR, "subdivide produced no children (all logits <= 0)");
+    *n_out = m;
+    if (coords_out->count < (size_t) m * 4 || parent_out->count < (size_t) m || subidx_out->count < (size_t) m) {
+        return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "build_c2s_map_into: outputs hold fewer than n_out children");
+    }
+    err = launch_c2s_fill(be->policy.compute_dtype, (const int32_t *) coords->ptr, logits->ptr, offsets, n,
+                          (int32_t *) coords_out->ptr, (int32_t *) parent_out->ptr, (int32_t *) subidx_out->ptr, s);
+    return hip_status(be, err, "build_c2s_map_into: fill");
 }
 
 trellis_status trellis_sparse_hip_s2c_build_device(trellis_sparse_backend * backend, const int32_t * fine_coords_bxyz,

@@ -111,6 +111,7 @@ ABI = {
     "trellis_sparse_hip_download_raw": (c_int, [_p, _p, c_void_p, c_size_t]),
     "trellis_sparse_hip_upload_coords": (c_int, [_p, _i32p, c_int64, POINTER(_p)]),
     "trellis_sparse_hip_free_c2s_map": (c_int, [_p, _p]),
+    "trellis_sparse_hip_build_c2s_map_into": (c_int, [_p, _p, _p, c_int64, _p, _p, _p, POINTER(c_int64)]),
     "trellis_sparse_hip_profile_enable": (c_int, [_p, c_int]),
     "trellis_sparse_hip_profile_read": (c_int, [_p, POINTER(StageTimes), c_int]),
     "trellis_sparse_hip_event_record": (c_int, [_p, c_int]),
@@ -374,6 +375,18 @@ class Backend:
         out = np.empty(count, dtype=np.int32)
         self._check(self.ops.download_f32(self.ptr, buf.handle, out.ctypes.data_as(_f32p), count), "download_f32")
         return out
+
+    def build_c2s_map_into(self, coords: Buffer, logits: Buffer, n: int, coords_out: Buffer, parent_out: Buffer,
+                           subidx_out: Buffer) -> int:
+        """Allocation-free subdivide into int32 buffers; returns the child count."""
+        m = c_int64()
+        st = LIB.trellis_sparse_hip_build_c2s_map_into(self.ptr, coords.handle, logits.handle, n, coords_out.handle,
+                                                       parent_out.handle, subidx_out.handle, ctypes.byref(m))
+        if st != OK:
+            err = HipError(st, "build_c2s_map_into", LIB.trellis_sparse_hip_last_error(self.ptr).decode())
+            err.n_out = m.value
+            raise err
+        return m.value
 
     def download_raw(self, buf: Buffer, count: int | None = None) -> np.ndarray:
         count = buf.count if count is None else count
