@@ -20,6 +20,9 @@
 //               and read pre-packed weight fragments; row groups of 16 with no
 //               valid neighbour skip the offset, others multiply zeros for
 //               their missing neighbours.
+//  * os64     - bf16/fp16 storage, Ci = Co = 64 (the compact schedule's
+//               choice for that shape): output-stationary over the same pair
+//               lists, sums in registers for all 27 offsets, no tile sums.
 //  * compact  - bf16/fp16 storage, Ci = 64 or Ci % 128 == 0, Co % 64 == 0 or
 //               Co = 16 / 32 (one 16/32-channel block).  The same MFMA
 //               tiles driven by the kernel map's compacted per-tile pair
@@ -1062,6 +1065,159 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     }
 }
 
+// ---------------------------------------------------------------------------
+// Output-stationary MFMA kernel for Ci = 64 (bf16 / fp16 storage).
+//
+// The compacted kernels add each 128-pair unit's products into fp32 tile sums
+// in LDS; with Ci = 64 a unit is only two K steps, so that read-modify-write
+// (Co x 8 bytes per pair) costs more than the unit's MFMAs.  Here every row's
+// sums stay in registers for all 27 offsets: a block owns one 256-row map
+// tile (4 wavefronts x 64 rows, lane = row), a wavefront 4 row blocks of 16
+// x all Co = 64 channels.  For offset k each row's source is read from the
+// tile's pair list for k (its rank among the tile's rows with a neighbour at
+// k comes from ballots of the row masks), the 16 source rows of a row block
+// are loaded coalesced (four lanes per 64-byte K step) and moved to MFMA
+// operand order with ds_bpermute; a row without a neighbour at k multiplies
+// zeros.  The offset's 8 KB of weights are shared through a double-buffered
+// LDS slot: one barrier per offset.  Each row's 27 sources are fetched in one
+// round trip at the start; operand loads run two offsets ahead.  No unit
+// lists, no tile sums, no flushes: the MFMA rows include the rows without a
+// neighbour (27 N row-offsets against P), which is the price of keeping the
+// sums in registers.  (Sorting each tile's rows by mask, so that 16-row
+// blocks without a neighbour at k could be skipped, measured slower.)
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ void __launch_bounds__(256, 2) k_conv_os64(const typename Store<DT>::T * __restrict__ x,
+                                                      const int32_t * __restrict__ pair_src,
+                                                      const int32_t * __restrict__ tile_off,
+                                                      const uint32_t * __restrict__ mask,
+                                                      const typename Store<DT>::T * __restrict__ w16,
+                                                      const float * __restrict__ bias,
+                                                      typename Store<DT>::T * __restrict__ y, int64_t n) {
+    using T = typename Store<DT>::T;
+    using V = typename Mfma<DT>::V;
+    constexpr int CI = 64, CO = 64;
+    constexpr int QB = 4;                      // row blocks per wavefront
+    constexpr int NT = CO / 16;                // column tiles (grouped packing: lane's NT columns adjacent)
+    constexpr int WSLOT = (CI / 8) * CO * 8;   // weight elements per offset
+    constexpr int WPT = WSLOT * 2 / 16 / 256;  // 16-byte weight pieces per thread per offset
+    static_assert(WPT == 2, "8 KB of weights per offset over 256 threads");
+    __shared__ __attribute__((aligned(16))) T s_w[2][WSLOT];
+    __shared__ int32_t s_cnt[27][4];
+    __shared__ int32_t s_off[27];
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int64_t tile = xcd_remap(blockIdx.x, (int64_t) gridDim.x);
+    const int64_t row0 = tile * kMapTile;
+    const int64_t my_row = row0 + wave * 64 + lane;
+    const uint32_t m = my_row < n ? mask[my_row] : 0u;
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    if (t < 27) s_off[t] = tile_off[tile * 27 + t];
+    // Rows of each wavefront with a neighbour at k, for the ranks below.
+#pragma unroll 1
+    for (int k = 0; k < 27; ++k) {
+        const int c = __popcll(__ballot((m >> k) & 1u));
+        if (lane == 0) s_cnt[k][wave] = c;
+    }
+    // Weights of offsets 0 (into slot 0) and 1 (in registers).
+    V wreg[WPT];
+#pragma unroll
+    for (int j = 0; j < WPT; ++j) wreg[j] = *(const V *) (w16 + (int64_t) (t + j * 256) * 8);
+#pragma unroll
+    for (int j = 0; j < WPT; ++j) *(V *) &s_w[0][(t + j * 256) * 8] = wreg[j];
+#pragma unroll
+    for (int j = 0; j < WPT; ++j) wreg[j] = *(const V *) (w16 + WSLOT + (int64_t) (t + j * 256) * 8);
+    lds_barrier();
+
+    // Source rows of this lane's row at every offset (or -1), all fetched
+    // in one round trip: the row's rank in the tile's list for k is the
+    // count of earlier rows with a neighbour at k.
+    int32_t src[27];
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        const uint64_t bk = __ballot((m >> k) & 1u);
+        int base = 0;
+        for (int w = 0; w < wave; ++w) base += s_cnt[k][w];
+        src[k] = ((m >> k) & 1u) ? pair_src[s_off[k] + base + __popcll(bk & lt)] : -1;
+    }
+    // A pieces of offset k: row block q, K step f; lane 4i + c holds 16 bytes
+    // (chunk c of the step) of row i of the block.
+    constexpr int AHEAD = 2;  // offsets whose A loads are in flight
+    V ra[AHEAD + 1][QB][2];
+    auto load_a = [&](V (&a)[QB][2], int32_t src) {
+#pragma unroll
+        for (int q = 0; q < QB; ++q) {
+            const int32_t sq = __shfl(src, q * 16 + (lane >> 2));
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+                a[q][f] = sq >= 0 ? *(const V *) (x + (int64_t) sq * CI + f * 32 + (lane & 3) * 8) : V{};
+        }
+    };
+    f32x4 acc[QB][NT];
+#pragma unroll
+    for (int q = 0; q < QB; ++q)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int perm = (4 * l16 + lg) * 4;
+#pragma unroll
+    for (int k = 0; k < AHEAD; ++k) load_a(ra[k], src[k]);
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        const int cur = k & 1;
+        const int ar = k % (AHEAD + 1);
+        if (k + AHEAD < 27) load_a(ra[(k + AHEAD) % (AHEAD + 1)], src[k + AHEAD]);
+        // Weight fragments of offset k: K step f, column tile nt.
+        V bw[2][NT];
+        const T * ws = &s_w[cur][0];
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) bw[f][nt] = *(const V *) (ws + ((f * 4 + lg) * CO + nt * 16 + l16) * 8);
+#pragma unroll
+        for (int q = 0; q < QB; ++q)
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+                const V a = to_mfma_rows<V>(ra[ar][q][f], perm);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[q][nt] = Mfma<DT>::mac(a, bw[f][nt], acc[q][nt]);
+            }
+        // Offset k + 1's weights into the other slot (read last at offset
+        // k - 1, before the previous barrier); offset k + 2's into registers.
+        if (k + 1 < 27) {
+#pragma unroll
+            for (int j = 0; j < WPT; ++j) *(V *) &s_w[cur ^ 1][(t + j * 256) * 8] = wreg[j];
+        }
+        if (k + 2 < 27) {
+#pragma unroll
+            for (int j = 0; j < WPT; ++j)
+                wreg[j] = *(const V *) (w16 + (int64_t) (k + 2) * WSLOT + (int64_t) (t + j * 256) * 8);
+        }
+        lds_barrier();
+    }
+    // Epilogue: bias, round, store; lane holds rows 4 lg + i of each row
+    // block, channels 4 l16 .. 4 l16 + 3 (grouped packing).
+    float bv[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) bv[nt] = bias != nullptr ? bias[l16 * NT + nt] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < QB; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t row = row0 + wave * 64 + q * 16 + lg * 4 + i;
+            if (row >= n) continue;
+            union {
+                uint2 u;
+                T h[4];
+            } o;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) o.h[nt] = round_to_store<DT>(acc[q][nt][i] + bv[nt]);
+            *(uint2 *) (y + row * CO + l16 * NT) = o.u;
+        }
+}
+
 }  // namespace
 
 hipError_t launch_conv_generic(int dtype, const void * x, const int32_t * nbr, const float * w32, const float * bias,
@@ -1192,6 +1348,24 @@ hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int3
 #undef TSH_STREAM
 }
 }  // namespace
+
+bool conv_os_supported(int dtype, int ci, int co) { return (dtype == kF16 || dtype == kBF16) && ci == 64 && co == 64; }
+
+hipError_t launch_conv_os(int dtype, const void * x, const int32_t * pair_src, const int32_t * tile_off,
+                          const uint32_t * mask, const void * w16, const float * bias, void * y, int64_t n, int ci,
+                          int co, hipStream_t s) {
+    if (!conv_os_supported(dtype, ci, co) || n <= 0) return hipErrorInvalidValue;
+    const int64_t tiles = (n + kMapTile - 1) / kMapTile;
+    if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+    if (dtype == kBF16) {
+        k_conv_os64<kBF16><<<(unsigned) tiles, 256, 0, s>>>((const uint16_t *) x, pair_src, tile_off, mask,
+                                                            (const uint16_t *) w16, bias, (uint16_t *) y, n);
+    } else {
+        k_conv_os64<kF16><<<(unsigned) tiles, 256, 0, s>>>((const _Float16 *) x, pair_src, tile_off, mask,
+                                                           (const _Float16 *) w16, bias, (_Float16 *) y, n);
+    }
+    return hipGetLastError();
+}
 
 hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const int32_t * pair_dst,
                                    const int32_t * tile_off, const int32_t * tile_counts, const void * w16,

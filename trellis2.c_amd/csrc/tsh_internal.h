@@ -221,6 +221,13 @@ hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pa
                                    const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
                                    const ConvEpilogue & epi = ConvEpilogue());
 
+// Output-stationary MFMA conv for Ci = Co = 64 over the tile-major pair lists
+// and the row masks (weights in the grouped packing of conv_stream_group(64)).
+bool conv_os_supported(int dtype, int ci, int co);
+hipError_t launch_conv_os(int dtype, const void * x, const int32_t * pair_src, const int32_t * tile_off,
+                          const uint32_t * mask, const void * w16, const float * bias, void * y, int64_t n, int ci,
+                          int co, hipStream_t s);
+
 // Everything else (kernels_misc.hip).
 hipError_t launch_convert_from_f32(int dtype, const float * src, void * dst, int64_t count, hipStream_t s);
 hipError_t launch_convert_to_f32(int dtype, const void * src, float * dst, int64_t count, hipStream_t s);
