@@ -450,11 +450,30 @@ def run_block(args):
 def conv_schedule(dtype, ci, co, algo):
     """Name of the conv kernel the backend runs (its fallback rules)."""
     mfma = dtype != sh.F32 and ci % 32 == 0 and co % 64 == 0
+    if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and ci == 64 and co == 64:
+        return "os64"  # output-stationary kernel over the compact lists (no fused epilogue)
     if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and (ci % 128 == 0 or ci == 64):
         return "compact"
     if algo in (sh.CONV_AUTO, sh.CONV_COMPACT, sh.CONV_MASKED) and mfma:
         return "masked"
     return "generic"
+
+
+def host_cpu_model():
+    """The host's CPU model string (/proc/cpuinfo), or the machine name."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+# Every stride-th output row of the CPU baseline's conv (about 5-30 s of CPU
+# work per configuration; config 1 runs in full).
+CPU_STRIDE = {1: 1, 2: 16, 3: 16, 4: 16, 5: 32}
 
 
 def cpu_baseline(cfg, w, stride):
@@ -491,11 +510,14 @@ def cpu_baseline(cfg, w, stride):
     t["conv"] = convs * t_sample * pairs_total / max(1, pairs_sample)
     total = sum(t.values())
     flops = convs * wl.conv_flops(pairs_total, w["ci"], w["co"])
-    sample = (f"cfg{cfg}: subdivide/broadcast/hash on the full set, conv timed on every {stride}th output row "
-              f"({pairs_sample} of {pairs_total} pairs) and extrapolated by pair count; 1 thread")
+    full = "subdivide, broadcast and hash" if cfg == 3 else "hash"
+    conv_part = ("conv on every output row" if stride == 1 else
+                 f"conv timed on every {stride}th output row ({pairs_sample} of {pairs_total} pairs) and "
+                 "extrapolated by pair count")
+    sample = f"cfg{cfg}: {full} on the full set, {conv_part}" + ("; both convs" if convs == 2 else "") + "; 1 thread"
     return {"value": flops / total / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port", "sample": sample,
             "seconds_full_estimate": round(total, 3), "stage_seconds": {k: round(v, 4) for k, v in t.items()},
-            "host_cpu": platform.processor() or platform.machine(), "host_nproc": os.cpu_count()}
+            "host_cpu": host_cpu_model(), "host_nproc": os.cpu_count()}
 
 
 def main():
@@ -505,7 +527,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-stride", type=int, default=16)
+    ap.add_argument("--cpu-stride", type=int, default=0,
+                    help="every n-th output row for the CPU baseline's conv (default: per configuration)")
     ap.add_argument("--conv-algo", type=int, default=sh.CONV_AUTO)
     ap.add_argument("--block", choices=["convnext", "convnext_fused", "convnext_block", "c2s", "s2c", "mesh"],
                     help="instead of the configuration step, time one decoder block composed from the backend's "
@@ -580,6 +603,16 @@ def main():
     per_launch_flops = wl.conv_flops(job.pairs, job.ci, job.co)
     achieved = per_launch_flops / (conv_avg * 1e-3) / 1e12 if conv_avg > 0 else 0.0
     hm_ms = (stages["hash"][0] + stages["map"][0]) / args.steps
+    # Hash + kernel map against HBM: the work definition's bytes (hash 28 N,
+    # map 16 N + 108 N + 8 P + 216, the 108 N being an [N][27] neighbour
+    # table), and the bytes the production build moves, which writes row
+    # masks and per-tile pair lists instead of that table (hash 28 N; map
+    # 16 N coordinates + 4 N masks + 8 P pairs + 2 x 108 bytes per 256-row
+    # tile of counts and list starts).
+    hm_def_bytes = wl.hash_bytes(job.m) + wl.map_bytes(job.m, job.pairs)
+    tiles = (job.m + 255) // 256
+    hm_moved_bytes = 28.0 * job.m + 16.0 * job.m + 4.0 * job.m + 8.0 * job.pairs + 216.0 * tiles
+    hm_gbs = hm_def_bytes / (hm_ms * 1e-3) / 1e9 if hm_ms > 0 else 0.0
     elem = 4 if spec["dtype"] == sh.F32 else 2
     # The conv's binding roofline: compute (2 P Ci Co at the dtype's MFMA or
     # fp32 peak) or HBM (compulsory bytes at 8 TB/s), whichever takes longer.
@@ -617,6 +650,12 @@ def main():
         "data": "synthetic (seeded generator, random-init weights)",
         "config": job.describe(),
         "hash_map_mvoxels_per_s": round(job.m / (hm_ms * 1e-3) / 1e6, 1) if hm_ms > 0 else None,
+        "hash_map_roofline": {
+            "bound": "hbm", "achieved": round(hm_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(hm_gbs / PEAK_HBM_GBS, 4), "ms_per_step": round(hm_ms, 4),
+            "definition_bytes": hm_def_bytes, "moved_bytes": hm_moved_bytes,
+            "moved_gbs": round(hm_moved_bytes / (hm_ms * 1e-3) / 1e9, 1) if hm_ms > 0 else 0.0,
+        },
         "conv_kernel_tflops": round(achieved, 2),
         "stage_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in stages.items()},
         "roofline": {
@@ -638,7 +677,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         log("bench: timing the CPU oracle baseline")
-        result["cpu_baseline"] = cpu_baseline(cfg, w, args.cpu_stride)
+        result["cpu_baseline"] = cpu_baseline(cfg, w, args.cpu_stride or CPU_STRIDE[cfg])
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
