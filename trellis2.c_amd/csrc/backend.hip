@@ -784,11 +784,9 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
         if (st != TRELLIS_STATUS_OK) return st;
     }
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_HASH);
-    TSH_TRY(be, launch_fill_u64((uint64_t *) r->bkeys.ptr, r->table_slots, 0ull, s));
-    TSH_TRY(be, launch_fill_i32((int32_t *) r->counters.ptr, kCounterInts, 0, s));
+    TSH_TRY(be, launch_hash_clear((uint64_t *) r->bkeys.ptr, r->table_slots, (int32_t *) r->counters.ptr, s));
     TSH_TRY(be, launch_brick_insert(coords, n, (uint64_t *) r->bkeys.ptr, (int32_t *) r->bidx.ptr, r->table_slots,
-                                    (int32_t *) r->counters.ptr, s));
-    TSH_TRY(be, launch_pool_init((int32_t *) r->pool.ptr, (const int32_t *) r->counters.ptr, n, s));
+                                    (int32_t *) r->counters.ptr, (int32_t *) r->pool.ptr, s));
     TSH_TRY(be, launch_voxel_insert(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
                                     r->table_slots, (int32_t *) r->pool.ptr, (int32_t *) r->counters.ptr, s));
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_HASH);

@@ -65,11 +65,13 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
 
 __device__ __forceinline__ int lane_id() { return (int) __lane_id(); }
 
-__global__ void k_fill_u64(uint64_t * __restrict__ p, int64_t count, uint64_t value) {
+// Empties the brick table (keys to 0) and clears the build's counters, in one
+// launch.
+__global__ void k_hash_clear(uint64_t * __restrict__ keys, int64_t slots, int32_t * __restrict__ counters) {
     const int64_t stride = (int64_t) gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
-        p[i] = value;
-    }
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < kCounterInts) counters[t] = 0;
+    for (int64_t i = t; i < slots; i += stride) keys[i] = 0ull;
 }
 
 __global__ void k_fill_i32(int32_t * __restrict__ p, int64_t count, int32_t value) {
@@ -82,11 +84,12 @@ __global__ void k_fill_i32(int32_t * __restrict__ p, int64_t count, int32_t valu
 // One lane per voxel.  Lanes of a wavefront first agree on one representative
 // per distinct brick (ballot/readlane, no memory traffic); representatives
 // then insert concurrently with a 64-bit CAS.  The lane that claims an empty
-// slot numbers the brick.
+// slot numbers the brick, and its wavefront sets the brick's 64 pool cells to
+// -1 (one coalesced 256-byte store per new brick).
 __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict__ coords, int64_t n,
                                                          uint64_t * __restrict__ bkeys, int32_t * __restrict__ bidx,
                                                          uint64_t mask, int32_t * __restrict__ counters,
-                                                         int32_t group_cap) {
+                                                         int32_t group_cap, int32_t * __restrict__ pool) {
     const int64_t i = (int64_t) blockIdx.x * kBlock + threadIdx.x;
     const bool active = i < n;
     uint64_t key = 0;
@@ -149,24 +152,16 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
         s_base = total > 0 ? g * group_cap + atomicAdd(&counters[kBrickCounter + g], total) : 0;
     }
     __syncthreads();
+    int32_t idx = 0;
     if (won) {
-        int32_t idx = s_base + __popcll(wins & below);
+        idx = s_base + __popcll(wins & below);
         for (int w = 0; w < wave; ++w) idx += s_wave_new[w];
         bidx[s] = idx;
     }
-}
-
-// Clears the pool cells of the bricks numbered so far (counts read on
-// device); blockIdx.y = brick group.
-__global__ void k_pool_init(int32_t * __restrict__ pool, const int32_t * __restrict__ counters, int32_t group_cap) {
-    const int g = blockIdx.y;
-    int32_t bricks = counters[kBrickCounter + g];
-    bricks = bricks < group_cap ? bricks : group_cap;
-    int32_t * gp = pool + (int64_t) g * group_cap * kBrickCells;
-    const int64_t cells = (int64_t) bricks * kBrickCells;
-    const int64_t stride = (int64_t) gridDim.x * blockDim.x * 4;
-    for (int64_t i = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) * 4; i < cells; i += stride) {
-        *(int4 *) (gp + i) = make_int4(-1, -1, -1, -1);
+    // The wavefront's new bricks start empty: lane c clears cell c of each.
+    for (uint64_t left = wins; left != 0; left &= left - 1) {
+        const int32_t b = __builtin_amdgcn_readlane(idx, __builtin_ctzll(left));
+        pool[(int64_t) b * kBrickCells + lane] = -1;
     }
 }
 
@@ -349,12 +344,6 @@ int grid_for(int64_t count, int block, int cap = 65536) {
 
 }  // namespace
 
-hipError_t launch_fill_u64(uint64_t * p, int64_t count, uint64_t value, hipStream_t s) {
-    if (count <= 0) return hipSuccess;
-    k_fill_u64<<<grid_for(count, 256, 16384), 256, 0, s>>>(p, count, value);
-    return hipGetLastError();
-}
-
 hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_t s) {
     if (count <= 0) return hipSuccess;
     k_fill_i32<<<grid_for(count, 256, 16384), 256, 0, s>>>(p, count, value);
@@ -363,19 +352,19 @@ hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_
 
 int64_t brick_group_cap(int64_t n) { return ((n + kBlock - 1) / kBlock + kBrickGroups - 1) / kBrickGroups * kBlock; }
 
-hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx, int64_t slots,
-                               int32_t * counters, hipStream_t s) {
-    const int64_t blocks = (n + kBlock - 1) / kBlock;
-    k_brick_insert<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
-                                                        (uint64_t) (slots - 1), counters,
-                                                        (int32_t) brick_group_cap(n));
+hipError_t launch_hash_clear(uint64_t * bkeys, int64_t slots, int32_t * counters, hipStream_t s) {
+    // The grid has at least 256 threads, which covers the counters.
+    static_assert(kCounterInts <= 256, "counters cleared by the first block");
+    k_hash_clear<<<grid_for(slots, 256, 16384), 256, 0, s>>>(bkeys, slots, counters);
     return hipGetLastError();
 }
 
-hipError_t launch_pool_init(int32_t * pool, const int32_t * counters, int64_t n, hipStream_t s) {
-    const int64_t cap = brick_group_cap(n);
-    const dim3 grid((unsigned) grid_for(cap * kBrickCells / 4, 256, 256), kBrickGroups);
-    k_pool_init<<<grid, 256, 0, s>>>(pool, counters, (int32_t) cap);
+hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx, int64_t slots,
+                               int32_t * counters, int32_t * pool, hipStream_t s) {
+    const int64_t blocks = (n + kBlock - 1) / kBlock;
+    k_brick_insert<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
+                                                        (uint64_t) (slots - 1), counters,
+                                                        (int32_t) brick_group_cap(n), pool);
     return hipGetLastError();
 }
 

@@ -170,13 +170,15 @@ namespace tsh {
 // ---------------------------------------------------------------------------
 
 // Voxel hash + kernel map (kernels_map.hip).
-hipError_t launch_fill_u64(uint64_t * p, int64_t count, uint64_t value, hipStream_t s);
 hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_t s);
+// Brick table keys to 0 and the build counters (kCounterInts) to 0, one launch.
+hipError_t launch_hash_clear(uint64_t * bkeys, int64_t slots, int32_t * counters, hipStream_t s);
+// Inserts the voxels' bricks, numbers the new ones and sets their pool rows to -1.
 hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx,
-                               int64_t slots, int32_t * counters, hipStream_t s);
+                               int64_t slots, int32_t * counters, int32_t * pool, hipStream_t s);
 // Bricks per group for n voxels (pool capacity = kBrickGroups * that).
 int64_t brick_group_cap(int64_t n);
-hipError_t launch_pool_init(int32_t * pool, const int32_t * counters, int64_t n, hipStream_t s);
+
 hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
                                int64_t slots, int32_t * pool, int32_t * counters, hipStream_t s);
 // Neighbour table, masks, per-(tile, offset) counts and list starts, and the
