@@ -16,7 +16,10 @@ tests/test_sparse_decoder_backend.c:16-24 (|a-b| <= 2e-2 max(1,|a|,|b|)).
 The deep-channel cases run Ci = 384, 512 and 1024 with 64- and 128-channel
 output blocks on ragged row counts: with Ci >= 512 (or Ci = 384) one unit of
 128 pairs takes more than one block of 8 (or 4) K steps, so the kernels'
-mid-unit block prefetch is executed.
+mid-unit block prefetch is executed.  Co % 256 == 0 (with Ci % 128 == 0) runs
+256-channel blocks over half map tiles: those cases include a last tile whose
+second half is short (900 and 1500 rows) or empty (1300 and 600 rows), and a
+single 200-row tile.
 """
 import math
 import sys
@@ -126,7 +129,7 @@ def test_config2_fused_block_full_size_vs_oracle_sample(backends):
 
 
 DEEP_CASES = [(512, 128, 3001), (384, 128, 2000), (1024, 128, 1200), (512, 64, 2500), (1024, 64, 1777),
-              (512, 512, 1300)]
+              (512, 512, 1300), (128, 256, 900), (256, 1024, 600), (384, 256, 1500), (256, 256, 200)]
 
 
 @pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])

@@ -203,7 +203,7 @@ def be_sched():
 
 @pytest.mark.parametrize("algo", ["compact", "masked"])
 @pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])
-@pytest.mark.parametrize("ci,co", [(64, 64), (128, 128), (256, 128), (32, 192), (64, 512)])
+@pytest.mark.parametrize("ci,co", [(64, 64), (128, 128), (256, 128), (32, 192), (64, 512), (128, 256)])
 def test_conv_mfma_vs_oracle(be_sched, algo, dtype, ci, co):
     be = be_sched[(algo, dtype)]
     c = wl.make_coords(1)

@@ -362,7 +362,7 @@ trellis_status get_weight(Backend * be, const float * host, size_t count, int la
             staged.resize(elems * 2);
             uint16_t * w = (uint16_t *) staged.data();
             const int ci8 = ci / 8;
-            const int g = conv_stream_group(co), wn = 16 * g;
+            const int g = conv_stream_group(ci, co), wn = 16 * g;
             for (int o = 0; o < co; ++o) {
                 // Packed column of channel o.
                 const int pos = layout == kLayoutConvMfma ? o : (o / wn) * wn + (o % g) * 16 + (o % wn) / g;
@@ -901,8 +901,9 @@ trellis_status conv_impl(trellis_sparse_backend * backend, const trellis_sparse_
             err = launch_conv_mfma_stream(dt, feats->ptr, (const int32_t *) rulebook->pair_src.ptr,
                                           (const int32_t *) rulebook->pair_dst.ptr,
                                           (const int32_t *) rulebook->tile_off.ptr,
-                                          (const int32_t *) rulebook->tile_counts.ptr, w, (const float *) bd,
-                                          out->ptr, n, ci, co, be->stream, epi);
+                                          (const int32_t *) rulebook->tile_counts.ptr,
+                                          (const uint32_t *) rulebook->mask.ptr, w, (const float *) bd, out->ptr, n,
+                                          ci, co, be->stream, epi);
         } else {
             st = rulebook_ensure_nbr(be, rulebook);
             if (st != TRELLIS_STATUS_OK) return st;

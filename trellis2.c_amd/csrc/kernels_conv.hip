@@ -673,12 +673,13 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-template <int DT, int BN, int RG, int UPB, int DEPTH>
+template <int DT, int BN, int RG, int UPB, int DEPTH, int TMR>
 __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,
                                                         const int32_t * __restrict__ pair_src,
                                                         const int32_t * __restrict__ pair_dst,
                                                         const int32_t * __restrict__ tile_off,
                                                         const int32_t * __restrict__ tile_counts,
+                                                        const uint32_t * __restrict__ mask,
                                                         const typename Store<DT>::T * __restrict__ w16,
                                                         const float * __restrict__ bias,
                                                         typename Store<DT>::T * __restrict__ y, int64_t n, int ci,
@@ -687,7 +688,9 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     using V = typename Mfma<DT>::V;
     constexpr int NW = 8;            // wavefronts
     constexpr int NTHR = 64 * NW;
-    constexpr int TM = kMapTile;     // rows per block = rows per kernel-map tile
+    constexpr int TM = TMR;          // rows per block: a kernel-map tile, or half of one
+    constexpr int HALVES = kMapTile / TM;
+    static_assert(HALVES == 1 || (HALVES == 2 && UPB == 1), "whole or half map tiles");
     constexpr int BK = 32;           // input channels per K step
     constexpr int CG = NW / RG;      // channel groups
     constexpr int WN = BN / CG;      // channels per wavefront
@@ -716,9 +719,12 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     const int rh = wave % RG, ch = wave / RG;
     const int l16 = lane & 15, lg = lane >> 4;
     const int64_t logical = xcd_remap(blockIdx.x, (int64_t) gridDim.x);
-    const int64_t tile = logical / n_col_tiles;
-    const int64_t row0 = tile * TM;
+    // Blocks of one map tile are adjacent: (tile, half, column block).
+    const int64_t tile = logical / (n_col_tiles * HALVES);
+    const int half = HALVES == 1 ? 0 : (int) ((logical / n_col_tiles) % HALVES);
+    const int64_t row0 = tile * kMapTile + half * TM;
     const int col0 = (int) (logical % n_col_tiles) * BN;
+    if (row0 >= n) return;  // the empty second half of a short last tile
     const int ci8 = ci >> 3;
     const int KS = ci / BK;
 
@@ -753,7 +759,9 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     // flushes store instead of adding and the tile sums need no clearing.
     const int tile_rows = (int) ((n - row0) < TM ? (n - row0) : TM);
     const int CU = (tile_rows + PASS - 1) / PASS;
-    const int64_t region = tile * TM * 27;
+    // The centre list holds one entry per row of the map tile, in row
+    // order, so this block's rows start `half * TM` entries into it.
+    const int64_t region = tile * kMapTile * 27 + half * TM;
     const int le = t & (PASS - 1);
     const int32_t * list = t < PASS ? pair_src : pair_dst;
     const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
@@ -774,6 +782,21 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
         s_cnt[t] = cnt_v;
         s_start[t] = off_v;
     }
+    // Half tiles: each offset's list (destinations ascending) splits where
+    // its destinations leave the first half, after as many entries as the
+    // first half's rows have a neighbour at that offset (mask ballots).
+    __shared__ int32_t s_lo[HALVES == 2 ? 27 * 2 : 1];
+    if constexpr (HALVES == 2) {
+        if (t < TM) {
+            const int64_t r = tile * kMapTile + t;
+            const uint32_t mr = r < n ? mask[r] : 0u;
+#pragma unroll 1
+            for (int k = 0; k < 27; ++k) {
+                const int c = __popcll(__ballot((mr >> k) & 1u));
+                if (lane == 0) s_lo[k * 2 + (t >> 6)] = c;
+            }
+        }
+    }
     lds_barrier();
     // Unit table: offset k contributes ceil(count / PASS) units, the centre
     // offset's first, then the others in k order (the packing order): lane p
@@ -781,7 +804,15 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     // unit counts gives each offset's first unit.
     if (t < 64) {
         const int k = t == 0 ? 13 : (t <= 13 ? t - 1 : t);
-        const int c = t < 27 ? s_cnt[k] : 0;
+        int c = t < 27 ? s_cnt[k] : 0;
+        int start = t < 27 ? s_start[k] : 0;
+        if constexpr (HALVES == 2) {
+            if (t < 27) {
+                const int lo = s_lo[k * 2] + s_lo[k * 2 + 1];
+                start += half ? lo : 0;
+                c = half ? c - lo : lo;
+            }
+        }
         const int nu = (c + PASS - 1) / PASS;
         int incl = nu;
 #pragma unroll
@@ -793,7 +824,7 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
 #pragma unroll 1
         for (int p = 0; p < c; p += PASS, ++u) {
             s_uk[u] = k;
-            s_ustart[u] = s_start[k] + p;
+            s_ustart[u] = start + p;
             s_ucnt[u] = c - p < PASS ? c - p : PASS;
         }
         if (t == 26) s_units = incl;
@@ -995,7 +1026,7 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     // Bias, scale and shift are fetched before the barrier so that their
     // latency overlaps the last accumulator flush; the residual chunks were
     // fetched at the start.
-    static_assert(CHUNKS == 16 || BN != 128, "a row's chunks fill one DPP row");
+    static_assert(CHUNKS == 16 || BN != 128, "a row's chunks fill one DPP row (the norm runs for BN = 128 only)");
     // Missing scale / shift are 1 and 0 (exact in r * g + b).
     float bv[8], gv[8], sv[8];
 #pragma unroll
@@ -1053,10 +1084,12 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     using kNorm = std::integral_constant<int, kEpiNorm>;
     using kAdd = std::integral_constant<int, kEpiAdd>;
     if (epi.mode == kEpiNorm) {
-        if (epi.silu) {
-            passes(kNorm(), std::true_type());
-        } else {
-            passes(kNorm(), std::false_type());
+        if constexpr (BN == 128) {
+            if (epi.silu) {
+                passes(kNorm(), std::true_type());
+            } else {
+                passes(kNorm(), std::false_type());
+            }
         }
     } else if (epi.mode == kEpiAdd) {
         passes(kAdd(), std::false_type());
@@ -1280,10 +1313,14 @@ hipError_t launch_conv_mfma_masked(int dtype, const void * x, const int32_t * nb
 }
 
 
-int conv_stream_group(int co) {
-    // 128-channel blocks run k_conv_mfma_wreg (2 row groups x 4 channel
-    // groups of 32), 64-channel blocks k_conv_mfma_stream; 16- and
-    // 32-channel outputs are one block of co channels there.
+bool conv_wide_supported(int ci, int co) { return co % 256 == 0 && ci % 128 == 0; }
+
+int conv_stream_group(int ci, int co) {
+    // 256-channel blocks over half map tiles and 128-channel blocks run
+    // k_conv_mfma_wreg (2 row groups x 4 channel groups of 64 or 32),
+    // 64-channel blocks k_conv_mfma_stream; 16- and 32-channel outputs are
+    // one block of co channels there.
+    if (conv_wide_supported(ci, co)) return 256 / 4 / 16;
     if (co % 128 == 0) return 128 / 4 / 16;
     if (co == 16 || co == 32) return co / (TSH_STREAM_WAVES / TSH_STREAM_ROW_GROUPS) / 16;
     return 64 / (TSH_STREAM_WAVES / TSH_STREAM_ROW_GROUPS) / 16;
@@ -1299,27 +1336,35 @@ bool conv_stream_supported(int dtype, int ci, int co) {
 namespace {
 template <int DT, int BN, int DEPTH, int NW, int RG, int UPB>
 hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
-                           const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
-                           const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
+                           const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
+                           const void * w16, const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
                            const ConvEpilogue & epi) {
     using T = typename Store<DT>::T;
     const int64_t tiles = (n + kMapTile - 1) / kMapTile;
     const int64_t col_tiles = co / BN;
-    const int64_t grid = tiles * col_tiles;
+    const int64_t grid = tiles * col_tiles * (BN == 256 ? 2 : 1);
     if (grid > 0x7fffffffLL) {
         return hipErrorInvalidValue;
     }
-    if constexpr (BN == 128) {
+    if constexpr (BN == 256) {
+        // Half map tiles (the tile sums of 128 rows x 256 channels fill the
+        // LDS as 256 x 128 do); 4-step blocks keep the weight ring in the
+        // register budget.
+        if (epi.mode == kEpiNorm || UPB != 1 || ci % 128 != 0) return hipErrorInvalidValue;
+        k_conv_mfma_wreg<DT, 256, 2, 1, 4, kMapTile / 2><<<(unsigned) grid, 512, 0, s>>>(
+            (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n, ci,
+            co, col_tiles, epi);
+    } else if constexpr (BN == 128) {
         // Weights in registers; blocks of 8 steps when a unit is a whole
         // number of them (Ci % 256 == 0), else 4.
         if (UPB == 1 && ci % 256 == 0) {
-            k_conv_mfma_wreg<DT, BN, 2, UPB, UPB == 1 ? 8 : 4><<<(unsigned) grid, 512, 0, s>>>(
-                (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co,
-                col_tiles, epi);
+            k_conv_mfma_wreg<DT, BN, 2, UPB, UPB == 1 ? 8 : 4, kMapTile><<<(unsigned) grid, 512, 0, s>>>(
+                (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n,
+                ci, co, col_tiles, epi);
         } else {
-            k_conv_mfma_wreg<DT, BN, 2, UPB, 4><<<(unsigned) grid, 512, 0, s>>>(
-                (const T *) x, pair_src, pair_dst, tile_off, tile_counts, (const T *) w16, bias, (T *) y, n, ci, co,
-                col_tiles, epi);
+            k_conv_mfma_wreg<DT, BN, 2, UPB, 4, kMapTile><<<(unsigned) grid, 512, 0, s>>>(
+                (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n,
+                ci, co, col_tiles, epi);
         }
     } else {
         if (epi.mode != kEpiNone) return hipErrorInvalidValue;  // 64-channel blocks: plain epilogue only
@@ -1332,15 +1377,16 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32
 
 template <int DT>
 hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
-                            const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
-                            const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
+                            const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
+                            const void * w16, const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
                             const ConvEpilogue & epi) {
     const bool wide = co % 128 == 0;
     const bool pair = ci == 64;  // two 2-step units per 4-step block
-#define TSH_STREAM(BNV, UV)                                                                                       \
-    launch_stream_t<DT, BNV, 4, TSH_STREAM_WAVES, TSH_STREAM_ROW_GROUPS, UV>(x, pair_src, pair_dst, tile_off,      \
-                                                                           tile_counts, w16, bias, y, n, ci, co, s, \
-                                                                           epi)
+#define TSH_STREAM(BNV, UV)                                                                                      \
+    launch_stream_t<DT, BNV, 4, TSH_STREAM_WAVES, TSH_STREAM_ROW_GROUPS, UV>(x, pair_src, pair_dst, tile_off,     \
+                                                                           tile_counts, mask, w16, bias, y, n, ci, \
+                                                                           co, s, epi)
+    if (conv_wide_supported(ci, co) && epi.mode != kEpiNorm) return TSH_STREAM(256, 1);
     if (wide) return pair ? TSH_STREAM(128, 2) : TSH_STREAM(128, 1);
     if (co == 16) return pair ? TSH_STREAM(16, 2) : TSH_STREAM(16, 1);
     if (co == 32) return pair ? TSH_STREAM(32, 2) : TSH_STREAM(32, 1);
@@ -1368,17 +1414,18 @@ hipError_t launch_conv_os(int dtype, const void * x, const int32_t * pair_src, c
 }
 
 hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const int32_t * pair_dst,
-                                   const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
-                                   const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
-                                   const ConvEpilogue & epi) {
+                                   const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
+                                   const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
+                                   hipStream_t s, const ConvEpilogue & epi) {
     if (!conv_stream_supported(dtype, ci, co) || (epi.mode == kEpiNorm && co != 128) ||
         (epi.mode != kEpiNone && co % 128 != 0)) {
         return hipErrorInvalidValue;
     }
     if (dtype == kBF16) {
-        return launch_stream_dt<kBF16>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s, epi);
+        return launch_stream_dt<kBF16>(x, pair_src, pair_dst, tile_off, tile_counts, mask, w16, bias, y, n, ci, co, s,
+                                       epi);
     }
-    return launch_stream_dt<kF16>(x, pair_src, pair_dst, tile_off, tile_counts, w16, bias, y, n, ci, co, s, epi);
+    return launch_stream_dt<kF16>(x, pair_src, pair_dst, tile_off, tile_counts, mask, w16, bias, y, n, ci, co, s, epi);
 }
 
 }  // namespace tsh

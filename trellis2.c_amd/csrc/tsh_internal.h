@@ -215,16 +215,19 @@ enum { kEpiNone = 0, kEpiNorm = 1, kEpiAdd = 2 };
 
 // Streamed compacted schedule over the tile-major pair lists (needs ci == 64 or ci % 128 == 0).
 // Its weights use the grouped packing: [27][ci/8][co][8] whose packed column
-// b*16g + nt*16 + l holds channel b*16g + l*g + nt, g = conv_stream_group(co).
-int conv_stream_group(int co);
+// b*16g + nt*16 + l holds channel b*16g + l*g + nt, g = conv_stream_group(ci, co).
+// Co % 256 == 0 with Ci % 128 == 0 runs 256-channel blocks over half map
+// tiles (conv_wide_supported), which need the row masks.
+bool conv_wide_supported(int ci, int co);
+int conv_stream_group(int ci, int co);
 bool conv_stream_supported(int dtype, int ci, int co);
 hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const int32_t * pair_dst,
-                                   const int32_t * tile_off, const int32_t * tile_counts, const void * w16,
-                                   const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
-                                   const ConvEpilogue & epi = ConvEpilogue());
+                                   const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
+                                   const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
+                                   hipStream_t s, const ConvEpilogue & epi = ConvEpilogue());
 
 // Output-stationary MFMA conv for Ci = Co = 64 over the tile-major pair lists
-// and the row masks (weights in the grouped packing of conv_stream_group(64)).
+// and the row masks (weights in the grouped packing of conv_stream_group(64, 64)).
 bool conv_os_supported(int dtype, int ci, int co);
 hipError_t launch_conv_os(int dtype, const void * x, const int32_t * pair_src, const int32_t * tile_off,
                           const uint32_t * mask, const void * w16, const float * bias, void * y, int64_t n, int ci,
