@@ -452,6 +452,8 @@ def conv_schedule(dtype, ci, co, algo):
     mfma = dtype != sh.F32 and ci % 32 == 0 and co % 64 == 0
     if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and ci == 64 and co == 64:
         return "os64"  # output-stationary kernel over the compact lists (no fused epilogue)
+    if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and co % 256 == 0 and ci % 128 == 0:
+        return "compact256"  # 256-channel blocks over half map tiles
     if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and (ci % 128 == 0 or ci == 64):
         return "compact"
     if algo in (sh.CONV_AUTO, sh.CONV_COMPACT, sh.CONV_MASKED) and mfma:
