@@ -661,6 +661,12 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
 // wavefront: 4 row blocks x 32 channels) balances the two.  Blocks of DEPTH =
 // 8 steps (when a unit is a whole number of them) give the gathers six steps
 // between fetch and use.
+// With Co % 256 == 0 a block covers 256 channels over half a map tile (TMR =
+// 128 rows; the 128 x 256 tile sums take the LDS that 256 x 128 take): each
+// offset's list is split where its destinations leave the first 128 rows, a
+// wavefront holds 64 rows x 64 channels, and every barrier, fragment read and
+// gather serves twice the MFMAs.  A row's sums are formed in the same order
+// either way, so the two layouts give bit-identical outputs.
 // ---------------------------------------------------------------------------
 
 // Sum over the 16 lanes of a DPP row, left in every lane of the row:
