@@ -665,8 +665,10 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
 // 128 rows; the 128 x 256 tile sums take the LDS that 256 x 128 take): each
 // offset's list is split where its destinations leave the first 128 rows, a
 // wavefront holds 64 rows x 64 channels, and every barrier, fragment read and
-// gather serves twice the MFMAs.  A row's sums are formed in the same order
-// either way, so the two layouts give bit-identical outputs.
+// gather serves twice the MFMAs.  With 4-step units (Ci % 256 != 0) a block
+// of 4 wavefronts covers half a tile with 64-pair units, so that two blocks
+// share a CU.  A row's sums are formed in the same order in every layout, so
+// all of them give bit-identical outputs.
 // ---------------------------------------------------------------------------
 
 // Sum over the 16 lanes of a DPP row, left in every lane of the row:
@@ -679,8 +681,8 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-template <int DT, int BN, int RG, int UPB, int DEPTH, int TMR>
-__global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,
+template <int DT, int BN, int RG, int UPB, int DEPTH, int TMR, int NW>
+__global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,
                                                         const int32_t * __restrict__ pair_src,
                                                         const int32_t * __restrict__ pair_dst,
                                                         const int32_t * __restrict__ tile_off,
@@ -692,7 +694,7 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
                                                         int co, int64_t n_col_tiles, ConvEpilogue epi) {
     using T = typename Store<DT>::T;
     using V = typename Mfma<DT>::V;
-    constexpr int NW = 8;            // wavefronts
+    // NW wavefronts; a unit holds one 16-row block per wavefront.
     constexpr int NTHR = 64 * NW;
     constexpr int TM = TMR;          // rows per block: a kernel-map tile, or half of one
     constexpr int HALVES = kMapTile / TM;
@@ -701,8 +703,8 @@ __global__ void __launch_bounds__(512) k_conv_mfma_wreg(const typename Store<DT>
     constexpr int CG = NW / RG;      // channel groups
     constexpr int WN = BN / CG;      // channels per wavefront
     constexpr int NT = WN / 16;      // MFMA column tiles per wavefront
-    constexpr int QB = 8 / RG;       // row blocks per wavefront per unit
-    constexpr int PASS = 128;        // pairs per unit
+    constexpr int PASS = 16 * NW;    // pairs per unit
+    constexpr int QB = NW / RG;      // row blocks per wavefront per unit
     constexpr int MAX_UNITS = 27 * (TM / PASS);
     constexpr int QF = QB < 2 ? QB : 2;  // row blocks per flush batch
     constexpr int RING = UPB == 1 ? 4 : 8;
@@ -1357,18 +1359,29 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32
         // LDS as 256 x 128 do); 4-step blocks keep the weight ring in the
         // register budget.
         if (epi.mode == kEpiNorm || UPB != 1 || ci % 128 != 0) return hipErrorInvalidValue;
-        k_conv_mfma_wreg<DT, 256, 2, 1, 4, kMapTile / 2><<<(unsigned) grid, 512, 0, s>>>(
+        k_conv_mfma_wreg<DT, 256, 2, 1, 4, kMapTile / 2, 8><<<(unsigned) grid, 512, 0, s>>>(
             (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n, ci,
             co, col_tiles, epi);
     } else if constexpr (BN == 128) {
         // Weights in registers; blocks of 8 steps when a unit is a whole
         // number of them (Ci % 256 == 0), else 4.
-        if (UPB == 1 && ci % 256 == 0) {
-            k_conv_mfma_wreg<DT, BN, 2, UPB, UPB == 1 ? 8 : 4, kMapTile><<<(unsigned) grid, 512, 0, s>>>(
+        if (UPB == 1 && ci % 256 != 0) {
+            // 4-step units (Ci = 128, 384, ...): half map tiles, 64-pair
+            // units and 4 wavefronts, so that two blocks (81 KB of LDS each)
+            // share a CU and one's barriers overlap the other's MFMAs
+            // (config 2: 0.636 -> 0.602 ms; 8-step units measured 1.5 %
+            // slower this way and keep whole tiles).
+            const int64_t hgrid = tiles * col_tiles * 2;
+            if (hgrid > 0x7fffffffLL) return hipErrorInvalidValue;
+            k_conv_mfma_wreg<DT, BN, 1, 1, 4, kMapTile / 2, 4><<<(unsigned) hgrid, 256, 0, s>>>(
+                (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n, ci,
+                co, col_tiles, epi);
+        } else if (UPB == 1) {
+            k_conv_mfma_wreg<DT, BN, 2, UPB, UPB == 1 ? 8 : 4, kMapTile, 8><<<(unsigned) grid, 512, 0, s>>>(
                 (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n,
                 ci, co, col_tiles, epi);
         } else {
-            k_conv_mfma_wreg<DT, BN, 2, UPB, 4, kMapTile><<<(unsigned) grid, 512, 0, s>>>(
+            k_conv_mfma_wreg<DT, BN, 2, UPB, 4, kMapTile, 8><<<(unsigned) grid, 512, 0, s>>>(
                 (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n,
                 ci, co, col_tiles, epi);
         }
