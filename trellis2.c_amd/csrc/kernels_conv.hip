@@ -40,9 +40,17 @@ namespace tsh {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Generic VALU kernel: 32 rows x 64 channels per 256-lane block.
+// Generic VALU kernel: 16 TM rows x 64 channels per 256-lane block, each
+// lane TM rows x 4 channels (TM = 1 for small row counts, for more blocks).  Every output is formed in the reference's order:
+// bias, then per offset k (rows with a neighbour at k only) a partial sum
+// over the input channels in ascending order, mul and add rounded
+// separately, added to the running sum.  The block's 32 x 27 neighbour rows
+// are staged once; offsets no row of the block has are skipped.  The (k,
+// 32-channel chunk) tiles run through a double-buffered LDS stage, the next
+// tile's gathers loaded into registers while the current one is multiplied,
+// one barrier per tile.
 // ---------------------------------------------------------------------------
-template <int DT>
+template <int DT, int TM>
 __global__ void __launch_bounds__(256) k_conv_generic(const typename Store<DT>::T * __restrict__ x,
                                                       const int32_t * __restrict__ nbr,
                                                       const float * __restrict__ w32,
@@ -50,88 +58,127 @@ __global__ void __launch_bounds__(256) k_conv_generic(const typename Store<DT>::
                                                       typename Store<DT>::T * __restrict__ y, int64_t n, int ci,
                                                       int co) {
 #pragma clang fp contract(off)
-    constexpr int BM = 32, BN = 64, BK = 32;
-    __shared__ float s_a[BM][BK + 1];
-    __shared__ float s_b[BK][BN];
-    __shared__ int32_t s_src[BM];
+    constexpr int BM = 16 * TM, BN = 64, BK = 32;
+    constexpr int AQ = BM * BK / 256;  // A elements per lane and tile
+    __shared__ float s_a[2][BM][BK + 1];
+    __shared__ __attribute__((aligned(16))) float s_b[2][BK][BN];
+    __shared__ int32_t s_nbr[BM * 27];
+    __shared__ int32_t s_klist[27];
+    __shared__ int32_t s_nk;
     const int t = threadIdx.x;
     const int tx = t & 15, ty = t >> 4;
     const int64_t row0 = (int64_t) blockIdx.x * BM;
     const int col0 = blockIdx.y * BN;
-    float acc[2][4];
-    float part[2][4];
+    const int rows = (int) ((n - row0) < BM ? (n - row0) : BM);
+    // The block's neighbour rows: rows * 27 consecutive entries.
+    for (int e = t; e < BM * 27; e += 256) s_nbr[e] = e < rows * 27 ? nbr[row0 * 27 + e] : -1;
+    __syncthreads();
+    if (t < 64) {
+        // Offsets some row of the block has, in ascending order (a ballot
+        // per offset, then a prefix count).
+        const int k = t;
+        bool has = false;
+        if (k < 27) {
+            for (int r = 0; r < BM; ++r) has = has || s_nbr[r * 27 + k] >= 0;
+        }
+        const uint64_t bal = __ballot(has);
+        if (has) s_klist[__popcll(bal & ((1ull << t) - 1ull))] = k;
+        if (t == 0) s_nk = __popcll(bal);
+    }
+    __syncthreads();
+    const int nk = s_nk;
+    const int nchunk = (ci + BK - 1) / BK;
+    const int tiles = nk * nchunk;
+
+    float acc[TM][4];
+    float part[TM][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int col = col0 + tx * 4 + j;
         const float b = (bias != nullptr && col < co) ? bias[col] : 0.0f;
-        acc[0][j] = b;
-        acc[1][j] = b;
-    }
-    for (int k = 0; k < 27; ++k) {
-        if (t < BM) {
-            const int64_t r = row0 + t;
-            s_src[t] = r < n ? nbr[r * 27 + k] : -1;
-        }
-        __syncthreads();
-        const bool any = __syncthreads_or(t < BM && s_src[t] >= 0);
-        if (!any) {
-            continue;
-        }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) part[i][j] = 0.0f;
-        for (int c0 = 0; c0 < ci; c0 += BK) {
-            // A: 32 rows x 32 channels, 4 per lane.
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int e = t + q * 256;
-                const int r = e >> 5, c = e & 31;
-                const int32_t src = s_src[r];
-                float v = 0.0f;
-                if (src >= 0 && c0 + c < ci) {
-                    v = Store<DT>::ld(x, (int64_t) src * ci + c0 + c);
-                }
-                s_a[r][c] = v;
-            }
-            // B: 32 channels x 64 outputs, 8 per lane.
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int e = t + q * 256;
-                const int c = e >> 6, o = e & 63;
-                float v = 0.0f;
-                if (c0 + c < ci && col0 + o < co) {
-                    v = w32[((int64_t) k * ci + c0 + c) * co + col0 + o];
-                }
-                s_b[c][o] = v;
-            }
-            __syncthreads();
-            const int kmax = (ci - c0) < BK ? (ci - c0) : BK;
-            for (int c = 0; c < kmax; ++c) {
-                const float a0 = s_a[ty * 2][c], a1 = s_a[ty * 2 + 1][c];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float b = s_b[c][tx * 4 + j];
-                    part[0][j] = part[0][j] + a0 * b;
-                    part[1][j] = part[1][j] + a1 * b;
-                }
-            }
-            __syncthreads();
-        }
-        // Rows without a neighbour at k keep their sum untouched (the
-        // reference skips the offset, it does not add a zero).
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            if (s_src[ty * 2 + i] >= 0) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = acc[i][j] + part[i][j];
-            }
-        }
-        __syncthreads();
+        for (int i = 0; i < TM; ++i) acc[i][j] = b;
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int64_t r = row0 + ty * 2 + i;
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) part[i][j] = 0.0f;
+
+    // Tile it = (k = s_klist[it / nchunk], c0 = (it % nchunk) * BK).
+    float ra[AQ], rb[8];
+    auto fetch = [&](int it) {
+        const int k = s_klist[it / nchunk];
+        const int c0 = (it % nchunk) * BK;
+#pragma unroll
+        for (int q = 0; q < AQ; ++q) {
+            const int e = t + q * 256;
+            const int r = e >> 5, c = e & 31;
+            const int32_t src = s_nbr[r * 27 + k];
+            ra[q] = (src >= 0 && c0 + c < ci) ? Store<DT>::ld(x, (int64_t) src * ci + c0 + c) : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int e = t + q * 256;
+            const int c = e >> 6, o = e & 63;
+            rb[q] = (c0 + c < ci && col0 + o < co) ? w32[((int64_t) k * ci + c0 + c) * co + col0 + o] : 0.0f;
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < AQ; ++q) {
+            const int e = t + q * 256;
+            s_a[buf][e >> 5][e & 31] = ra[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int e = t + q * 256;
+            s_b[buf][e >> 6][e & 63] = rb[q];
+        }
+    };
+    if (tiles > 0) {
+        fetch(0);
+        stage(0);
+    }
+    __syncthreads();
+    for (int it = 0; it < tiles; ++it) {
+        const int buf = it & 1;
+        if (it + 1 < tiles) fetch(it + 1);
+        const int k = s_klist[it / nchunk];
+        const int c0 = (it % nchunk) * BK;
+        const int kmax = (ci - c0) < BK ? (ci - c0) : BK;
+        for (int c = 0; c < kmax; ++c) {
+            float a[TM];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) a[i] = s_a[buf][ty * TM + i][c];
+            const float4 b = *(const float4 *) &s_b[buf][c][tx * 4];
+            const float bb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < TM; ++i) part[i][j] = part[i][j] + a[i] * bb[j];
+        }
+        if (it % nchunk == nchunk - 1) {
+            // Offset k done: rows with a neighbour at k add their partial sum
+            // (the reference skips the offset for the others, it does not add
+            // a zero).
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                if (s_nbr[(ty * TM + i) * 27 + k] >= 0) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = acc[i][j] + part[i][j];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) part[i][j] = 0.0f;
+            }
+        }
+        // The other buffer was last read by the previous tile, before the
+        // previous barrier.
+        if (it + 1 < tiles) stage(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int64_t r = row0 + ty * TM + i;
         if (r >= n) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1263,22 +1310,29 @@ __global__ void __launch_bounds__(256, 2) k_conv_os64(const typename Store<DT>::
 
 hipError_t launch_conv_generic(int dtype, const void * x, const int32_t * nbr, const float * w32, const float * bias,
                                void * y, int64_t n, int ci, int co, hipStream_t s) {
-    const dim3 grid((unsigned) ((n + 31) / 32), (unsigned) ((co + 63) / 64));
+    // Two rows per lane, or one (twice the blocks) when the whole conv is
+    // fewer than 1024 tiles of 32 rows x 32 input channels x 64 outputs: the
+    // GPU then runs short of blocks (config 1, 64 -> 64: 0.192 -> 0.169 ms;
+    // larger convs measured slower with one row per lane).
+    const int64_t tiles32 = (n + 31) / 32 * ((co + 63) / 64) * ((ci + 31) / 32);
+    const int tm = tiles32 < 1024 ? 1 : 2;
+    const dim3 grid((unsigned) ((n + 16 * tm - 1) / (16 * tm)), (unsigned) ((co + 63) / 64));
+#define TSH_GENERIC(DTV, TYPE, TMV)                                                                           \
+    k_conv_generic<DTV, TMV><<<grid, 256, 0, s>>>((const TYPE *) x, nbr, w32, bias, (TYPE *) y, n, ci, co)
     switch (dtype) {
         case kF32:
-            k_conv_generic<kF32><<<grid, 256, 0, s>>>((const float *) x, nbr, w32, bias, (float *) y, n, ci, co);
+            if (tm == 2) TSH_GENERIC(kF32, float, 2); else TSH_GENERIC(kF32, float, 1);
             break;
         case kF16:
-            k_conv_generic<kF16><<<grid, 256, 0, s>>>((const _Float16 *) x, nbr, w32, bias, (_Float16 *) y, n, ci,
-                                                      co);
+            if (tm == 2) TSH_GENERIC(kF16, _Float16, 2); else TSH_GENERIC(kF16, _Float16, 1);
             break;
         case kBF16:
-            k_conv_generic<kBF16><<<grid, 256, 0, s>>>((const uint16_t *) x, nbr, w32, bias, (uint16_t *) y, n, ci,
-                                                       co);
+            if (tm == 2) TSH_GENERIC(kBF16, uint16_t, 2); else TSH_GENERIC(kBF16, uint16_t, 1);
             break;
         default:
             return hipErrorInvalidValue;
     }
+#undef TSH_GENERIC
     return hipGetLastError();
 }
 
