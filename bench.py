@@ -454,6 +454,8 @@ def conv_schedule(dtype, ci, co, algo):
         return "os64"  # output-stationary kernel over the compact lists (no fused epilogue)
     if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and co % 256 == 0 and ci % 128 == 0:
         return "compact256"  # 256-channel blocks over half map tiles
+    if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and co % 128 == 0 and ci % 128 == 0 and ci % 256 != 0:
+        return "compact_half"  # 4-step units: half map tiles, 4 wavefronts, two blocks per CU
     if algo in (sh.CONV_AUTO, sh.CONV_COMPACT) and mfma and (ci % 128 == 0 or ci == 64):
         return "compact"
     if algo in (sh.CONV_AUTO, sh.CONV_COMPACT, sh.CONV_MASKED) and mfma:
