@@ -104,6 +104,50 @@ def test_kernel_map_configs_bitexact(be32, cfg):
     rb.free()
 
 
+def random_coord_set(seed):
+    """Seeded random voxel sets of varied shape: uniform boxes from dense to
+    sparse, Gaussian clusters, sets straddling the 16-bit wrap of every axis,
+    many batches with large batch ids, and repeated coordinates."""
+    rng = np.random.default_rng(1000 + seed)
+    kind = seed % 5
+    n = int(rng.integers(1, 60000))
+    if kind == 0:  # uniform box, density from ~1 to ~0.001
+        side = int(max(2, round((n / rng.uniform(0.001, 1.0)) ** (1 / 3))))
+        c = np.stack([np.zeros(n), *(rng.integers(0, side, n) for _ in range(3))], 1)
+    elif kind == 1:  # clusters
+        centres = rng.integers(0, 3000, (int(rng.integers(1, 40)), 3))
+        pick = rng.integers(0, centres.shape[0], n)
+        pts = centres[pick] + rng.normal(0, rng.uniform(1, 12), (n, 3))
+        c = np.concatenate([rng.integers(0, 3, (n, 1)), np.rint(pts)], 1)
+    elif kind == 2:  # around the 16-bit wrap on every axis
+        c = np.stack([rng.integers(0, 2, n), *(rng.integers(-9, 9, n) for _ in range(3))], 1)
+        c[:, 1:][c[:, 1:] < 0] += 65536
+    elif kind == 3:  # many batches, large batch ids
+        c = np.stack([rng.integers(60000, 65536, n), *(rng.integers(0, 20, n) for _ in range(3))], 1)
+    else:  # repeated rows among a small set
+        base = np.stack([rng.integers(0, 4, n), *(rng.integers(0, 24, n) for _ in range(3))], 1)
+        c = base[rng.integers(0, base.shape[0], n)]
+    return np.ascontiguousarray(c.astype(np.int32))
+
+
+@pytest.mark.parametrize("seed", list(range(15)))
+def test_kernel_map_random_sets_bitexact(be32, bebf, seed):
+    """Neighbour table and pair lists equal the oracle's on seeded random
+    sets, on an fp32 backend (the neighbour table) and a bf16 one (the
+    compact lists the MFMA convs read)."""
+    c = random_coord_set(seed)
+    say(f"kernel map random set seed={seed} kind={seed % 5}: n={c.shape[0]}")
+    exp = orc.Rulebook(c).neighbors()
+    ec, es, ed = orc.pairs(exp)
+    rb = be32.build_rulebook(c)
+    assert np.array_equal(be32.neighbors(rb), exp)
+    rb.free()
+    rb = bebf.build_rulebook(c)
+    counts, src, dst = bebf.pairs(rb)
+    assert np.array_equal(counts, ec) and np.array_equal(src, es) and np.array_equal(dst, ed)
+    rb.free()
+
+
 def test_rulebook_rejects_bad_arguments(be32):
     with pytest.raises(sh.HipError) as e:
         be32.build_rulebook(np.zeros((0, 4), np.int32))
