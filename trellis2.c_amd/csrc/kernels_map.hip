@@ -190,8 +190,12 @@ __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict
 }
 
 // Kernel map in one pass.  One block = one 256-row tile:
-//  1. the tile's [256][27] neighbour rows are found and staged in LDS (a few
-//     brick probes per voxel plus 27 pool reads), with the row masks;
+//  1. each row's 27 neighbour rows are found (a few brick probes per voxel
+//     plus 9 z-row pool reads) and kept in its lane's registers, with the row
+//     masks; only a launch that also writes the neighbour table (NBR) stages
+//     the tile's [256][27] rows in LDS, for a coalesced copy.  Without that
+//     28 KB of LDS per block the kernel runs 8 wavefronts per SIMD instead
+//     of 5, which is what its dependent probe and pool loads need;
 //  2. per-offset pair counts of the tile (wavefront ballots);
 //  3. the neighbour table (16-byte vectorised copy of the LDS block), the
 //     per-(tile, offset) counts and list starts, and the pair lists,
@@ -204,6 +208,7 @@ __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict
 // duplicate of its coordinates), so the centre list holds the tile's rows in
 // order, starting at the region's start: a consumer can find it without the
 // tile's counts.
+template <bool NBR>
 __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ coords, int64_t n,
                                                       const uint64_t * __restrict__ bkeys,
                                                       const int32_t * __restrict__ bidx, uint64_t hmask,
@@ -213,7 +218,7 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
                                                       int32_t * __restrict__ tile_off,
                                                       int32_t * __restrict__ pair_src,
                                                       int32_t * __restrict__ pair_dst, int32_t * __restrict__ counters) {
-    __shared__ __attribute__((aligned(16))) int32_t s_nbr[kBlock * 27];
+    __shared__ __attribute__((aligned(16))) int32_t s_nbr[NBR ? kBlock * 27 : 4];
     __shared__ int32_t s_wave_cnt[27][kBlock / 64];
     __shared__ int32_t s_koff[27];
     const int t = threadIdx.x;
@@ -223,6 +228,9 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
     const int64_t row0 = tile * kBlock;
     const int64_t i = row0 + t;
     uint32_t m = 0;
+    int32_t nb[27];
+#pragma unroll
+    for (int k = 0; k < 27; ++k) nb[k] = -1;
     if (i < n) {
         const int4 c = coords[i];
         const uint32_t b = (uint32_t) c.x & 0xffffu;
@@ -272,20 +280,20 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
                     const int nz = cz + kw - 1;
                     const int32_t r = nz < 0 || nz > 3 ? e : (nz == 0 ? v.x : (nz == 1 ? v.y : (nz == 2 ? v.z : v.w)));
                     const int k = kd * 9 + kh * 3 + kw;
-                    s_nbr[t * 27 + k] = r;
+                    nb[k] = r;
+                    if constexpr (NBR) s_nbr[t * 27 + k] = r;
                     m |= (r >= 0 ? 1u : 0u) << k;
                 }
             }
         }
         mask_out[i] = m;
     }
-    // Rank of this row among the tile's rows with a neighbour at k, per wavefront.
+    // Rows of this wavefront with a neighbour at k (the ranks are recomputed
+    // from the same ballots when the pairs are written).
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int32_t rank[27];
 #pragma unroll
     for (int k = 0; k < 27; ++k) {
         const uint64_t bal = __ballot((m >> k) & 1u);
-        rank[k] = __popcll(bal & lt);
         if (lane == 0) s_wave_cnt[k][wave] = __popcll(bal);
     }
     __syncthreads();
@@ -310,26 +318,29 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
     __syncthreads();
     const int64_t base = tile * kBlock * 27;
     if (t < 27) tile_off[tile * 27 + t] = (int32_t) (base + s_koff[t]);
-    // Coalesced copy of the tile's neighbour table (when the caller wants it).
-    const int64_t rows = (n - row0) < kBlock ? (n - row0) : kBlock;
-    const int64_t words = nbr != nullptr ? rows * 27 : 0;
-    int32_t * dst = nbr != nullptr ? nbr + row0 * 27 : nullptr;
-    if ((words & 3) == 0) {
-        for (int64_t w = (int64_t) t * 4; w < words; w += kBlock * 4) {
-            *(int4 *) (dst + w) = *(const int4 *) (s_nbr + w);
-        }
-    } else {
-        for (int64_t w = t; w < words; w += kBlock) {
-            dst[w] = s_nbr[w];
+    if constexpr (NBR) {
+        // Coalesced copy of the tile's neighbour table.
+        const int64_t rows = (n - row0) < kBlock ? (n - row0) : kBlock;
+        const int64_t words = rows * 27;
+        int32_t * dst = nbr + row0 * 27;
+        if ((words & 3) == 0) {
+            for (int64_t w = (int64_t) t * 4; w < words; w += kBlock * 4) {
+                *(int4 *) (dst + w) = *(const int4 *) (s_nbr + w);
+            }
+        } else {
+            for (int64_t w = t; w < words; w += kBlock) {
+                dst[w] = s_nbr[w];
+            }
         }
     }
-    if (i >= n || m == 0) return;
+    // Every lane takes part in the ballots; rows past n have no neighbours.
 #pragma unroll
     for (int k = 0; k < 27; ++k) {
+        const uint64_t bal = __ballot((m >> k) & 1u);
         if ((m >> k) & 1u) {
-            int64_t pos = base + s_koff[k] + rank[k];
+            int64_t pos = base + s_koff[k] + __popcll(bal & lt);
             for (int w = 0; w < wave; ++w) pos += s_wave_cnt[k][w];
-            pair_src[pos] = s_nbr[t * 27 + k];
+            pair_src[pos] = nb[k];
             pair_dst[pos] = (int32_t) i;
         }
     }
@@ -381,9 +392,15 @@ hipError_t launch_map_tiles(const int32_t * coords, int64_t n, const uint64_t * 
                             int32_t * tile_counts, int32_t * tile_off, int32_t * pair_src, int32_t * pair_dst,
                             int32_t * counters, hipStream_t s) {
     const int64_t blocks = (n + kBlock - 1) / kBlock;
-    k_map_tiles<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx, (uint64_t) (slots - 1),
-                                                     pool, nbr, mask, tile_counts, tile_off, pair_src, pair_dst,
-                                                     counters);
+    if (nbr != nullptr) {
+        k_map_tiles<true><<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
+                                                               (uint64_t) (slots - 1), pool, nbr, mask, tile_counts,
+                                                               tile_off, pair_src, pair_dst, counters);
+    } else {
+        k_map_tiles<false><<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
+                                                                (uint64_t) (slots - 1), pool, nbr, mask, tile_counts,
+                                                                tile_off, pair_src, pair_dst, counters);
+    }
     return hipGetLastError();
 }
 
