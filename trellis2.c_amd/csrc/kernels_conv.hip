@@ -146,7 +146,29 @@ __global__ void __launch_bounds__(256) k_conv_generic(const typename Store<DT>::
         const int k = s_klist[it / nchunk];
         const int c0 = (it % nchunk) * BK;
         const int kmax = (ci - c0) < BK ? (ci - c0) : BK;
-        for (int c = 0; c < kmax; ++c) {
+        // Channels in groups of 4: the group's LDS reads are all issued
+        // before its multiplies, so one LDS latency covers four channels;
+        // the sums still run channel by channel.
+        const int kmax4 = kmax & ~3;
+        for (int c = 0; c < kmax4; c += 4) {
+            float a[4][TM];
+            float4 b[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) a[u][i] = s_a[buf][ty * TM + i][c + u];
+                b[u] = *(const float4 *) &s_b[buf][c + u][tx * 4];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float bb[4] = {b[u].x, b[u].y, b[u].z, b[u].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) part[i][j] = part[i][j] + a[u][i] * bb[j];
+            }
+        }
+        for (int c = kmax4; c < kmax; ++c) {
             float a[TM];
 #pragma unroll
             for (int i = 0; i < TM; ++i) a[i] = s_a[buf][ty * TM + i][c];
