@@ -90,6 +90,10 @@ struct Backend {
     // (grown on demand; released by trim(FREE_BUFFERS) and destroy).
     void * pinned = nullptr;
     size_t pinned_bytes = 0;
+    // Pinned words for small device-to-host reads (child and face counts),
+    // and the event the host spins on for them (allocated at creation).
+    int32_t * host_words = nullptr;
+    hipEvent_t words_ready = nullptr;
     // Timing.
     bool profiling = false;
     std::vector<StageMark> pending;
@@ -260,6 +264,37 @@ trellis_status pinned_reserve(Backend * be, size_t bytes) {
     be->pinned = p;
     be->pinned_bytes = want;
     return TRELLIS_STATUS_OK;
+}
+
+// Reads up to kHostWords int32 values from device memory (one or two source
+// ranges) into host variables, through the backend's pinned words: the
+// copies write host memory directly, and the host spins on an event, so it
+// resumes within microseconds of the copy, where a blocking stream
+// synchronisation and a pageable destination cost tens of microseconds.
+// The queue is drained up to the copy, as hipStreamSynchronize would.
+constexpr int kHostWords = 16;
+hipError_t read_words(Backend * be, hipStream_t s, int32_t * dst0, const void * src0, int count0,
+                      int32_t * dst1 = nullptr, const void * src1 = nullptr, int count1 = 0) {
+    if (be->host_words == nullptr || be->words_ready == nullptr || count0 + count1 > kHostWords) {
+        hipError_t err = hipMemcpyAsync(dst0, src0, (size_t) count0 * 4, hipMemcpyDeviceToHost, s);
+        if (err == hipSuccess && count1 > 0) err = hipMemcpyAsync(dst1, src1, (size_t) count1 * 4, hipMemcpyDeviceToHost, s);
+        if (err == hipSuccess) err = hipStreamSynchronize(s);
+        return err;
+    }
+    hipError_t err = hipMemcpyAsync(be->host_words, src0, (size_t) count0 * 4, hipMemcpyDeviceToHost, s);
+    if (err == hipSuccess && count1 > 0) {
+        err = hipMemcpyAsync(be->host_words + count0, src1, (size_t) count1 * 4, hipMemcpyDeviceToHost, s);
+    }
+    if (err == hipSuccess) err = hipEventRecord(be->words_ready, s);
+    if (err != hipSuccess) return err;
+    while ((err = hipEventQuery(be->words_ready)) == hipErrorNotReady) {
+    }
+    (void) hipGetLastError();  // the not-ready polls are not errors
+    if (err != hipSuccess) return err;
+    const volatile int32_t * w = be->host_words;
+    for (int i = 0; i < count0; ++i) dst0[i] = w[i];
+    for (int i = 0; i < count1; ++i) dst1[i] = w[count0 + i];
+    return hipSuccess;
 }
 
 // ---- stage timing -----------------------------------------------------------
@@ -1097,8 +1132,7 @@ trellis_status c2s_build(Backend * be, const int32_t * coords_dev, const trellis
                                         (int32_t *) total.ptr, tmp.ptr, s);
         }
         stage_end(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
-        if (err == hipSuccess) err = hipMemcpyAsync(&m, total.ptr, 4, hipMemcpyDeviceToHost, s);
-        if (err == hipSuccess) err = hipStreamSynchronize(s);
+        if (err == hipSuccess) err = read_words(be, s, &m, total.ptr, 1);
         st = hip_status(be, err, "c2s count/scan");
     }
     if (st == TRELLIS_STATUS_OK && m <= 0) {
@@ -1416,9 +1450,7 @@ trellis_status s2c_build(Backend * be, const int32_t * fine_coords_host, const i
                                         tmp.ptr, s);
         }
         stage_end(be, TRELLIS_SPARSE_HIP_STAGE_SUBDIVIDE);
-        if (err == hipSuccess) err = hipMemcpyAsync(hf, flags.ptr, 4, hipMemcpyDeviceToHost, s);
-        if (err == hipSuccess) err = hipMemcpyAsync(&m, total.ptr, 4, hipMemcpyDeviceToHost, s);
-        if (err == hipSuccess) err = hipStreamSynchronize(s);
+        if (err == hipSuccess) err = read_words(be, s, hf, flags.ptr, 1, &m, total.ptr, 1);
         st = hip_status(be, err, "s2c sort");
     }
     if (st == TRELLIS_STATUS_OK && (hf[0] & 2)) {
@@ -1598,8 +1630,7 @@ trellis_status fdg_mesh_impl(trellis_sparse_backend * backend, const int32_t * c
                                         tmp.ptr, s);
         }
         stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
-        if (err == hipSuccess) err = hipMemcpyAsync(&quads, total.ptr, 4, hipMemcpyDeviceToHost, s);
-        if (err == hipSuccess) err = hipStreamSynchronize(s);
+        if (err == hipSuccess) err = read_words(be, s, &quads, total.ptr, 1);
         st = hip_status(be, err, "flex_dual_grid_mesh count");
     }
     if (st == TRELLIS_STATUS_OK && quads > 0) {
@@ -1751,6 +1782,8 @@ void op_destroy(trellis_sparse_backend * backend) {
     for (hipEvent_t e : be->user_events)
         if (e != nullptr) (void) hipEventDestroy(e);
     if (be->pinned != nullptr) (void) hipHostFree(be->pinned);
+    if (be->host_words != nullptr) (void) hipHostFree(be->host_words);
+    if (be->words_ready != nullptr) (void) hipEventDestroy(be->words_ready);
     if (be->side != nullptr) (void) hipStreamDestroy(be->side);
     (void) hipStreamDestroy(be->stream);
     delete be;
@@ -1818,6 +1851,16 @@ trellis_status trellis_sparse_hip_backend_create_ex(int device, const trellis_sp
     if (hipStreamCreateWithFlags(&be->side, hipStreamNonBlocking) != hipSuccess) {
         (void) hipGetLastError();
         be->side = nullptr;  // rulebooks are then built on the main stream
+    }
+    // Small reads fall back to pageable copies and a stream synchronisation
+    // when either of these is missing.
+    if (hipHostMalloc((void **) &be->host_words, tsh::kHostWords * 4, hipHostMallocDefault) != hipSuccess) {
+        (void) hipGetLastError();
+        be->host_words = nullptr;
+    }
+    if (hipEventCreateWithFlags(&be->words_ready, hipEventDisableTiming) != hipSuccess) {
+        (void) hipGetLastError();
+        be->words_ready = nullptr;
     }
     be->base.ops = &tsh::g_ops;
     be->base.kind = TRELLIS_SPARSE_BACKEND_HIP;
@@ -2061,8 +2104,7 @@ trellis_status trellis_sparse_hip_build_c2s_map_into(trellis_sparse_backend * ba
     hipError_t err = launch_c2s_count(be->policy.compute_dtype, logits->ptr, n, counts, s);
     if (err == hipSuccess) err = launch_scan_exclusive(counts, offsets, n, total, sums, s);
     int32_t m = 0;
-    if (err == hipSuccess) err = hipMemcpyAsync(&m, total, 4, hipMemcpyDeviceToHost, s);
-    if (err == hipSuccess) err = hipStreamSynchronize(s);
+    if (err == hipSuccess) err = read_words(be, s, &m, total, 1);
     if (err != hipSuccess) return hip_status(be, err, "build_c2s_map_into: count/scan");
     if (m <= 0) return fail(be, TRELLIS_STATUS_ERROR, "subdivide produced no children (all logits <= 0)");
     *n_out = m;
