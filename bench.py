@@ -177,10 +177,8 @@ class Block:
       (executor.c:257-554).
     In c2s and s2c the closing conv -> add runs as one trellis_sparse_hip_conv_add
     (slot "conv_add_post") unless --slots is given.
-    Slot times come from HIP events on the backend stream between slots.  A
-    rulebook built from a device map runs on the backend's second stream, so
-    its time shows up in the slot that first waits for it (the next conv),
-    and work queued between the two overlaps it.
+    Slot times come from HIP events on the backend stream between slots (every
+    slot runs on that stream, in call order).
     """
 
     def __init__(self, be, kind, slots=False):
@@ -579,9 +577,7 @@ def main():
     for _ in range(args.warmup):
         job.step()
     be.synchronize()
-    # Timed steps: the production path, without stage events (rulebooks built
-    # from device maps run on the backend's second stream, overlapping the
-    # broadcast).
+    # Timed steps: the production path, without stage events.
     t0 = time.perf_counter()
     be.event(0)
     for _ in range(args.steps):
@@ -591,8 +587,7 @@ def main():
     wall = (time.perf_counter() - t0) * 1e3
     dev_ms = be.elapsed(0, 1)
     # Stage breakdown and the conv's launch time (the roofline's denominator):
-    # a second pass of as many steps with stage events, which keep every
-    # stage on the backend stream.
+    # a second pass of as many steps with stage events around each stage.
     be.profile(True)
     be.profile_read(reset=True)
     for _ in range(args.steps):

@@ -62,10 +62,6 @@ struct Backend {
     int device = 0;
     int cus = 0;  // compute units of the device
     hipStream_t stream = nullptr;
-    // Rulebooks for device maps are built here, overlapping whatever the
-    // caller queues next on `stream` (e.g. the feature broadcast); both at
-    // the default priority.
-    hipStream_t side = nullptr;
     trellis_sparse_hip_policy policy{};
     std::string last_error;
     // Pool: size class -> free device blocks.
@@ -733,15 +729,12 @@ trellis_status op_add(trellis_sparse_backend * backend, const trellis_sparse_buf
 }
 
 // ---- rulebook -------------------------------------------------------------------
-// Orders the main stream after a side-stream build (once per rulebook).
-void rulebook_wait(Backend * be, const trellis_sparse_rulebook * r);
 trellis_status map_pass(Backend * be, trellis_sparse_rulebook * r, hipStream_t s);
 
 // The neighbour table of a rulebook built without it, written on first use.
 trellis_status rulebook_ensure_nbr(Backend * be, const trellis_sparse_rulebook * rc) {
     auto * r = const_cast<trellis_sparse_rulebook *>(rc);
     if (r->nbr.ptr != nullptr) return TRELLIS_STATUS_OK;
-    rulebook_wait(be, r);
     const trellis_status st = dev_alloc(be, (size_t) r->n * 27 * 4, &r->nbr);
     if (st != TRELLIS_STATUS_OK) return st;
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
@@ -749,16 +742,7 @@ trellis_status rulebook_ensure_nbr(Backend * be, const trellis_sparse_rulebook *
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_MAP);
     return mst;
 }
-void rulebook_wait(Backend * be, const trellis_sparse_rulebook * r) {
-    auto * w = const_cast<trellis_sparse_rulebook *>(r);
-    if (w == nullptr || w->ready == nullptr) return;
-    (void) hipStreamWaitEvent(be->stream, w->ready, 0);
-    be->spare_events.push_back(w->ready);
-    w->ready = nullptr;
-}
-
 void rulebook_release(Backend * be, trellis_sparse_rulebook * r) {
-    rulebook_wait(be, r);
     if (r == nullptr) return;
     DevMem * mems[] = {&r->coords_mem, &r->bkeys, &r->bidx, &r->pool, &r->counters, &r->nbr, &r->mask,
                        &r->tile_counts, &r->tile_off, &r->pair_src, &r->pair_dst};
@@ -893,7 +877,6 @@ trellis_status conv_impl(trellis_sparse_backend * backend, const trellis_sparse_
         epi = *fused_epi;
     }
     CallScope scope(be);
-    rulebook_wait(be, rulebook);
     int algo = be->policy.conv_algo;
     if (algo == TRELLIS_SPARSE_HIP_CONV_AUTO) {
         // The streamed compacted schedule multiplies valid pairs only; where it
@@ -1279,33 +1262,12 @@ trellis_status op_build_rulebook_for_c2s_map(trellis_sparse_backend * backend,
     CallScope scope(be);
     auto * r = new (std::nothrow) trellis_sparse_rulebook();
     if (r == nullptr) return TRELLIS_STATUS_OUT_OF_MEMORY;
-    // Built on the side stream after everything queued so far on the main
-    // stream, so that the caller's next work there (typically the feature
-    // broadcast over the same map) runs alongside; every later use of the
-    // rulebook waits for it.  With stage timing, or when duplicates must be
-    // rejected (a synchronous check), it stays on the main stream.  The map
-    // owns the coordinates and outlives the rulebook.
-    const bool side = be->side != nullptr && !be->profiling && !be->policy.reject_duplicates;
-    hipEvent_t start = side ? take_event(be) : nullptr;
-    hipEvent_t done = side ? take_event(be) : nullptr;
-    trellis_status st = TRELLIS_STATUS_OK;
-    if (side && start != nullptr && done != nullptr) {
-        hipError_t err = hipEventRecord(start, be->stream);
-        if (err == hipSuccess) err = hipStreamWaitEvent(be->side, start, 0);
-        st = hip_status(be, err, "build_rulebook_for_c2s_map: stream order");
-        if (st == TRELLIS_STATUS_OK) st = rulebook_build_device(be, (const int32_t *) map->coords.ptr, map->n, r, be->side);
-        if (st == TRELLIS_STATUS_OK) st = hip_status(be, hipEventRecord(done, be->side), "build_rulebook_for_c2s_map");
-        if (st == TRELLIS_STATUS_OK) {
-            r->ready = done;
-            done = nullptr;
-        } else {
-            (void) hipStreamSynchronize(be->side);
-        }
-    } else {
-        st = rulebook_build_device(be, (const int32_t *) map->coords.ptr, map->n, r);
-    }
-    if (start != nullptr) be->spare_events.push_back(start);
-    if (done != nullptr) be->spare_events.push_back(done);
+    // Built on the backend stream, in call order: a second stream that let
+    // the build overlap the caller's next work (the feature broadcast of
+    // config 3) made that phase longer, as the two kernels share the CUs and
+    // HBM (config-3 step 2.061 -> 2.023 ms without it).  The map owns the
+    // coordinates and outlives the rulebook.
+    const trellis_status st = rulebook_build_device(be, (const int32_t *) map->coords.ptr, map->n, r);
     if (st != TRELLIS_STATUS_OK) {
         rulebook_release(be, r);
         return st;
@@ -1695,7 +1657,6 @@ trellis_status op_trim(trellis_sparse_backend * backend, unsigned flags, size_t 
     if (flags == 0) return TRELLIS_STATUS_OK;
     Backend * be = as_backend(backend);
     CallScope scope(be);
-    if (be->side != nullptr) TSH_TRY(be, hipStreamSynchronize(be->side));
     TSH_TRY(be, hipStreamSynchronize(be->stream));
     size_t released = 0;
     if (flags & TRELLIS_SPARSE_TRIM_WEIGHTS) {
@@ -1766,7 +1727,6 @@ void op_destroy(trellis_sparse_backend * backend) {
     if (backend == nullptr) return;
     Backend * be = as_backend(backend);
     select_device(be);
-    if (be->side != nullptr) (void) hipStreamSynchronize(be->side);
     (void) hipStreamSynchronize(be->stream);
     for (auto * m : be->maps) map_release(be, m);
     be->maps.clear();
@@ -1784,7 +1744,6 @@ void op_destroy(trellis_sparse_backend * backend) {
     if (be->pinned != nullptr) (void) hipHostFree(be->pinned);
     if (be->host_words != nullptr) (void) hipHostFree(be->host_words);
     if (be->words_ready != nullptr) (void) hipEventDestroy(be->words_ready);
-    if (be->side != nullptr) (void) hipStreamDestroy(be->side);
     (void) hipStreamDestroy(be->stream);
     delete be;
 }
@@ -1848,10 +1807,6 @@ trellis_status trellis_sparse_hip_backend_create_ex(int device, const trellis_sp
         delete be;
         return TRELLIS_STATUS_CUDA_UNAVAILABLE;
     }
-    if (hipStreamCreateWithFlags(&be->side, hipStreamNonBlocking) != hipSuccess) {
-        (void) hipGetLastError();
-        be->side = nullptr;  // rulebooks are then built on the main stream
-    }
     // Small reads fall back to pageable copies and a stream synchronisation
     // when either of these is missing.
     if (hipHostMalloc((void **) &be->host_words, tsh::kHostWords * 4, hipHostMallocDefault) != hipSuccess) {
@@ -1906,10 +1861,6 @@ trellis_status trellis_sparse_hip_synchronize(trellis_sparse_backend * backend) 
     if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
     Backend * be = tsh::as_backend(backend);
     tsh::select_device(be);
-    if (be->side != nullptr) {
-        const hipError_t err = hipStreamSynchronize(be->side);
-        if (err != hipSuccess) return tsh::hip_status(be, err, "synchronize");
-    }
     return tsh::hip_status(be, hipStreamSynchronize(be->stream), "synchronize");
 }
 
@@ -1919,7 +1870,6 @@ trellis_status trellis_sparse_hip_rulebook_stats(trellis_sparse_backend * backen
     if (backend == nullptr || rulebook == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
     Backend * be = tsh::as_backend(backend);
     tsh::select_device(be);
-    tsh::rulebook_wait(be, rulebook);
     int32_t ctr[tsh::kCounterInts];
     std::vector<int32_t> cnt((size_t) rulebook->n_tiles * 27);
     hipError_t err = hipMemcpyAsync(ctr, rulebook->counters.ptr, sizeof(ctr), hipMemcpyDeviceToHost, be->stream);
@@ -1946,7 +1896,6 @@ trellis_status trellis_sparse_hip_download_neighbors(trellis_sparse_backend * ba
     }
     Backend * be = tsh::as_backend(backend);
     tsh::select_device(be);
-    tsh::rulebook_wait(be, rulebook);
     const trellis_status st = tsh::rulebook_ensure_nbr(be, rulebook);
     if (st != TRELLIS_STATUS_OK) return st;
     hipError_t err = hipMemcpyAsync(nbr_out, rulebook->nbr.ptr, (size_t) n * 27 * 4, hipMemcpyDeviceToHost, be->stream);
@@ -1960,7 +1909,6 @@ trellis_status trellis_sparse_hip_download_pairs(trellis_sparse_backend * backen
     if (backend == nullptr || rulebook == nullptr || counts_out == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
     Backend * be = tsh::as_backend(backend);
     tsh::select_device(be);
-    tsh::rulebook_wait(be, rulebook);
     // Per-offset totals are the column sums of the per-(tile, offset) counts.
     const int64_t tiles = rulebook->n_tiles;
     std::vector<int32_t> off((size_t) tiles * 27), cnt((size_t) tiles * 27);

@@ -148,9 +148,6 @@ struct trellis_sparse_rulebook {
     tsh::DevMem tile_off;    // int32  [n_tiles][27] start of (tile, k) in the pair arrays
     tsh::DevMem pair_src;    // int32  [n_tiles][kMapTile * 27]: per tile, offsets ascending, dst ascending
     tsh::DevMem pair_dst;    // int32  [n_tiles][kMapTile * 27]
-    // Built on the backend's side stream: recorded there when the build is
-    // done; the main stream waits on it before the first use.
-    hipEvent_t ready = nullptr;
 };
 
 struct trellis_sparse_c2s_device_map {
