@@ -910,7 +910,7 @@ trellis_status conv_impl(trellis_sparse_backend * backend, const trellis_sparse_
                         &w);
         if (st != TRELLIS_STATUS_OK) return st;
         stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_CONV);
-        if (algo == TRELLIS_SPARSE_HIP_CONV_COMPACT && epi.mode == kEpiNone && conv_os_supported(dt, ci, co)) {
+        if (algo == TRELLIS_SPARSE_HIP_CONV_COMPACT && epi.mode == kEpiNone && conv_os_supported(dt, ci, co, n)) {
             // Ci = Co = 64: the output-stationary kernel over the same lists.
             err = launch_conv_os(dt, feats->ptr, (const int32_t *) rulebook->pair_src.ptr,
                                  (const int32_t *) rulebook->tile_off.ptr, (const uint32_t *) rulebook->mask.ptr, w,

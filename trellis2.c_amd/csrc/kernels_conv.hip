@@ -1188,7 +1188,11 @@ __global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) k_conv_mfma_wreg(con
 // k comes from ballots of the row masks), the 16 source rows of a row block
 // are loaded coalesced (four lanes per 64-byte K step) and moved to MFMA
 // operand order with ds_bpermute; a row without a neighbour at k multiplies
-// zeros.  The offset's 8 KB of weights are shared through a double-buffered
+// zeros.  The loads are raw buffer loads over x: a missing neighbour gets an
+// offset past the buffer's end, which the hardware answers with zeros and no
+// memory request, so no branch guards a load and the compiler's memory waits
+// keep the two-offset look-ahead (a guarded load made it wait for each
+// offset's loads almost at once).  The offset's 8 KB of weights are shared through a double-buffered
 // LDS slot: one barrier per offset.  Each row's 27 sources are fetched in one
 // round trip at the start; operand loads run two offsets ahead.  No unit
 // lists, no tile sums, no flushes: the MFMA rows include the rows without a
@@ -1254,17 +1258,27 @@ __global__ void __launch_bounds__(256, 2) k_conv_os64(const typename Store<DT>::
         src[k] = ((m >> k) & 1u) ? pair_src[s_off[k] + base + __popcll(bk & lt)] : -1;
     }
     // A pieces of offset k: row block q, K step f; lane 4i + c holds 16 bytes
-    // (chunk c of the step) of row i of the block.
+    // (chunk c of the step) of row i of the block.  Byte offsets into x per
+    // row block (rows of the lane's quad), prepared one offset before their
+    // loads so that the shuffles' latency stays off the load path.
     constexpr int AHEAD = 2;  // offsets whose A loads are in flight
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc((void *) x, 0, (int) (n * CI * (int64_t) sizeof(T)), 0x00020000);
     V ra[AHEAD + 1][QB][2];
-    auto load_a = [&](V (&a)[QB][2], int32_t src) {
+    uint32_t voff[QB];
+    auto prep_a = [&](int32_t src) {
 #pragma unroll
         for (int q = 0; q < QB; ++q) {
             const int32_t sq = __shfl(src, q * 16 + (lane >> 2));
+            voff[q] = sq >= 0 ? (uint32_t) sq * (uint32_t) (CI * sizeof(T)) + (uint32_t) (lane & 3) * 16u : 0x80000000u;
+        }
+    };
+    auto load_a = [&](V (&a)[QB][2]) {
+#pragma unroll
+        for (int q = 0; q < QB; ++q)
 #pragma unroll
             for (int f = 0; f < 2; ++f)
-                a[q][f] = sq >= 0 ? *(const V *) (x + (int64_t) sq * CI + f * 32 + (lane & 3) * 8) : V{};
-        }
+                a[q][f] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(xres, voff[q] + f * 64u, 0, 0));
     };
     f32x4 acc[QB][NT];
 #pragma unroll
@@ -1273,12 +1287,20 @@ __global__ void __launch_bounds__(256, 2) k_conv_os64(const typename Store<DT>::
         for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int perm = (4 * l16 + lg) * 4;
 #pragma unroll
-    for (int k = 0; k < AHEAD; ++k) load_a(ra[k], src[k]);
+    for (int k = 0; k < AHEAD; ++k) {
+        prep_a(src[k]);
+        load_a(ra[k]);
+    }
+    prep_a(src[AHEAD]);
 #pragma unroll
     for (int k = 0; k < 27; ++k) {
         const int cur = k & 1;
         const int ar = k % (AHEAD + 1);
-        if (k + AHEAD < 27) load_a(ra[(k + AHEAD) % (AHEAD + 1)], src[k + AHEAD]);
+        if (k + AHEAD < 27) load_a(ra[(k + AHEAD) % (AHEAD + 1)]);
+        if (k + AHEAD + 1 < 27) prep_a(src[k + AHEAD + 1]);
+        // The scheduler would otherwise move the transposes of the loads just
+        // issued up to them, which makes the loads wait at once.
+        __builtin_amdgcn_sched_barrier(0);
         // Weight fragments of offset k: K step f, column tile nt.
         V bw[2][NT];
         const T * ws = &s_w[cur][0];
@@ -1490,12 +1512,17 @@ hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int3
 }
 }  // namespace
 
-bool conv_os_supported(int dtype, int ci, int co) { return (dtype == kF16 || dtype == kBF16) && ci == 64 && co == 64; }
+// The gathers address x through a buffer resource whose byte range is an
+// int32: up to 2^31 / 128 rows (16.7M voxels); beyond that the compacted
+// streamed kernel runs instead.
+bool conv_os_supported(int dtype, int ci, int co, int64_t n) {
+    return (dtype == kF16 || dtype == kBF16) && ci == 64 && co == 64 && n > 0 && n <= (int64_t) INT32_MAX / 128;
+}
 
 hipError_t launch_conv_os(int dtype, const void * x, const int32_t * pair_src, const int32_t * tile_off,
                           const uint32_t * mask, const void * w16, const float * bias, void * y, int64_t n, int ci,
                           int co, hipStream_t s) {
-    if (!conv_os_supported(dtype, ci, co) || n <= 0) return hipErrorInvalidValue;
+    if (!conv_os_supported(dtype, ci, co, n)) return hipErrorInvalidValue;
     const int64_t tiles = (n + kMapTile - 1) / kMapTile;
     if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
     if (dtype == kBF16) {

@@ -225,7 +225,7 @@ hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pa
 
 // Output-stationary MFMA conv for Ci = Co = 64 over the tile-major pair lists
 // and the row masks (weights in the grouped packing of conv_stream_group(64, 64)).
-bool conv_os_supported(int dtype, int ci, int co);
+bool conv_os_supported(int dtype, int ci, int co, int64_t n);
 hipError_t launch_conv_os(int dtype, const void * x, const int32_t * pair_src, const int32_t * tile_off,
                           const uint32_t * mask, const void * w16, const float * bias, void * y, int64_t n, int ci,
                           int co, hipStream_t s);
