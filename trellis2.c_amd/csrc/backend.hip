@@ -788,7 +788,7 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
     } need[] = {
         {&r->bkeys, slots * 8},
         {&r->bidx, slots * 4},
-        {&r->pool, (size_t) (kBrickGroups * brick_group_cap(n)) * kBrickCells * 4},
+        {&r->pool, (size_t) (pool_empty_brick(n) + 1) * kBrickCells * 4},
         {&r->counters, kCounterInts * 4},
         {&r->nbr, want_nbr ? (size_t) n * 27 * 4 : 0},
         {&r->mask, (size_t) n * 4},
@@ -803,7 +803,8 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
         if (st != TRELLIS_STATUS_OK) return st;
     }
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_HASH);
-    TSH_TRY(be, launch_hash_clear((uint64_t *) r->bkeys.ptr, r->table_slots, (int32_t *) r->counters.ptr, s));
+    TSH_TRY(be, launch_hash_clear((uint64_t *) r->bkeys.ptr, r->table_slots, (int32_t *) r->counters.ptr,
+                                  (int32_t *) r->pool.ptr, n, s));
     TSH_TRY(be, launch_brick_insert(coords, n, (uint64_t *) r->bkeys.ptr, (int32_t *) r->bidx.ptr, r->table_slots,
                                     (int32_t *) r->counters.ptr, (int32_t *) r->pool.ptr, s));
     TSH_TRY(be, launch_voxel_insert(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,

@@ -57,6 +57,19 @@ __device__ __forceinline__ int32_t brick_find(const uint64_t * __restrict__ bkey
     return -1;
 }
 
+// brick_find continued from slot s (the home slot held another key).
+__device__ __forceinline__ int32_t brick_find_from(const uint64_t * __restrict__ bkeys,
+                                                   const int32_t * __restrict__ bidx, uint64_t mask, uint64_t key,
+                                                   uint64_t s) {
+    for (uint64_t step = 1; step <= mask; ++step) {
+        const uint64_t k = bkeys[s];
+        if (k == key) return bidx[s];
+        if (k == 0) return -1;
+        s = (s + 1) & mask;
+    }
+    return -1;
+}
+
 __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
     const uint32_t lo = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) v, lane);
     const uint32_t hi = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) (v >> 32), lane);
@@ -65,12 +78,15 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
 
 __device__ __forceinline__ int lane_id() { return (int) __lane_id(); }
 
-// Empties the brick table (keys to 0) and clears the build's counters, in one
-// launch.
-__global__ void k_hash_clear(uint64_t * __restrict__ keys, int64_t slots, int32_t * __restrict__ counters) {
+// Empties the brick table (keys to 0), clears the build's counters and sets
+// the pool's spare row (the empty brick the kernel map reads for a missing
+// neighbour brick) to -1, in one launch.
+__global__ void k_hash_clear(uint64_t * __restrict__ keys, int64_t slots, int32_t * __restrict__ counters,
+                             int32_t * __restrict__ empty_row) {
     const int64_t stride = (int64_t) gridDim.x * blockDim.x;
     const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (t < kCounterInts) counters[t] = 0;
+    if (t < kBrickCells) empty_row[t] = -1;
     for (int64_t i = t; i < slots; i += stride) keys[i] = 0ull;
 }
 
@@ -212,7 +228,8 @@ template <bool NBR>
 __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ coords, int64_t n,
                                                       const uint64_t * __restrict__ bkeys,
                                                       const int32_t * __restrict__ bidx, uint64_t hmask,
-                                                      const int32_t * __restrict__ pool, int32_t * __restrict__ nbr,
+                                                      const int32_t * __restrict__ pool, int32_t empty_brick,
+                                                      int32_t * __restrict__ nbr,
                                                       uint32_t * __restrict__ mask_out,
                                                       int32_t * __restrict__ tile_counts,
                                                       int32_t * __restrict__ tile_off,
@@ -241,18 +258,40 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
         const int sx = cx == 0 ? -1 : (cx == 3 ? 1 : 0);
         const int sy = cy == 0 ? -1 : (cy == 3 ? 1 : 0);
         const int sz = cz == 0 ? -1 : (cz == 3 ? 1 : 0);
+        // The (up to) 8 bricks the 27 neighbours lie in.  Every lane loads
+        // the home slot's key and index of all 8 at once (a brick it does
+        // not need probes a dummy key), so one round trip resolves nearly
+        // all of them; only a home slot holding another key continues the
+        // linear probe.
         int32_t br[8];
+        uint64_t bkey[8], hkey[8];
+        int32_t hidx[8];
+        uint64_t hs[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const int ax = q & 1, ay = (q >> 1) & 1, az = (q >> 2) & 1;
+            const bool need = (ax == 0 || sx != 0) && (ay == 0 || sy != 0) && (az == 0 || sz != 0);
+            const uint32_t nbx = (bx + (uint32_t) (ax * sx)) & 0x3fffu;
+            const uint32_t nby = (by + (uint32_t) (ay * sy)) & 0x3fffu;
+            const uint32_t nbz = (bz + (uint32_t) (az * sz)) & 0x3fffu;
+            bkey[q] = need ? brick_key(b, nbx, nby, nbz) : 0ull;
+            hs[q] = mix64(bkey[q]) & hmask;
+            hkey[q] = bkeys[hs[q]];
+            hidx[q] = bidx[hs[q]];
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
             br[q] = -1;
-            if ((ax == 0 || sx != 0) && (ay == 0 || sy != 0) && (az == 0 || sz != 0)) {
-                const uint32_t nbx = (bx + (uint32_t) (ax * sx)) & 0x3fffu;
-                const uint32_t nby = (by + (uint32_t) (ay * sy)) & 0x3fffu;
-                const uint32_t nbz = (bz + (uint32_t) (az * sz)) & 0x3fffu;
-                br[q] = brick_find(bkeys, bidx, hmask, brick_key(b, nbx, nby, nbz));
+            if (bkey[q] != 0ull && hkey[q] != 0ull) {
+                br[q] = hkey[q] == bkey[q] ? hidx[q] : brick_find_from(bkeys, bidx, hmask, bkey[q], (hs[q] + 1) & hmask);
             }
         }
+        // All 9 z-rows and 9 face cells are loaded before any is used (one
+        // round trip per voxel); a missing brick (and, for a voxel off the z
+        // faces, the face cell) reads the pool's spare row of -1, so no
+        // branch guards a load.
+        int4 zrow[9];
+        int32_t face[9];
 #pragma unroll
         for (int kd = 0; kd < 3; ++kd) {
             const int nx = cx + kd - 1;
@@ -271,19 +310,25 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
                 // The z-row (nx, ny, 0..3) of the brick, and the one cell of
                 // the next brick along z that a face voxel also needs.
                 const int row = ((nx & 3) << 4) | ((ny & 3) << 2);
-                int4 v = make_int4(-1, -1, -1, -1);
-                if (brick >= 0) v = *(const int4 *) (pool + (int64_t) brick * kBrickCells + row);
-                int32_t e = -1;
-                if (sz != 0 && brick_z >= 0) e = pool[(int64_t) brick_z * kBrickCells + row + (sz < 0 ? 3 : 0)];
+                const int32_t vb = brick >= 0 ? brick : empty_brick;
+                const int32_t eb = (sz != 0 && brick_z >= 0) ? brick_z : empty_brick;
+                zrow[kd * 3 + kh] = *(const int4 *) (pool + (int64_t) vb * kBrickCells + row);
+                face[kd * 3 + kh] = pool[(int64_t) eb * kBrickCells + row + (sz < 0 ? 3 : 0)];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int kw = 0; kw < 3; ++kw) {
-                    const int nz = cz + kw - 1;
-                    const int32_t r = nz < 0 || nz > 3 ? e : (nz == 0 ? v.x : (nz == 1 ? v.y : (nz == 2 ? v.z : v.w)));
-                    const int k = kd * 9 + kh * 3 + kw;
-                    nb[k] = r;
-                    if constexpr (NBR) s_nbr[t * 27 + k] = r;
-                    m |= (r >= 0 ? 1u : 0u) << k;
-                }
+        for (int c = 0; c < 9; ++c) {
+            const int4 v = zrow[c];
+            const int32_t e = face[c];
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) {
+                const int nz = cz + kw - 1;
+                const int32_t r = nz < 0 || nz > 3 ? e : (nz == 0 ? v.x : (nz == 1 ? v.y : (nz == 2 ? v.z : v.w)));
+                const int k = c * 3 + kw;
+                nb[k] = r;
+                if constexpr (NBR) s_nbr[t * 27 + k] = r;
+                m |= (r >= 0 ? 1u : 0u) << k;
             }
         }
         mask_out[i] = m;
@@ -362,11 +407,15 @@ hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_
 }
 
 int64_t brick_group_cap(int64_t n) { return ((n + kBlock - 1) / kBlock + kBrickGroups - 1) / kBrickGroups * kBlock; }
+int64_t pool_empty_brick(int64_t n) { return kBrickGroups * brick_group_cap(n); }
 
-hipError_t launch_hash_clear(uint64_t * bkeys, int64_t slots, int32_t * counters, hipStream_t s) {
-    // The grid has at least 256 threads, which covers the counters.
-    static_assert(kCounterInts <= 256, "counters cleared by the first block");
-    k_hash_clear<<<grid_for(slots, 256, 16384), 256, 0, s>>>(bkeys, slots, counters);
+hipError_t launch_hash_clear(uint64_t * bkeys, int64_t slots, int32_t * counters, int32_t * pool, int64_t n,
+                             hipStream_t s) {
+    // The grid has at least 256 threads, which covers the counters and the
+    // spare pool row.
+    static_assert(kCounterInts <= 256 && kBrickCells <= 256, "cleared by the first block");
+    k_hash_clear<<<grid_for(slots, 256, 16384), 256, 0, s>>>(bkeys, slots, counters,
+                                                             pool + pool_empty_brick(n) * kBrickCells);
     return hipGetLastError();
 }
 
@@ -392,14 +441,15 @@ hipError_t launch_map_tiles(const int32_t * coords, int64_t n, const uint64_t * 
                             int32_t * tile_counts, int32_t * tile_off, int32_t * pair_src, int32_t * pair_dst,
                             int32_t * counters, hipStream_t s) {
     const int64_t blocks = (n + kBlock - 1) / kBlock;
+    const int32_t empty = (int32_t) pool_empty_brick(n);
     if (nbr != nullptr) {
         k_map_tiles<true><<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
-                                                               (uint64_t) (slots - 1), pool, nbr, mask, tile_counts,
-                                                               tile_off, pair_src, pair_dst, counters);
+                                                               (uint64_t) (slots - 1), pool, empty, nbr, mask,
+                                                               tile_counts, tile_off, pair_src, pair_dst, counters);
     } else {
         k_map_tiles<false><<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
-                                                                (uint64_t) (slots - 1), pool, nbr, mask, tile_counts,
-                                                                tile_off, pair_src, pair_dst, counters);
+                                                                (uint64_t) (slots - 1), pool, empty, nbr, mask,
+                                                                tile_counts, tile_off, pair_src, pair_dst, counters);
     }
     return hipGetLastError();
 }

@@ -169,12 +169,16 @@ namespace tsh {
 // Voxel hash + kernel map (kernels_map.hip).
 hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_t s);
 // Brick table keys to 0 and the build counters (kCounterInts) to 0, one launch.
-hipError_t launch_hash_clear(uint64_t * bkeys, int64_t slots, int32_t * counters, hipStream_t s);
+// Also sets the pool's spare row (brick pool_empty_brick(n)) to -1.
+hipError_t launch_hash_clear(uint64_t * bkeys, int64_t slots, int32_t * counters, int32_t * pool, int64_t n,
+                             hipStream_t s);
 // Inserts the voxels' bricks, numbers the new ones and sets their pool rows to -1.
 hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx,
                                int64_t slots, int32_t * counters, int32_t * pool, hipStream_t s);
-// Bricks per group for n voxels (pool capacity = kBrickGroups * that).
+// Bricks per group for n voxels (pool capacity = kBrickGroups * that, plus
+// one spare row of -1 at index pool_empty_brick(n)).
 int64_t brick_group_cap(int64_t n);
+int64_t pool_empty_brick(int64_t n);
 
 hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
                                int64_t slots, int32_t * pool, int32_t * counters, hipStream_t s);
