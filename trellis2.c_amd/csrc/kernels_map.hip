@@ -41,23 +41,8 @@ __device__ __forceinline__ uint64_t brick_key(uint32_t b, uint32_t bx, uint32_t 
     return (((uint64_t) b << 42) | ((uint64_t) bx << 28) | ((uint64_t) by << 14) | (uint64_t) bz) + 1ull;
 }
 
-__device__ __forceinline__ int32_t brick_find(const uint64_t * __restrict__ bkeys, const int32_t * __restrict__ bidx,
-                                              uint64_t mask, uint64_t key) {
-    uint64_t s = mix64(key) & mask;
-    for (uint64_t step = 0; step <= mask; ++step) {
-        const uint64_t k = bkeys[s];
-        if (k == key) {
-            return bidx[s];
-        }
-        if (k == 0) {
-            return -1;
-        }
-        s = (s + 1) & mask;
-    }
-    return -1;
-}
-
-// brick_find continued from slot s (the home slot held another key).
+// Linear probe for key from slot s on (the home slot held another key):
+// the brick's index, or -1 at an empty slot.
 __device__ __forceinline__ int32_t brick_find_from(const uint64_t * __restrict__ bkeys,
                                                    const int32_t * __restrict__ bidx, uint64_t mask, uint64_t key,
                                                    uint64_t s) {
@@ -193,7 +178,13 @@ __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict
     }
     const int4 c = coords[i];
     const uint32_t x = (uint32_t) c.y & 0xffffu, y = (uint32_t) c.z & 0xffffu, z = (uint32_t) c.w & 0xffffu;
-    const int32_t b = brick_find(bkeys, bidx, mask, brick_key((uint32_t) c.x & 0xffffu, x >> 2, y >> 2, z >> 2));
+    // The home slot's key and index in one round trip; only a home slot
+    // holding another key continues the probe.
+    const uint64_t key = brick_key((uint32_t) c.x & 0xffffu, x >> 2, y >> 2, z >> 2);
+    const uint64_t hs = mix64(key) & mask;
+    const uint64_t hk = bkeys[hs];
+    const int32_t hi = bidx[hs];
+    const int32_t b = hk == key ? hi : (hk == 0ull ? -1 : brick_find_from(bkeys, bidx, mask, key, (hs + 1) & mask));
     if (b < 0) {
         atomicOr(&counters[4], 2);  // unreachable: every voxel's brick was inserted
         return;
