@@ -161,20 +161,28 @@ __global__ void k_c2s_count(const typename Store<DT>::T * __restrict__ logits, i
     }
 }
 
+// One lane per (parent, subidx) slot, 8 consecutive lanes per parent: a
+// child's place is the parent's offset plus the number of earlier slots of
+// the parent that have a child (a ballot over the lane's group of 8), so the
+// children a wavefront writes are consecutive in all three outputs.  (One
+// lane per parent wrote its children 64 bytes apart from its neighbours'.)
 template <int DT>
 __global__ void k_c2s_fill(const int4 * __restrict__ coords, const typename Store<DT>::T * __restrict__ logits,
                            const int32_t * __restrict__ offsets, int64_t n, int4 * __restrict__ out_coords,
                            int32_t * __restrict__ parent, int32_t * __restrict__ subidx) {
-    TSH_GRID_STRIDE(p, n) {
-        const int4 c = coords[p];
-        int64_t w = offsets[p];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            if (!(Store<DT>::ld(logits, p * 8 + s) > 0.0f)) continue;
-            out_coords[w] = make_int4(c.x, 2 * c.y + (s & 1), 2 * c.z + ((s >> 1) & 1), 2 * c.w + ((s >> 2) & 1));
+    const int64_t stride = (int64_t) gridDim.x * blockDim.x;  // a multiple of 64: groups of 8 stay aligned
+    const int lane = (int) (threadIdx.x & 63);
+    for (int64_t e = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; e < n * 8; e += stride) {
+        const int64_t p = e >> 3;
+        const int sidx = (int) (e & 7);
+        const bool on = Store<DT>::ld(logits, e) > 0.0f;
+        const uint32_t grp = (uint32_t) (__ballot(on) >> (lane & 56)) & 0xffu;
+        if (on) {
+            const int4 c = coords[p];
+            const int64_t w = offsets[p] + __popc(grp & ((1u << sidx) - 1u));
+            out_coords[w] = make_int4(c.x, 2 * c.y + (sidx & 1), 2 * c.z + ((sidx >> 1) & 1), 2 * c.w + ((sidx >> 2) & 1));
             parent[w] = (int32_t) p;
-            subidx[w] = s;
-            ++w;
+            subidx[w] = sidx;
         }
     }
 }
@@ -612,7 +620,7 @@ hipError_t launch_scan_exclusive(const int32_t * in, int32_t * out, int64_t n, i
 
 hipError_t launch_c2s_fill(int dtype, const int32_t * coords, const void * logits, const int32_t * offsets, int64_t n,
                            int32_t * out_coords, int32_t * parent, int32_t * subidx, hipStream_t s) {
-    const int g = blocks_for(n, 256, 16384);
+    const int g = blocks_for(n * 8, 256, 16384);
     const int4 * c = (const int4 *) coords;
     int4 * oc = (int4 *) out_coords;
     switch (dtype) {
