@@ -339,6 +339,8 @@ __global__ void k_skip_repeat(const typename Store<DT>::T * __restrict__ x, cons
 // them instead of running back to back.  kSingle: the repeat count is a
 // multiple of the chunk width, so one source element fills the whole chunk
 // (repeat-interleave of 8 or more); rshift >= 0: the repeat count is 2^rshift.
+typedef int I32x4 __attribute__((ext_vector_type(4)));
+
 template <int DT, bool kSingle>
 __global__ void __launch_bounds__(256) k_skip_repeat_vec(const typename Store<DT>::T * __restrict__ x,
                                                          const int32_t * __restrict__ parent,
@@ -392,7 +394,11 @@ __global__ void __launch_bounds__(256) k_skip_repeat_vec(const typename Store<DT
         }
 #pragma unroll
         for (int u = 0; u < kIlp; ++u) {
-            if (e0 + u * S < total) *(int4 *) (y + (int64_t) r[u] * co + c0[u]) = out[u].v;
+            // Non-temporal: the broadcast rows are read back only by the next
+            // kernel's gathers, from HBM either way (config 3: 647 MB), and
+            // leaving them out of the caches shortened the conv that follows
+            // (step 1.990 -> 1.976 ms).
+            if (e0 + u * S < total) __builtin_nontemporal_store(__builtin_bit_cast(I32x4, out[u].v), (I32x4 *) (y + (int64_t) r[u] * co + c0[u]));
         }
     }
 }
