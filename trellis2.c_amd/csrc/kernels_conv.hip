@@ -750,8 +750,8 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-template <int DT, int BN, int RG, int UPB, int DEPTH, int TMR, int NW>
-__global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,
+template <int DT, int BN, int RG, int UPB, int DEPTH, int TMR, int NW, int AP = 1>
+__global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,
                                                         const int32_t * __restrict__ pair_src,
                                                         const int32_t * __restrict__ pair_dst,
                                                         const int32_t * __restrict__ tile_off,
@@ -763,7 +763,7 @@ __global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) k_conv_mfma_wreg(con
                                                         int co, int64_t n_col_tiles, ConvEpilogue epi) {
     using T = typename Store<DT>::T;
     using V = typename Mfma<DT>::V;
-    // NW wavefronts; a unit holds one 16-row block per wavefront.
+    // NW wavefronts; a unit holds AP 16-row blocks per wavefront.
     constexpr int NTHR = 64 * NW;
     constexpr int TM = TMR;          // rows per block: a kernel-map tile, or half of one
     constexpr int HALVES = kMapTile / TM;
@@ -772,14 +772,15 @@ __global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) k_conv_mfma_wreg(con
     constexpr int CG = NW / RG;      // channel groups
     constexpr int WN = BN / CG;      // channels per wavefront
     constexpr int NT = WN / 16;      // MFMA column tiles per wavefront
-    constexpr int PASS = 16 * NW;    // pairs per unit
-    constexpr int QB = NW / RG;      // row blocks per wavefront per unit
+    constexpr int PASS = 16 * NW * AP;  // pairs per unit
+    constexpr int QB = NW * AP / RG;    // row blocks per wavefront per unit
     constexpr int MAX_UNITS = 27 * (TM / PASS);
     constexpr int QF = QB < 2 ? QB : 2;  // row blocks per flush batch
     constexpr int RING = UPB == 1 ? 4 : 8;
     constexpr int SPU = DEPTH / UPB;
     static_assert((RG == 1 || RG == 2 || RG == 4) && NT >= 1 && WN % 16 == 0, "row groups");
-    static_assert(PASS * 4 == NTHR, "one 16-byte A piece per thread and step");
+    static_assert(PASS * 4 == NTHR * AP && (AP == 1 || AP == 2), "AP 16-byte A pieces per thread and step");
+    static_assert(2 * PASS <= NTHR, "a thread per src and dst list entry");
     static_assert(UPB == 1 || UPB == 2, "units per block");
     static_assert(DEPTH == 4 || DEPTH == 8, "block of 4 or 8 steps");
     __shared__ float s_acc[(TM + 1) * BN];      // row TM absorbs padding rows
@@ -935,12 +936,17 @@ __global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) k_conv_mfma_wreg(con
     for (int j = 0; j < UPB; ++j) lv[j] = list_load(2 * UPB + j);
     lds_barrier();
 
-    // This thread's A piece: wavefront w fetches and stores row block w of the
-    // unit; quad j of the wavefront (lanes 4j .. 4j+3) fetches row
-    // a_quad_row(j) of the block, lane 4j + c its chunk c.  Fragment q of
-    // this lane: chunk lg of row l16 of row block rh + RG q.
-    const int arow = (t >> 6) * 16 + a_quad_row((t >> 2) & 15), achunk = t & 3;
-    const int a_st = ((t >> 6) * 64 + a_granule(arow & 15, achunk)) * 8;
+    // This thread's A pieces: wavefront w fetches and stores row blocks w +
+    // NW p (p < AP) of the unit; quad j of the wavefront (lanes 4j .. 4j+3)
+    // fetches row a_quad_row(j) of the block, lane 4j + c its chunk c.
+    // Fragment q of this lane: chunk lg of row l16 of row block rh + RG q.
+    const int achunk = t & 3;
+    int arow[AP], a_st[AP];
+#pragma unroll
+    for (int p = 0; p < AP; ++p) {
+        arow[p] = ((t >> 6) + NW * p) * 16 + a_quad_row((t >> 2) & 15);
+        a_st[p] = (((t >> 6) + NW * p) * 64 + a_granule(arow[p] & 15, achunk)) * 8;
+    }
     const int a_ld = (rh * 64 + a_granule(l16, lg)) * 8;
     constexpr int A_QSTRIDE = RG * 64 * 8;
 
@@ -949,29 +955,38 @@ __global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) k_conv_mfma_wreg(con
     // step r (past the last unit: the last unit again).
     const int64_t bstep = (int64_t) 4 * co * 8;  // elements between consecutive K steps' weights
     const int64_t blane = ((int64_t) lg * co + ch * WN + l16) * 8;
-    const T * pa[UPB];
+    const T * pa[UPB][AP];
     const T * pb[UPB];
     auto target = [&](int tu0, int tps) {
 #pragma unroll
         for (int uo = 0; uo < UPB; ++uo) {
             const int tu = tu0 + uo < U ? tu0 + uo : U - 1;
-            const int32_t src = s_rsrc[tu & (RING - 1)][arow];
-            pa[uo] = x + (int64_t) src * ci + tps * BK + achunk * 8;
+#pragma unroll
+            for (int p = 0; p < AP; ++p) {
+                const int32_t src = s_rsrc[tu & (RING - 1)][arow[p]];
+                pa[uo][p] = x + (int64_t) src * ci + tps * BK + achunk * 8;
+            }
             pb[uo] = w16 + ((int64_t) (s_uk[tu] * ci8 + tps * 4) * co + col0) * 8 + blane;
         }
     };
-    auto load_a = [&](V & a, int r) { a = *(const V *) (pa[r / SPU] + (r % SPU) * BK); };
+    auto load_a = [&](V (&a)[AP], int r) {
+#pragma unroll
+        for (int p = 0; p < AP; ++p) a[p] = *(const V *) (pa[r / SPU][p] + (r % SPU) * BK);
+    };
     auto load_b = [&](V * b, int r) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) b[nt] = *(const V *) (pb[r / SPU] + (r % SPU) * bstep + nt * 16 * 8);
     };
-    auto store_a = [&](int slot, const V & a) { *(V *) (&s_a[slot][a_st]) = a; };
+    auto store_a = [&](int slot, const V (&a)[AP]) {
+#pragma unroll
+        for (int p = 0; p < AP; ++p) *(V *) (&s_a[slot][a_st[p]]) = a[p];
+    };
     auto read_a = [&](V * f, int slot) {
 #pragma unroll
         for (int q = 0; q < QB; ++q) f[q] = *(const V *) (&s_a[slot][a_ld + q * A_QSTRIDE]);
     };
 
-    V ra[DEPTH];      // A pieces in flight
+    V ra[DEPTH][AP];  // A pieces in flight
     V rb[DEPTH][NT];  // weights of the block's steps (refilled with the next block's)
     V af[2][QB];      // A fragments of step g in af[g & 1]
     f32x4 acc[QB][NT];
@@ -1185,15 +1200,17 @@ __global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) k_conv_mfma_wreg(con
 // tile (4 wavefronts x 64 rows, lane = row), a wavefront 4 row blocks of 16
 // x all Co = 64 channels.  For offset k each row's source is read from the
 // tile's pair list for k (its rank among the tile's rows with a neighbour at
-// k comes from ballots of the row masks), the 16 source rows of a row block
-// are loaded coalesced (four lanes per 64-byte K step) and moved to MFMA
-// operand order with ds_bpermute; a row without a neighbour at k multiplies
-// zeros.  The loads are raw buffer loads over x: a missing neighbour gets an
+// k comes from ballots of the row masks), and the 16 source rows of a row
+// block are loaded straight into MFMA operand order (lane i + 16 c: chunk c
+// of row i's 64-byte K step); a row without a neighbour at k multiplies
+// zeros.  (Loading each row's 64 bytes with four neighbouring lanes and
+// moving them to operand order with ds_bpermute, 4 per fragment, measured
+// 15 % slower: config 4, 1.196 -> 1.036 ms.)  The loads are raw buffer loads over x: a missing neighbour gets an
 // offset past the buffer's end, which the hardware answers with zeros and no
 // memory request, so no branch guards a load and the compiler's memory waits
 // keep the two-offset look-ahead (a guarded load made it wait for each
-// offset's loads almost at once).  The offset's 8 KB of weights are shared through a double-buffered
-// LDS slot: one barrier per offset.  Each row's 27 sources are fetched in one
+// offset's loads almost at once).  The offset's 8 KB of weights are shared
+// through a double-buffered LDS slot: one barrier per offset.  Each row's 27 sources are fetched in one
 // round trip at the start; operand loads run two offsets ahead.  No unit
 // lists, no tile sums, no flushes: the MFMA rows include the rows without a
 // neighbour (27 N row-offsets against P), which is the price of keeping the
@@ -1257,10 +1274,10 @@ __global__ void __launch_bounds__(256, 2) k_conv_os64(const typename Store<DT>::
         for (int w = 0; w < wave; ++w) base += s_cnt[k][w];
         src[k] = ((m >> k) & 1u) ? pair_src[s_off[k] + base + __popcll(bk & lt)] : -1;
     }
-    // A pieces of offset k: row block q, K step f; lane 4i + c holds 16 bytes
-    // (chunk c of the step) of row i of the block.  Byte offsets into x per
-    // row block (rows of the lane's quad), prepared one offset before their
-    // loads so that the shuffles' latency stays off the load path.
+    // A fragments of offset k: row block q, K step f; lane i + 16 c holds 16
+    // bytes (chunk c of the step) of row i of the block.  Byte offsets into x
+    // per row block, prepared one offset before their loads so that the
+    // shuffles' latency stays off the load path.
     constexpr int AHEAD = 2;  // offsets whose A loads are in flight
     const __amdgpu_buffer_rsrc_t xres =
         __builtin_amdgcn_make_buffer_rsrc((void *) x, 0, (int) (n * CI * (int64_t) sizeof(T)), 0x00020000);
@@ -1269,8 +1286,8 @@ __global__ void __launch_bounds__(256, 2) k_conv_os64(const typename Store<DT>::
     auto prep_a = [&](int32_t src) {
 #pragma unroll
         for (int q = 0; q < QB; ++q) {
-            const int32_t sq = __shfl(src, q * 16 + (lane >> 2));
-            voff[q] = sq >= 0 ? (uint32_t) sq * (uint32_t) (CI * sizeof(T)) + (uint32_t) (lane & 3) * 16u : 0x80000000u;
+            const int32_t sq = __shfl(src, q * 16 + l16);
+            voff[q] = sq >= 0 ? (uint32_t) sq * (uint32_t) (CI * sizeof(T)) + (uint32_t) lg * 16u : 0x80000000u;
         }
     };
     auto load_a = [&](V (&a)[QB][2]) {
@@ -1285,7 +1302,6 @@ __global__ void __launch_bounds__(256, 2) k_conv_os64(const typename Store<DT>::
     for (int q = 0; q < QB; ++q)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int perm = (4 * l16 + lg) * 4;
 #pragma unroll
     for (int k = 0; k < AHEAD; ++k) {
         prep_a(src[k]);
@@ -1298,8 +1314,8 @@ __global__ void __launch_bounds__(256, 2) k_conv_os64(const typename Store<DT>::
         const int ar = k % (AHEAD + 1);
         if (k + AHEAD < 27) load_a(ra[(k + AHEAD) % (AHEAD + 1)]);
         if (k + AHEAD + 1 < 27) prep_a(src[k + AHEAD + 1]);
-        // The scheduler would otherwise move the transposes of the loads just
-        // issued up to them, which makes the loads wait at once.
+        // Keeps the loads just issued ahead of this offset's weight reads and
+        // MFMAs (the scheduler would interleave them).
         __builtin_amdgcn_sched_barrier(0);
         // Weight fragments of offset k: K step f, column tile nt.
         V bw[2][NT];
@@ -1312,9 +1328,8 @@ __global__ void __launch_bounds__(256, 2) k_conv_os64(const typename Store<DT>::
         for (int q = 0; q < QB; ++q)
 #pragma unroll
             for (int f = 0; f < 2; ++f) {
-                const V a = to_mfma_rows<V>(ra[ar][q][f], perm);
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) acc[q][nt] = Mfma<DT>::mac(a, bw[f][nt], acc[q][nt]);
+                for (int nt = 0; nt < NT; ++nt) acc[q][nt] = Mfma<DT>::mac(ra[ar][q][f], bw[f][nt], acc[q][nt]);
             }
         // Offset k + 1's weights into the other slot (read last at offset
         // k - 1, before the previous barrier); offset k + 2's into registers.
