@@ -1881,7 +1881,7 @@ trellis_status trellis_sparse_hip_rulebook_stats(trellis_sparse_backend * backen
     int64_t total = 0;
     for (const int32_t c : cnt) total += c;
     int64_t nb = 0;
-    for (int g = 0; g < tsh::kBrickGroups; ++g) nb += ctr[tsh::kBrickCounter + g];
+    for (int g = 0; g < tsh::kBrickCounters; ++g) nb += ctr[tsh::kBrickCounter + g];
     if (n != nullptr) *n = rulebook->n;
     if (pairs != nullptr) *pairs = total;
     if (table_slots != nullptr) *table_slots = rulebook->table_slots;

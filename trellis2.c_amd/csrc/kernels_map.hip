@@ -86,11 +86,14 @@ __global__ void k_fill_i32(int32_t * __restrict__ p, int64_t count, int32_t valu
 // per distinct brick (ballot/readlane, no memory traffic); representatives
 // then insert concurrently with a 64-bit CAS.  The lane that claims an empty
 // slot numbers the brick, and its wavefront sets the brick's 64 pool cells to
-// -1 (one coalesced 256-byte store per new brick).
+// -1 (one coalesced 256-byte store per new brick).  Block b numbers its new
+// bricks from b * 256 (a block has at most one per voxel), so numbering
+// needs no global counter and no second round trip; the pool has a row per
+// voxel slot, of which the map reads only the rows of existing bricks.
 __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict__ coords, int64_t n,
                                                          uint64_t * __restrict__ bkeys, int32_t * __restrict__ bidx,
                                                          uint64_t mask, int32_t * __restrict__ counters,
-                                                         int32_t group_cap, int32_t * __restrict__ pool) {
+                                                         int32_t * __restrict__ pool) {
     const int64_t i = (int64_t) blockIdx.x * kBlock + threadIdx.x;
     const bool active = i < n;
     uint64_t key = 0;
@@ -132,10 +135,9 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
             atomicOr(&counters[4], 1);  // table full; cannot happen with slots >= 2n
         }
     }
-    // Number the new bricks with one global atomic per block: wave ballots give
-    // each winner its rank, LDS gives each wave its block offset.
+    // Number the new bricks: wave ballots give each winner its rank, LDS gives
+    // each wave its offset in the block's range.
     __shared__ int32_t s_wave_new[kBlock / 64];
-    __shared__ int32_t s_base;
     const int wave = threadIdx.x >> 6;
     const uint64_t wins = __ballot(won);
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -144,18 +146,15 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        // Block b numbers its bricks in group b % kBrickGroups, whose counter
-        // few other blocks share; the group's range holds one brick per voxel
-        // of its blocks.
+        // The brick count (statistics only): one add per block, spread over
+        // kBrickCounters counters, whose result nothing waits for.
         int32_t total = 0;
         for (int w = 0; w < kBlock / 64; ++w) total += s_wave_new[w];
-        const int g = blockIdx.x % kBrickGroups;
-        s_base = total > 0 ? g * group_cap + atomicAdd(&counters[kBrickCounter + g], total) : 0;
+        if (total > 0) atomicAdd(&counters[kBrickCounter + blockIdx.x % kBrickCounters], total);
     }
-    __syncthreads();
     int32_t idx = 0;
     if (won) {
-        idx = s_base + __popcll(wins & below);
+        idx = (int32_t) blockIdx.x * kBlock + __popcll(wins & below);
         for (int w = 0; w < wave; ++w) idx += s_wave_new[w];
         bidx[s] = idx;
     }
@@ -167,7 +166,9 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
 }
 
 // One lane per voxel: record the row in its brick cell.  atomicMax makes the
-// highest row (the last duplicate in input order) win deterministically.
+// highest row (the last duplicate in input order) win deterministically; its
+// result is not waited for (the kernel map finds duplicates: a row whose own
+// cell holds another row).
 __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict__ coords, int64_t n,
                                                          const uint64_t * __restrict__ bkeys,
                                                          const int32_t * __restrict__ bidx, uint64_t mask,
@@ -190,10 +191,7 @@ __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict
         return;
     }
     const uint32_t cell = (z & 3u) | ((y & 3u) << 2) | ((x & 3u) << 4);
-    const int32_t old = atomicMax(&pool[(int64_t) b * kBrickCells + cell], (int32_t) i);
-    if (old >= 0) {
-        atomicOr(&counters[1], 1);
-    }
+    atomicMax(&pool[(int64_t) b * kBrickCells + cell], (int32_t) i);
 }
 
 // Kernel map in one pass.  One block = one 256-row tile:
@@ -323,6 +321,9 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
             }
         }
         mask_out[i] = m;
+        // The centre neighbour is the highest row at these coordinates: any
+        // other value means duplicate coordinates.
+        if (nb[13] != (int32_t) i) atomicOr(&counters[1], 1);
     }
     // Rows of this wavefront with a neighbour at k (the ranks are recomputed
     // from the same ballots when the pairs are written).
@@ -397,8 +398,7 @@ hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_
     return hipGetLastError();
 }
 
-int64_t brick_group_cap(int64_t n) { return ((n + kBlock - 1) / kBlock + kBrickGroups - 1) / kBrickGroups * kBlock; }
-int64_t pool_empty_brick(int64_t n) { return kBrickGroups * brick_group_cap(n); }
+int64_t pool_empty_brick(int64_t n) { return (n + kBlock - 1) / kBlock * kBlock; }
 
 hipError_t launch_hash_clear(uint64_t * bkeys, int64_t slots, int32_t * counters, int32_t * pool, int64_t n,
                              hipStream_t s) {
@@ -414,8 +414,7 @@ hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bke
                                int32_t * counters, int32_t * pool, hipStream_t s) {
     const int64_t blocks = (n + kBlock - 1) / kBlock;
     k_brick_insert<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
-                                                        (uint64_t) (slots - 1), counters,
-                                                        (int32_t) brick_group_cap(n), pool);
+                                                        (uint64_t) (slots - 1), counters, pool);
     return hipGetLastError();
 }
 

@@ -105,11 +105,12 @@ template <int DT> __device__ inline int4 pack_chunk(const float * v) {
 // Work split of a rulebook build / conv: rows per tile of the kernel map.
 constexpr int kMapTile = 256;
 constexpr int kBrickCells = 64;  // 4x4x4 cells per brick
-// Bricks are numbered in kBrickGroups groups (counters[kBrickCounter + g]);
-// group g owns bricks [g * cap, (g + 1) * cap), cap = brick_group_cap(n).
-constexpr int kBrickGroups = 64;
+// Build counters: [1] duplicate flag, [4] internal-error flags, and the
+// brick count (statistics) summed over kBrickCounters counters from
+// counters[kBrickCounter].
+constexpr int kBrickCounters = 64;
 constexpr int kBrickCounter = 64;
-constexpr int kCounterInts = kBrickCounter + kBrickGroups;
+constexpr int kCounterInts = kBrickCounter + kBrickCounters;
 
 struct Backend;
 
@@ -139,7 +140,7 @@ struct trellis_sparse_rulebook {
     tsh::DevMem bkeys;       // uint64 [table_slots]
     tsh::DevMem bidx;        // int32  [table_slots]
     tsh::DevMem pool;        // int32  [cap_bricks][64] voxel rows, -1 = empty
-    tsh::DevMem counters;    // int32  [kCounterInts]: [1] duplicate flag, [4] internal-error flags, [64..] brick groups
+    tsh::DevMem counters;    // int32  [kCounterInts]: [1] duplicate flag, [4] internal-error flags, [64..] brick counts
     // Kernel map.
     tsh::DevMem nbr;         // int32  [n][27]
     tsh::DevMem mask;        // uint32 [n] bit k set when nbr[i][k] >= 0
@@ -172,12 +173,12 @@ hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_
 // Also sets the pool's spare row (brick pool_empty_brick(n)) to -1.
 hipError_t launch_hash_clear(uint64_t * bkeys, int64_t slots, int32_t * counters, int32_t * pool, int64_t n,
                              hipStream_t s);
-// Inserts the voxels' bricks, numbers the new ones and sets their pool rows to -1.
+// Inserts the voxels' bricks, numbers the new ones (block b's from b * 256)
+// and sets their pool rows to -1.
 hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx,
                                int64_t slots, int32_t * counters, int32_t * pool, hipStream_t s);
-// Bricks per group for n voxels (pool capacity = kBrickGroups * that, plus
-// one spare row of -1 at index pool_empty_brick(n)).
-int64_t brick_group_cap(int64_t n);
+// Pool rows for n voxels (one per voxel slot of the insert's blocks); the
+// spare row of -1 sits at index pool_empty_brick(n).
 int64_t pool_empty_brick(int64_t n);
 
 hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
