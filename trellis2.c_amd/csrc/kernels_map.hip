@@ -115,13 +115,18 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
         todo &= ~same;
     }
     // Representatives probe; a lane that claims an empty slot owns a new brick.
+    // A slot's key only ever changes from 0 to its final value, so a read
+    // that returns a key is final: the CAS is issued only for a slot that
+    // read empty.  Other wavefronts insert most bricks first (a 4^3 brick
+    // spans rows far apart in raster order).
     uint64_t s = 0;
     bool won = false;
     if (first) {
         s = mix64(key) & mask;
         uint64_t step = 0;
         for (; step <= mask; ++step) {
-            const uint64_t prev = atomicCAS((unsigned long long *) &bkeys[s], 0ull, (unsigned long long) key);
+            uint64_t prev = __hip_atomic_load(&bkeys[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (prev == 0) prev = atomicCAS((unsigned long long *) &bkeys[s], 0ull, (unsigned long long) key);
             if (prev == 0) {
                 won = true;
                 break;
