@@ -744,7 +744,7 @@ trellis_status rulebook_ensure_nbr(Backend * be, const trellis_sparse_rulebook *
 }
 void rulebook_release(Backend * be, trellis_sparse_rulebook * r) {
     if (r == nullptr) return;
-    DevMem * mems[] = {&r->coords_mem, &r->bkeys, &r->bidx, &r->pool, &r->counters, &r->nbr, &r->mask,
+    DevMem * mems[] = {&r->coords_mem, &r->table, &r->pool, &r->counters, &r->nbr, &r->mask,
                        &r->tile_counts, &r->tile_off, &r->pair_src, &r->pair_dst};
     for (DevMem * m : mems) dev_release(be, m);
     delete r;
@@ -760,7 +760,7 @@ int64_t next_pow2(int64_t v) {
 // kernel, which rewrites the pair lists with the same values).
 trellis_status map_pass(Backend * be, trellis_sparse_rulebook * r, hipStream_t s) {
     return hip_status(be,
-                      launch_map_tiles(r->coords, r->n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
+                      launch_map_tiles(r->coords, r->n, (const uint64_t *) r->table.ptr,
                                        r->table_slots, (const int32_t *) r->pool.ptr, (int32_t *) r->nbr.ptr,
                                        (uint32_t *) r->mask.ptr, (int32_t *) r->tile_counts.ptr,
                                        (int32_t *) r->tile_off.ptr, (int32_t *) r->pair_src.ptr,
@@ -786,8 +786,7 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
         DevMem * m;
         size_t bytes;
     } need[] = {
-        {&r->bkeys, slots * 8},
-        {&r->bidx, slots * 4},
+        {&r->table, slots * 16},
         {&r->pool, (size_t) (pool_empty_brick(n) + 1) * kBrickCells * 4},
         {&r->counters, kCounterInts * 4},
         {&r->nbr, want_nbr ? (size_t) n * 27 * 4 : 0},
@@ -803,11 +802,11 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
         if (st != TRELLIS_STATUS_OK) return st;
     }
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_HASH);
-    TSH_TRY(be, launch_hash_clear((uint64_t *) r->bkeys.ptr, r->table_slots, (int32_t *) r->counters.ptr,
+    TSH_TRY(be, launch_hash_clear((uint64_t *) r->table.ptr, r->table_slots, (int32_t *) r->counters.ptr,
                                   (int32_t *) r->pool.ptr, n, s));
-    TSH_TRY(be, launch_brick_insert(coords, n, (uint64_t *) r->bkeys.ptr, (int32_t *) r->bidx.ptr, r->table_slots,
+    TSH_TRY(be, launch_brick_insert(coords, n, (uint64_t *) r->table.ptr, r->table_slots,
                                     (int32_t *) r->counters.ptr, (int32_t *) r->pool.ptr, s));
-    TSH_TRY(be, launch_voxel_insert(coords, n, (const uint64_t *) r->bkeys.ptr, (const int32_t *) r->bidx.ptr,
+    TSH_TRY(be, launch_voxel_insert(coords, n, (const uint64_t *) r->table.ptr,
                                     r->table_slots, (int32_t *) r->pool.ptr, (int32_t *) r->counters.ptr, s));
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_HASH);
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_MAP);

@@ -6,7 +6,8 @@
 //   neighbour (b, x+kd-1, y+kh-1, z+kw-1), k = kd*9+kh*3+kw, never across b  :348-358
 //
 // Layout in HBM (all sized from n, no host synchronisation):
-//   brick table  uint64 keys[slots] + int32 idx[slots], slots = nextpow2(2n).
+//   brick table  16-byte slots {uint64 key, int32 idx, pad}, slots = nextpow2(2n),
+//                so that one load returns a slot's key and brick index.
 //                Key = (b:16 | x>>2:14 | y>>2:14 | z>>2:14) + 1, 0 = empty,
 //                linear probing from splitmix64(key).
 //   voxel pool   int32 [bricks][64]: row of the voxel at cell (z&3)|(y&3)<<2|(x&3)<<4, -1 = empty
@@ -41,15 +42,26 @@ __device__ __forceinline__ uint64_t brick_key(uint32_t b, uint32_t bx, uint32_t 
     return (((uint64_t) b << 42) | ((uint64_t) bx << 28) | ((uint64_t) by << 14) | (uint64_t) bz) + 1ull;
 }
 
+// Slot s of the brick table (two uint64 words per slot: the key, then the
+// brick index in the low half of the second word), read with one load.
+typedef unsigned long long U64x2 __attribute__((ext_vector_type(2)));
+struct Slot {
+    uint64_t key;
+    int32_t idx;
+};
+__device__ __forceinline__ Slot slot_load(const uint64_t * __restrict__ table, uint64_t s) {
+    const U64x2 e = *(const U64x2 *) (table + 2 * s);
+    return {e.x, (int32_t) (uint32_t) e.y};
+}
+
 // Linear probe for key from slot s on (the home slot held another key):
 // the brick's index, or -1 at an empty slot.
-__device__ __forceinline__ int32_t brick_find_from(const uint64_t * __restrict__ bkeys,
-                                                   const int32_t * __restrict__ bidx, uint64_t mask, uint64_t key,
+__device__ __forceinline__ int32_t brick_find_from(const uint64_t * __restrict__ table, uint64_t mask, uint64_t key,
                                                    uint64_t s) {
     for (uint64_t step = 1; step <= mask; ++step) {
-        const uint64_t k = bkeys[s];
-        if (k == key) return bidx[s];
-        if (k == 0) return -1;
+        const Slot e = slot_load(table, s);
+        if (e.key == key) return e.idx;
+        if (e.key == 0) return -1;
         s = (s + 1) & mask;
     }
     return -1;
@@ -66,13 +78,13 @@ __device__ __forceinline__ int lane_id() { return (int) __lane_id(); }
 // Empties the brick table (keys to 0), clears the build's counters and sets
 // the pool's spare row (the empty brick the kernel map reads for a missing
 // neighbour brick) to -1, in one launch.
-__global__ void k_hash_clear(uint64_t * __restrict__ keys, int64_t slots, int32_t * __restrict__ counters,
+__global__ void k_hash_clear(uint64_t * __restrict__ table, int64_t slots, int32_t * __restrict__ counters,
                              int32_t * __restrict__ empty_row) {
     const int64_t stride = (int64_t) gridDim.x * blockDim.x;
     const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (t < kCounterInts) counters[t] = 0;
     if (t < kBrickCells) empty_row[t] = -1;
-    for (int64_t i = t; i < slots; i += stride) keys[i] = 0ull;
+    for (int64_t i = t; i < slots; i += stride) *(U64x2 *) (table + 2 * i) = U64x2{0ull, 0ull};
 }
 
 __global__ void k_fill_i32(int32_t * __restrict__ p, int64_t count, int32_t value) {
@@ -91,9 +103,8 @@ __global__ void k_fill_i32(int32_t * __restrict__ p, int64_t count, int32_t valu
 // needs no global counter and no second round trip; the pool has a row per
 // voxel slot, of which the map reads only the rows of existing bricks.
 __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict__ coords, int64_t n,
-                                                         uint64_t * __restrict__ bkeys, int32_t * __restrict__ bidx,
-                                                         uint64_t mask, int32_t * __restrict__ counters,
-                                                         int32_t * __restrict__ pool) {
+                                                         uint64_t * __restrict__ table, uint64_t mask,
+                                                         int32_t * __restrict__ counters, int32_t * __restrict__ pool) {
     const int64_t i = (int64_t) blockIdx.x * kBlock + threadIdx.x;
     const bool active = i < n;
     uint64_t key = 0;
@@ -125,8 +136,8 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
         s = mix64(key) & mask;
         uint64_t step = 0;
         for (; step <= mask; ++step) {
-            uint64_t prev = __hip_atomic_load(&bkeys[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (prev == 0) prev = atomicCAS((unsigned long long *) &bkeys[s], 0ull, (unsigned long long) key);
+            uint64_t prev = __hip_atomic_load(&table[2 * s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (prev == 0) prev = atomicCAS((unsigned long long *) &table[2 * s], 0ull, (unsigned long long) key);
             if (prev == 0) {
                 won = true;
                 break;
@@ -161,7 +172,7 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
     if (won) {
         idx = (int32_t) blockIdx.x * kBlock + __popcll(wins & below);
         for (int w = 0; w < wave; ++w) idx += s_wave_new[w];
-        bidx[s] = idx;
+        *(int32_t *) (table + 2 * s + 1) = idx;
     }
     // The wavefront's new bricks start empty: lane c clears cell c of each.
     for (uint64_t left = wins; left != 0; left &= left - 1) {
@@ -175,8 +186,7 @@ __global__ void __launch_bounds__(kBlock) k_brick_insert(const int4 * __restrict
 // result is not waited for (the kernel map finds duplicates: a row whose own
 // cell holds another row).
 __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict__ coords, int64_t n,
-                                                         const uint64_t * __restrict__ bkeys,
-                                                         const int32_t * __restrict__ bidx, uint64_t mask,
+                                                         const uint64_t * __restrict__ table, uint64_t mask,
                                                          int32_t * __restrict__ pool, int32_t * __restrict__ counters) {
     const int64_t i = (int64_t) blockIdx.x * kBlock + threadIdx.x;
     if (i >= n) {
@@ -188,9 +198,8 @@ __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict
     // holding another key continues the probe.
     const uint64_t key = brick_key((uint32_t) c.x & 0xffffu, x >> 2, y >> 2, z >> 2);
     const uint64_t hs = mix64(key) & mask;
-    const uint64_t hk = bkeys[hs];
-    const int32_t hi = bidx[hs];
-    const int32_t b = hk == key ? hi : (hk == 0ull ? -1 : brick_find_from(bkeys, bidx, mask, key, (hs + 1) & mask));
+    const Slot h = slot_load(table, hs);
+    const int32_t b = h.key == key ? h.idx : (h.key == 0ull ? -1 : brick_find_from(table, mask, key, (hs + 1) & mask));
     if (b < 0) {
         atomicOr(&counters[4], 2);  // unreachable: every voxel's brick was inserted
         return;
@@ -220,8 +229,7 @@ __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict
 // tile's counts.
 template <bool NBR>
 __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ coords, int64_t n,
-                                                      const uint64_t * __restrict__ bkeys,
-                                                      const int32_t * __restrict__ bidx, uint64_t hmask,
+                                                      const uint64_t * __restrict__ table, uint64_t hmask,
                                                       const int32_t * __restrict__ pool, int32_t empty_brick,
                                                       int32_t * __restrict__ nbr,
                                                       uint32_t * __restrict__ mask_out,
@@ -270,14 +278,15 @@ __global__ void __launch_bounds__(kBlock) k_map_tiles(const int4 * __restrict__ 
             const uint32_t nbz = (bz + (uint32_t) (az * sz)) & 0x3fffu;
             bkey[q] = need ? brick_key(b, nbx, nby, nbz) : 0ull;
             hs[q] = mix64(bkey[q]) & hmask;
-            hkey[q] = bkeys[hs[q]];
-            hidx[q] = bidx[hs[q]];
+            const Slot e = slot_load(table, hs[q]);
+            hkey[q] = e.key;
+            hidx[q] = e.idx;
         }
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             br[q] = -1;
             if (bkey[q] != 0ull && hkey[q] != 0ull) {
-                br[q] = hkey[q] == bkey[q] ? hidx[q] : brick_find_from(bkeys, bidx, hmask, bkey[q], (hs[q] + 1) & hmask);
+                br[q] = hkey[q] == bkey[q] ? hidx[q] : brick_find_from(table, hmask, bkey[q], (hs[q] + 1) & hmask);
             }
         }
         // All 9 z-rows and 9 face cells are loaded before any is used (one
@@ -405,44 +414,44 @@ hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_
 
 int64_t pool_empty_brick(int64_t n) { return (n + kBlock - 1) / kBlock * kBlock; }
 
-hipError_t launch_hash_clear(uint64_t * bkeys, int64_t slots, int32_t * counters, int32_t * pool, int64_t n,
+hipError_t launch_hash_clear(uint64_t * table, int64_t slots, int32_t * counters, int32_t * pool, int64_t n,
                              hipStream_t s) {
     // The grid has at least 256 threads, which covers the counters and the
     // spare pool row.
     static_assert(kCounterInts <= 256 && kBrickCells <= 256, "cleared by the first block");
-    k_hash_clear<<<grid_for(slots, 256, 16384), 256, 0, s>>>(bkeys, slots, counters,
+    k_hash_clear<<<grid_for(slots, 256, 16384), 256, 0, s>>>(table, slots, counters,
                                                              pool + pool_empty_brick(n) * kBrickCells);
     return hipGetLastError();
 }
 
-hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx, int64_t slots,
+hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * table, int64_t slots,
                                int32_t * counters, int32_t * pool, hipStream_t s) {
     const int64_t blocks = (n + kBlock - 1) / kBlock;
-    k_brick_insert<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
+    k_brick_insert<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, table,
                                                         (uint64_t) (slots - 1), counters, pool);
     return hipGetLastError();
 }
 
-hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
+hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * table,
                                int64_t slots, int32_t * pool, int32_t * counters, hipStream_t s) {
     const int64_t blocks = (n + kBlock - 1) / kBlock;
-    k_voxel_insert<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
+    k_voxel_insert<<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, table,
                                                         (uint64_t) (slots - 1), pool, counters);
     return hipGetLastError();
 }
 
-hipError_t launch_map_tiles(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
+hipError_t launch_map_tiles(const int32_t * coords, int64_t n, const uint64_t * table,
                             int64_t slots, const int32_t * pool, int32_t * nbr, uint32_t * mask,
                             int32_t * tile_counts, int32_t * tile_off, int32_t * pair_src, int32_t * pair_dst,
                             int32_t * counters, hipStream_t s) {
     const int64_t blocks = (n + kBlock - 1) / kBlock;
     const int32_t empty = (int32_t) pool_empty_brick(n);
     if (nbr != nullptr) {
-        k_map_tiles<true><<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
+        k_map_tiles<true><<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, table,
                                                                (uint64_t) (slots - 1), pool, empty, nbr, mask,
                                                                tile_counts, tile_off, pair_src, pair_dst, counters);
     } else {
-        k_map_tiles<false><<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, bkeys, bidx,
+        k_map_tiles<false><<<(unsigned) blocks, kBlock, 0, s>>>((const int4 *) coords, n, table,
                                                                 (uint64_t) (slots - 1), pool, empty, nbr, mask,
                                                                 tile_counts, tile_off, pair_src, pair_dst, counters);
     }

@@ -137,8 +137,7 @@ struct trellis_sparse_rulebook {
     tsh::DevMem coords_mem;  // owned copy (empty when borrowed from a C2S map)
     // Brick hash: open-addressed uint64 keys (b, x>>2, y>>2, z>>2)+1 -> brick index.
     int64_t table_slots;
-    tsh::DevMem bkeys;       // uint64 [table_slots]
-    tsh::DevMem bidx;        // int32  [table_slots]
+    tsh::DevMem table;       // brick table: [table_slots] x {uint64 key, int32 idx, pad}
     tsh::DevMem pool;        // int32  [cap_bricks][64] voxel rows, -1 = empty
     tsh::DevMem counters;    // int32  [kCounterInts]: [1] duplicate flag, [4] internal-error flags, [64..] brick counts
     // Kernel map.
@@ -171,22 +170,22 @@ namespace tsh {
 hipError_t launch_fill_i32(int32_t * p, int64_t count, int32_t value, hipStream_t s);
 // Brick table keys to 0 and the build counters (kCounterInts) to 0, one launch.
 // Also sets the pool's spare row (brick pool_empty_brick(n)) to -1.
-hipError_t launch_hash_clear(uint64_t * bkeys, int64_t slots, int32_t * counters, int32_t * pool, int64_t n,
+hipError_t launch_hash_clear(uint64_t * table, int64_t slots, int32_t * counters, int32_t * pool, int64_t n,
                              hipStream_t s);
 // Inserts the voxels' bricks, numbers the new ones (block b's from b * 256)
 // and sets their pool rows to -1.
-hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * bkeys, int32_t * bidx,
+hipError_t launch_brick_insert(const int32_t * coords, int64_t n, uint64_t * table,
                                int64_t slots, int32_t * counters, int32_t * pool, hipStream_t s);
 // Pool rows for n voxels (one per voxel slot of the insert's blocks); the
 // spare row of -1 sits at index pool_empty_brick(n).
 int64_t pool_empty_brick(int64_t n);
 
-hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
+hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t * table,
                                int64_t slots, int32_t * pool, int32_t * counters, hipStream_t s);
 // Neighbour table, masks, per-(tile, offset) counts and list starts, and the
 // pair lists in one pass.  Tile t's lists fill the start of its region
 // [t * kMapTile * 27, (t + 1) * kMapTile * 27) of the pair arrays.
-hipError_t launch_map_tiles(const int32_t * coords, int64_t n, const uint64_t * bkeys, const int32_t * bidx,
+hipError_t launch_map_tiles(const int32_t * coords, int64_t n, const uint64_t * table,
                             int64_t slots, const int32_t * pool, int32_t * nbr, uint32_t * mask,
                             int32_t * tile_counts, int32_t * tile_off, int32_t * pair_src, int32_t * pair_dst,
                             int32_t * counters, hipStream_t s);
