@@ -1080,17 +1080,19 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
                 // A of step g + 2 (fetched DEPTH - 2 steps ago) into the slot
                 // whose fragments every wavefront read before the last
                 // barrier.  Both LDS operations are issued ahead of the MFMAs
-                // so that they run under them.
+                // so that they run under them, and so is the fetch of step
+                // g + DEPTH's A into the register stored two steps ago (0.7 %
+                // faster than after the MFMAs).
                 store_a(s2, ra[(r + 2) % DEPTH]);
+                load_a(ra[r], r);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int q = 0; q < QB; ++q)
 #pragma unroll
                     for (int nt = 0; nt < NT; ++nt)
                         acc[q][nt] = Mfma<DT>::mac(af[r & 1][q], rb[r][nt], acc[q][nt]);
-                // Refill: A of step g + DEPTH, and the next block's weights in
-                // place of the ones just used.
-                load_a(ra[r], r);
+                // Refill: the next block's weights in place of the ones just
+                // used.
                 load_b(rb[r], r);
                 aslot = s1;
                 lds_barrier();
