@@ -357,19 +357,6 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
 #define TSH_STREAM_ROW_GROUPS 8
 #endif
 
-// Lane permute of a 16-byte fragment: lane l receives lane perm/4's value
-// (ds_bpermute per dword; the crossbar, no LDS storage).
-template <typename V> __device__ __forceinline__ V to_mfma_rows(V v, int perm) {
-    typedef int i4 __attribute__((ext_vector_type(4)));
-    const i4 u = __builtin_bit_cast(i4, v);
-    i4 r;
-    r.x = __builtin_amdgcn_ds_bpermute(perm, u.x);
-    r.y = __builtin_amdgcn_ds_bpermute(perm, u.y);
-    r.z = __builtin_amdgcn_ds_bpermute(perm, u.z);
-    r.w = __builtin_amdgcn_ds_bpermute(perm, u.w);
-    return __builtin_bit_cast(V, r);
-}
-
 template <int DT, int BN, int DEPTH, int NW, int RG, int UPB>
 __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Store<DT>::T * __restrict__ x,
                                                                const int32_t * __restrict__ pair_src,
@@ -521,11 +508,12 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     }
     const T * pa[UPB][QB];
     const T * pb[UPB];
-    // A rows are fetched with the lane order of a coalesced load (lane
-    // 4*i + c reads 16 bytes c of row i of the row block: four neighbouring
-    // lanes read one 64-byte segment) and moved to the MFMA operand order
-    // (lane i + 16*c) with cross-lane permutes; an uncoalesced gather of
-    // 16-byte pieces costs the vector memory path four times as much.
+    // A rows are fetched straight in MFMA operand order (lane i + 16 c reads
+    // 16 bytes c of row i of the row block).  Fetching them in the lane order
+    // of a coalesced load (four neighbouring lanes per 64-byte segment) and
+    // moving them to operand order with ds_bpermute moved the vector memory
+    // path's bytes faster in a microbenchmark, but the permutes cost more:
+    // the S2C block's 64 -> 16 conv took 0.304 ms that way, 0.270 ms this way.
     auto target = [&](int tu0, int tps) {
 #pragma unroll
         for (int uo = 0; uo < UPB; ++uo) {
@@ -533,8 +521,8 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
             const int slot = tu & (RING - 1);
 #pragma unroll
             for (int q = 0; q < QB; ++q) {
-                const int32_t src = s_rsrc[slot][(rh + RG * q) * 16 + (lane >> 2)];
-                pa[uo][q] = x + (int64_t) src * ci + tps * BK + (lane & 3) * 8;
+                const int32_t src = s_rsrc[slot][(rh + RG * q) * 16 + l16];
+                pa[uo][q] = x + (int64_t) src * ci + tps * BK + lg * 8;
             }
             pb[uo] = w16 + ((int64_t) (s_uk[tu] * ci8 + tps * 4) * co + col0) * 8;
         }
@@ -557,8 +545,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
         }
     };
 
-    const int perm = (4 * l16 + lg) * 4;  // byte address of the source lane for to_mfma_rows
-    V ra[DEPTH][QB];  // A as loaded (coalesced lane order)
+    V ra[DEPTH][QB];  // A fragments in flight
     V rw[DEPTH][BLOADS];
     V rf[2][NT];  // weight fragments of step g in rf[g & 1]
     f32x4 acc[QB][NT];
@@ -669,7 +656,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
                 for (int q = 0; q < QB; ++q)
 #pragma unroll
                     for (int nt = 0; nt < NT; ++nt)
-                        acc[q][nt] = Mfma<DT>::mac(to_mfma_rows<V>(ra[r][q], perm), rf[r & 1][nt], acc[q][nt]);
+                        acc[q][nt] = Mfma<DT>::mac(ra[r][q], rf[r & 1][nt], acc[q][nt]);
                 // Weights of step g + 2 (fetched two steps ago) into the slot
                 // whose fragments every wavefront read before the last barrier.
                 store_b(s2, rw[(r + 2) % DEPTH]);
