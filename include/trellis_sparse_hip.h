@@ -299,11 +299,14 @@ trellis_status trellis_sparse_hip_free_c2s_map(trellis_sparse_backend * backend,
  * serving loops, harnesses that forbid hipMalloc).  It calls no hipMalloc,
  * hipFree or other allocating routine: its working memory (per-parent child
  * counts and their scan) is a fixed device array of about 8 MB per GPU,
- * held until the process ends and shared by every call on that GPU, so calls
- * that overlap on one GPU (e.g. two backends on different streams) race.
+ * held until the process ends and shared by every call on that GPU.  Calls
+ * on one GPU are ordered: a call holds a per-GPU lock for its duration, and
+ * its kernels wait (on its backend's stream) for the previous call's fill,
+ * so concurrent callers on other threads or streams wait their turn.
  *   coords      int32 buffer (upload_i32) of the n parents' (b, x, y, z)
  *   logits      [n][8] buffer in the backend's compute_dtype; child s of
- *               parent p exists iff logits[p][s] > 0 (executor.c:108-154)
+ *               parent p exists iff logits[p][s] > 0, exactly as in
+ *               build_c2s_map_device
  *   coords_out  int32 buffer of >= 4 m entries, parent_out / subidx_out
  *               int32 buffers of >= m entries; children parent-major,
  *               subidx ascending, coordinates (b, 2x+(s&1), 2y+((s>>1)&1),

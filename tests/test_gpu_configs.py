@@ -6,6 +6,10 @@ At full size the oracle (trellis_sparse_cpu.c:324-373 restated) runs on a
 strided sample of output rows, from the same rounded inputs the backend
 reads; the sampled rows are compared to the storage tolerance of
 tests/test_sparse_decoder_backend.c:16-24 (|a-b| <= 2e-2 max(1,|a|,|b|)).
+For configs 4 and 5 the stride is 255 rows plus the last row, so every
+256-row map tile (the kernels' unit of work) holds at least one sampled row,
+including the last, partial tile, and the sampled positions within a tile
+cycle through all 256 (both half tiles of the 256-channel blocks).
 
   config 2  conv(128->128) -> LayerNorm -> SiLU -> conv(128->128) + skip, fp16,
             419,340 voxels: each fused launch against the oracle, the second
@@ -13,8 +17,11 @@ tests/test_sparse_decoder_backend.c:16-24 (|a-b| <= 2e-2 max(1,|a|,|b|)).
   config 4  conv 64->64 bf16 on the 3,788,747-voxel R=1024 shell set
   config 5  conv 512->512 bf16 on the four batched structures (327,680 voxels)
 
-The deep-channel cases run Ci = 384, 512 and 1024 with 64- and 128-channel
-output blocks on ragged row counts: with Ci >= 512 (or Ci = 384) one unit of
+The deep-channel cases include the decoder's own widths
+(sparse_unet_decoder/decoder.c:248-249, the C2S conv Ci -> 8 Co of
+executor.c:456): 1024 -> 1024 (the level-0 ConvNeXt conv), 512 -> 2048 and
+1024 -> 4096 (levels 1 and 0 of the upsample).  They run Ci = 384, 512 and
+1024 with 64- and 128-channel output blocks on ragged row counts: with Ci >= 512 (or Ci = 384) one unit of
 128 pairs takes more than one block of 8 (or 4) K steps, so the kernels'
 mid-unit block prefetch is executed.  Co % 256 == 0 (with Ci % 128 == 0) runs
 256-channel blocks over half map tiles: those cases include a last tile whose
@@ -80,11 +87,19 @@ def test_config_conv_full_size_vs_oracle_sample(backends, cfg):
     got = be.download(yb).reshape(n, co)
     del xb, yb
     assert np.all(np.isfinite(got))
-    rows = sample_rows(n, 5000 if ci * co <= 8192 else 900)
+    # One row in every 255: each 256-row tile holds a sampled row, at a
+    # position that moves by one per tile; plus the last row.
+    rows = (3, n, 255)
     orb = orc.Rulebook(coords)
     exp = orb.conv(x, wr, bias, ci, co, rows=rows)
     err = max_rel_err(got[rows[0]:rows[1]:rows[2]], exp)
-    say(f"cfg{cfg} full conv pairs={stats['pairs']} sampled rows={exp.shape[0]} max_rel_err={err:.3e}")
+    exp_last = orb.conv(x, wr, bias, ci, co, rows=(n - 1, n, 1))
+    err = max(err, max_rel_err(got[n - 1:n], exp_last))
+    tiles = (n + 255) // 256
+    sampled_tiles = np.unique(np.concatenate([np.arange(rows[0], n, rows[2]), [n - 1]]) // 256)
+    assert sampled_tiles.size == tiles
+    say(f"cfg{cfg} full conv pairs={stats['pairs']} sampled rows={exp.shape[0] + 1} of {tiles} tiles "
+        f"max_rel_err={err:.3e}")
     assert err <= 2e-2
     rb.free()
 
@@ -129,7 +144,8 @@ def test_config2_fused_block_full_size_vs_oracle_sample(backends):
 
 
 DEEP_CASES = [(512, 128, 3001), (384, 128, 2000), (1024, 128, 1200), (512, 64, 2500), (1024, 64, 1777),
-              (512, 512, 1300), (128, 256, 900), (256, 1024, 600), (384, 256, 1500), (256, 256, 200)]
+              (512, 512, 1300), (128, 256, 900), (256, 1024, 600), (384, 256, 1500), (256, 256, 200),
+              (1024, 1024, 700), (512, 2048, 650), (1024, 4096, 520)]
 
 
 @pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])
@@ -146,7 +162,7 @@ def test_conv_deep_channels_vs_oracle(backends, dtype, ci, co, n):
     xb, yb = be.upload(x), be.alloc(n * co)
     be.conv(rb, xb, w, bias, yb, ci, co)
     got = be.download(yb).reshape(n, co)
-    rows = sample_rows(n, 400)
+    rows = sample_rows(n, 400 if ci * co <= 512 * 1024 else 120)
     exp = orc.Rulebook(coords).conv(x, w, bias, ci, co, rows=rows)
     err = max_rel_err(got[rows[0]:rows[1]:rows[2]], exp)
     say(f"deep conv dtype={dtype} ci={ci} co={co} n={n} rows={exp.shape[0]} max_rel_err={err:.3e}")

@@ -3,7 +3,9 @@ against the allocating entry point it is a variant of, build_c2s_map_device
 (src/architectures/sparse_unet_decoder/executor.c:108-154 semantics): the
 same children, bit for bit, on two calls in a row, the second with fewer
 parents than the first (its scratch keeps the first call's counts beyond
-the second's parents, which must not leak into the result); then the
+the second's parents, which must not leak into the result), and with every
+device allocation attempt failing (the backend's allocation-failure hook
+after its buffer pool is emptied), which the call must not notice; then the
 argument errors: more parents than its scratch holds, outputs smaller than
 the child count (reported in n_out), no children."""
 import sys
@@ -38,7 +40,13 @@ def test_build_c2s_map_into_matches_device_map(dtype):
             oc = be.upload_i32(np.full(4 * cap, -7, np.int32))
             op = be.upload_i32(np.full(cap, -7, np.int32))
             os_ = be.upload_i32(np.full(cap, -7, np.int32))
-            m = be.build_c2s_map_into(cb, lgb, npar, oc, op, os_)
+            # Every device allocation fails from here: the call allocates nothing.
+            be.trim(sh.TRIM_FREE_BUFFERS)
+            be.fail_alloc(0)
+            try:
+                m = be.build_c2s_map_into(cb, lgb, npar, oc, op, os_)
+            finally:
+                be.fail_alloc(-1)
             say(f"build_c2s_map_into dtype={dtype} parents={npar}: {m} children (device map {dm.n})")
             assert m == dm.n
             assert np.array_equal(be.download_i32(oc, 4 * m).reshape(m, 4), ec)

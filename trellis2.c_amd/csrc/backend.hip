@@ -12,6 +12,7 @@
 // independent.  Every call enqueues on the instance's own stream; calls that
 // hand data back to the host (download_*, build_c2s_map*, n_out) synchronise.
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -57,6 +58,8 @@ struct StageMark {
     int stage = 0;
 };
 
+struct IntoScratch;
+
 struct Backend {
     trellis_sparse_backend base;
     int device = 0;
@@ -76,7 +79,7 @@ struct Backend {
     int64_t alloc_attempts = 0;
     // Device address of this device's copy of `scratch` (the allocation-free
     // subdivide's working memory), or null when it could not be resolved.
-    unsigned char * scratch_dev = nullptr;
+    IntoScratch * into = nullptr;  // build_c2s_map_into's scratch on this backend's device
     // Weight cache.
     std::unordered_map<WeightKey, DevMem, WeightKeyHash> weights;
     std::vector<DevMem> transient;  // uncached weights of the current call
@@ -114,24 +117,37 @@ constexpr size_t kIntoSums = kIntoTotal + 256;                           // scan
 constexpr size_t kIntoScratchBytes = kIntoSums + 16384;
 static __device__ __align__(256) unsigned char scratch[kIntoScratchBytes];
 
-// Resolves this device's copy of `scratch` once per device (the caller has
-// made `device` current).  Returns null on failure.
-unsigned char * scratch_address(int device) {
+// Per device: the address of its copy of `scratch`, and the lock and event
+// that order calls on that device (each call waits, on its own stream, for
+// the previous call's last kernel, which still reads the scratch after the
+// previous call returned).
+struct IntoScratch {
+    unsigned char * addr = nullptr;
+    hipEvent_t done = nullptr;
+    std::mutex mu;
+};
+
+// Resolves this device's copy of `scratch` and creates its event, once per
+// device (the caller has made `device` current).  Returns null on failure.
+IntoScratch * scratch_for(int device) {
     constexpr int kMaxDevices = 64;
     static std::mutex mu;
-    static unsigned char * addr[kMaxDevices] = {};
+    static IntoScratch dev[kMaxDevices];
     if (device < 0 || device >= kMaxDevices) return nullptr;
     std::lock_guard<std::mutex> lock(mu);
-    if (addr[device] == nullptr) {
+    IntoScratch & d = dev[device];
+    if (d.addr == nullptr) {
         void * p = nullptr;
-        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (err != hipSuccess || p == nullptr) {
+        hipEvent_t e = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr ||
+            hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
             (void) hipGetLastError();
             return nullptr;
         }
-        addr[device] = (unsigned char *) p;
+        d.done = e;
+        d.addr = (unsigned char *) p;
     }
-    return addr[device];
+    return &d;
 }
 
 namespace {
@@ -264,10 +280,13 @@ trellis_status pinned_reserve(Backend * be, size_t bytes) {
 
 // Reads up to kHostWords int32 values from device memory (one or two source
 // ranges) into host variables, through the backend's pinned words: the
-// copies write host memory directly, and the host spins on an event, so it
-// resumes within microseconds of the copy, where a blocking stream
-// synchronisation and a pageable destination cost tens of microseconds.
-// The queue is drained up to the copy, as hipStreamSynchronize would.
+// copies write host memory directly, and the host polls an event for up to
+// kSpinMicros, so it resumes within microseconds of a short wait, where a
+// blocking stream synchronisation and a pageable destination cost tens of
+// microseconds; longer waits (work still queued ahead of the copy) block in
+// hipEventSynchronize instead of spinning.  The queue is drained up to the
+// copy, as hipStreamSynchronize would.
+constexpr int kSpinMicros = 50;
 constexpr int kHostWords = 16;
 hipError_t read_words(Backend * be, hipStream_t s, int32_t * dst0, const void * src0, int count0,
                       int32_t * dst1 = nullptr, const void * src1 = nullptr, int count1 = 0) {
@@ -283,7 +302,12 @@ hipError_t read_words(Backend * be, hipStream_t s, int32_t * dst0, const void * 
     }
     if (err == hipSuccess) err = hipEventRecord(be->words_ready, s);
     if (err != hipSuccess) return err;
+    const auto spin_end = std::chrono::steady_clock::now() + std::chrono::microseconds(kSpinMicros);
     while ((err = hipEventQuery(be->words_ready)) == hipErrorNotReady) {
+        if (std::chrono::steady_clock::now() >= spin_end) {
+            err = hipEventSynchronize(be->words_ready);
+            break;
+        }
     }
     (void) hipGetLastError();  // the not-ready polls are not errors
     if (err != hipSuccess) return err;
@@ -1822,7 +1846,7 @@ trellis_status trellis_sparse_hip_backend_create_ex(int device, const trellis_sp
     be->base.device = device;
     be->device = device;
     be->policy = p;
-    be->scratch_dev = tsh::scratch_address(device);
+    be->into = tsh::scratch_for(device);
     // TRELLIS_HIP_FAIL_ALLOC_AFTER=N[,K]: the device allocation attempts after
     // the first N fail (K of them, default all), for out-of-memory tests.
     if (const char * env = getenv("TRELLIS_HIP_FAIL_ALLOC_AFTER")) {
@@ -2037,19 +2061,24 @@ trellis_status trellis_sparse_hip_build_c2s_map_into(trellis_sparse_backend * ba
         return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT,
                     "build_c2s_map_into: more than 1048576 parents (the size of its fixed scratch)");
     }
-    if (be->scratch_dev == nullptr) {
+    if (be->into == nullptr) {
         return fail(be, TRELLIS_STATUS_ERROR, "build_c2s_map_into: scratch address unavailable on this device");
     }
     select_device(be);
     hipStream_t s = be->stream;
-    int32_t * counts = (int32_t *) (be->scratch_dev + kIntoCounts);
-    int32_t * offsets = (int32_t *) (be->scratch_dev + kIntoOffsets);
-    int32_t * total = (int32_t *) (be->scratch_dev + kIntoTotal);
-    void * sums = be->scratch_dev + kIntoSums;
+    IntoScratch & sc = *be->into;
+    // One call at a time per device; this call's kernels start after the
+    // previous call's fill, whatever stream it ran on.
+    std::lock_guard<std::mutex> lock(sc.mu);
+    int32_t * counts = (int32_t *) (sc.addr + kIntoCounts);
+    int32_t * offsets = (int32_t *) (sc.addr + kIntoOffsets);
+    int32_t * total = (int32_t *) (sc.addr + kIntoTotal);
+    void * sums = sc.addr + kIntoSums;
     static_assert(kIntoSums + (kIntoMaxParents / 2048 + 2) * 4 <= kIntoScratchBytes, "scan sums fit");
     // Every counts and offsets entry below n, the total and the tile sums
     // are written before they are read, so nothing needs clearing.
-    hipError_t err = launch_c2s_count(be->policy.compute_dtype, logits->ptr, n, counts, s);
+    hipError_t err = hipStreamWaitEvent(s, sc.done, 0);
+    if (err == hipSuccess) err = launch_c2s_count(be->policy.compute_dtype, logits->ptr, n, counts, s);
     if (err == hipSuccess) err = launch_scan_exclusive(counts, offsets, n, total, sums, s);
     int32_t m = 0;
     if (err == hipSuccess) err = read_words(be, s, &m, total, 1);
@@ -2059,8 +2088,10 @@ trellis_status trellis_sparse_hip_build_c2s_map_into(trellis_sparse_backend * ba
     if (coords_out->count < (size_t) m * 4 || parent_out->count < (size_t) m || subidx_out->count < (size_t) m) {
         return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "build_c2s_map_into: outputs hold fewer than n_out children");
     }
+    // (The returns above follow read_words, which waited for count and scan.)
     err = launch_c2s_fill(be->policy.compute_dtype, (const int32_t *) coords->ptr, logits->ptr, offsets, n,
                           (int32_t *) coords_out->ptr, (int32_t *) parent_out->ptr, (int32_t *) subidx_out->ptr, s);
+    if (err == hipSuccess) err = hipEventRecord(sc.done, s);
     return hip_status(be, err, "build_c2s_map_into: fill");
 }
 

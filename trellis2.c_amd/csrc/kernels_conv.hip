@@ -1217,6 +1217,10 @@ __global__ void __launch_bounds__(256, 2) k_conv_os64(const typename Store<DT>::
     using T = typename Store<DT>::T;
     using V = typename Mfma<DT>::V;
     constexpr int CI = 64, CO = 64;
+    // The weights come in conv_stream_group(64, 64)'s packing, which this
+    // kernel reads with g = 4: lane l16 owns channels 4 l16 .. 4 l16 + 3.
+    static_assert(64 / (TSH_STREAM_WAVES / TSH_STREAM_ROW_GROUPS) / 16 == 4,
+                  "k_conv_os64 needs the 64-channel grouped packing with g = 4");
     constexpr int QB = 4;                      // row blocks per wavefront
     constexpr int NT = CO / 16;                // column tiles (grouped packing: lane's NT columns adjacent)
     constexpr int WSLOT = (CI / 8) * CO * 8;   // weight elements per offset
