@@ -1,0 +1,438 @@
+/*
+ * encoder_conformance.c - a compiled C caller of include/trellis_sparse_hip.h.
+ *
+ * Runs a sparse U-Net encoder through backend->ops, slot by slot in the order
+ * of the reference executor (src/architectures/sparse_unet_encoder/
+ * executor.c:392-649: input linear, rulebook, per level the ConvNeXt blocks
+ * (:27-134) and the S2C down-block (:160-360), output head row_norm eps 1e-5
+ * -> linear to 2*latent channels of which the first latent are kept
+ * (:546-603)).  The down-block's host steps - trellis_sparse_s2c_host_build
+ * and the download / pack / skip-mean / upload round trip (executor.c:
+ * 209-300) - run on the device through trellis_sparse_hip_s2c_build_device,
+ * _s2c_pack_device and _s2c_skip_mean_device; the coarse rulebook comes from
+ * the coarse device map (build_rulebook_for_c2s_map) and the output
+ * coordinates from download_c2s_coords.
+ *
+ * Checked against the same chain on the CPU oracle (oracle/trellis_oracle.h)
+ * with the storage rounding after every slot that stores: the output
+ * coordinates and every level's guide (download_c2s_map of the level's fine
+ * map: fine coordinates, parent, subidx) bit for bit, the last level's
+ * features and the latent within tolerance.
+ *
+ * Models:
+ *   tiny    the reference test's weights and voxels (tests/
+ *           test_sparse_encoder_backend.c:15-61, :84-110): in 2, channels
+ *           2 -> 8, no ConvNeXt blocks, latent 1.  Also checked against that
+ *           test's known answers (:139-161): 3 coarse voxels, their
+ *           coordinates, the guide's parent/subidx, the coarse features
+ *           (exact: the convs have zero weights, so the block's output is the
+ *           skip mean) and the latent against its closed form, the first
+ *           channel of LN(features) plus the bias 0.125, within 3e-4.
+ *   medium  in 6, channels 32 -> 64 -> 128, one ConvNeXt block per level,
+ *           latent 8, seeded weights, on a sphere shell of ~4k voxels.
+ *
+ * Usage: encoder_conformance <tiny|medium> <f32|bf16> [oracle]
+ *   oracle: no device; the oracle chain alone (tiny: against the known
+ *   answers).
+ * Exit 0 = pass, 1 = mismatch or error, 77 = no HIP device (skipped).
+ */
+#include "conformance_common.h"
+
+#define ENC_LEVELS 3
+
+/* ------------------------------------------------------------------ model */
+
+typedef struct down_w {
+    int ci, co;
+    float *norm1_g, *norm1_b, *conv1_w, *conv1_b, *conv2_w, *conv2_b;
+} down_w;
+
+typedef struct enc_model {
+    int in_c, latent, levels;
+    int channels[ENC_LEVELS], blocks[ENC_LEVELS];
+    float *input_w, *input_b, *to_latent_w, *to_latent_b;
+    block_w block[ENC_LEVELS];
+    down_w down[ENC_LEVELS - 1];
+} enc_model;
+
+static void down_alloc(down_w * d, int ci, int co) {
+    d->ci = ci, d->co = co;
+    d->norm1_g = fvec(ci), d->norm1_b = fvec(ci);
+    d->conv1_w = fvec((size_t) (co / 8) * 27 * ci), d->conv1_b = fvec(co / 8);
+    d->conv2_w = fvec((size_t) co * 27 * co), d->conv2_b = fvec(co);
+}
+
+/* test_sparse_encoder_backend.c:15-61: identity input linear, unit norm1
+ * gain, zero convs, to_latent picks channel 0 and adds 0.125. */
+static void model_tiny(enc_model * m) {
+    memset(m, 0, sizeof(*m));
+    m->in_c = 2, m->latent = 1, m->levels = 2;
+    m->channels[0] = 2, m->channels[1] = 8;
+    m->input_w = fvec(4), m->input_b = fvec(2);
+    m->input_w[0] = 1.0f, m->input_w[3] = 1.0f;
+    down_alloc(&m->down[0], 2, 8);
+    m->down[0].norm1_g[0] = 1.0f, m->down[0].norm1_g[1] = 1.0f;
+    m->to_latent_w = fvec(2 * 8), m->to_latent_b = fvec(2);
+    m->to_latent_w[0] = 1.0f;
+    m->to_latent_b[0] = 0.125f;
+}
+
+static void model_medium(enc_model * m) {
+    memset(m, 0, sizeof(*m));
+    m->in_c = 6, m->latent = 8, m->levels = 3;
+    for (int l = 0; l < 3; ++l) {
+        m->channels[l] = 32 << l;
+        m->blocks[l] = 1;
+        block_rand(&m->block[l], m->channels[l]);
+    }
+    m->input_w = fvec(32 * 6), m->input_b = fvec(32);
+    fill_rand(m->input_w, 32 * 6, 1.7f / sqrtf(6.0f));
+    fill_rand(m->input_b, 32, 0.05f);
+    for (int l = 0; l < 2; ++l) {
+        down_w * d = &m->down[l];
+        const int ci = m->channels[l], co = m->channels[l + 1];
+        down_alloc(d, ci, co);
+        for (int i = 0; i < ci; ++i) d->norm1_g[i] = 1.0f + urand(0.1f), d->norm1_b[i] = urand(0.1f);
+        fill_rand(d->conv1_w, (size_t) (co / 8) * 27 * ci, 1.7f / sqrtf(27.0f * ci));
+        fill_rand(d->conv1_b, co / 8, 0.05f);
+        fill_rand(d->conv2_w, (size_t) co * 27 * co, 1.7f / sqrtf(27.0f * co));
+        fill_rand(d->conv2_b, co, 0.05f);
+    }
+    m->to_latent_w = fvec(16 * 128), m->to_latent_b = fvec(16);
+    fill_rand(m->to_latent_w, 16 * 128, 1.7f / sqrtf(128.0f));
+    fill_rand(m->to_latent_b, 16, 0.05f);
+}
+
+/* One pass's result, guides in down order (level 0 = the input voxels; the
+ * reference hands them back coarsest first, executor.c:377-390). */
+typedef struct enc_out {
+    int64_t n;
+    int32_t * coords; /* [n][4] */
+    float * h;        /* [n][channels[levels-1]], the input of the head */
+    float * latent;   /* [n][latent] */
+    int n_guides;
+    int64_t guide_n[ENC_LEVELS - 1];
+    int32_t *guide_coords[ENC_LEVELS - 1], *guide_parent[ENC_LEVELS - 1], *guide_subidx[ENC_LEVELS - 1];
+} enc_out;
+
+static void enc_out_free(enc_out * eo) {
+    free(eo->coords), free(eo->h), free(eo->latent);
+    for (int i = 0; i < eo->n_guides; ++i) free(eo->guide_coords[i]), free(eo->guide_parent[i]), free(eo->guide_subidx[i]);
+    memset(eo, 0, sizeof(*eo));
+}
+
+/* ------------------------------------------------- device pass (the ops) */
+
+/* The S2C down-block (executor.c:160-360): out = conv2(silu(LN(pack(conv1(
+ * silu(LN(h))))))) + skip_mean(h) on the coarse voxels, with the S2C relation
+ * built on the device from host coordinates (level 0) or the previous level's
+ * coarse map. */
+static int down_dev(trellis_sparse_backend * be, const down_w * d, const int32_t * host_coords,
+                    const trellis_sparse_c2s_device_map * coords_map, int64_t n, const trellis_sparse_rulebook * rb,
+                    trellis_sparse_buffer ** hp, trellis_sparse_c2s_device_map ** fine_map,
+                    trellis_sparse_c2s_device_map ** coarse_map, trellis_sparse_rulebook ** coarse_rb,
+                    int64_t * coarse_n) {
+    const trellis_sparse_backend_ops * ops = be->ops;
+    const int ci = d->ci, co = d->co, pc = d->co / 8;
+    trellis_sparse_buffer * h = *hp;
+    trellis_sparse_buffer *norm1 = NULL, *conv1 = NULL, *packed = NULL, *skip = NULL, *norm2 = NULL, *conv2 = NULL,
+                          *out = NULL;
+    CHECK_OK(be, trellis_sparse_hip_s2c_build_device(be, host_coords, coords_map, n, fine_map, coarse_map, coarse_n));
+    const int64_t m = *coarse_n;
+    CHECK_OK(be, ops->alloc_f32(be, (size_t) n * ci, &norm1));
+    CHECK_OK(be, ops->row_norm_silu(be, h, d->norm1_g, d->norm1_b, norm1, n, ci, 1e-6f));
+    CHECK_OK(be, ops->alloc_f32(be, (size_t) n * pc, &conv1));
+    CHECK_OK(be, ops->sparse_conv3d(be, rb, norm1, d->conv1_w, d->conv1_b, conv1, n, ci, pc));
+    ops->free_buffer(be, norm1);
+    CHECK_OK(be, ops->alloc_f32(be, (size_t) m * co, &packed));
+    CHECK_OK(be, trellis_sparse_hip_s2c_pack_device(be, conv1, *fine_map, packed, co));
+    ops->free_buffer(be, conv1);
+    CHECK_OK(be, ops->alloc_f32(be, (size_t) m * co, &skip));
+    CHECK_OK(be, trellis_sparse_hip_s2c_skip_mean_device(be, h, *fine_map, skip, ci, co));
+    CHECK_OK(be, ops->build_rulebook_for_c2s_map(be, *coarse_map, coarse_rb));
+    CHECK_OK(be, ops->alloc_f32(be, (size_t) m * co, &norm2));
+    CHECK_OK(be, ops->row_norm_silu(be, packed, NULL, NULL, norm2, m, co, 1e-6f));
+    ops->free_buffer(be, packed);
+    CHECK_OK(be, ops->alloc_f32(be, (size_t) m * co, &conv2));
+    CHECK_OK(be, ops->sparse_conv3d(be, *coarse_rb, norm2, d->conv2_w, d->conv2_b, conv2, m, co, co));
+    ops->free_buffer(be, norm2);
+    CHECK_OK(be, ops->alloc_f32(be, (size_t) m * co, &out));
+    CHECK_OK(be, ops->add(be, conv2, skip, out, (size_t) m * co));
+    ops->free_buffer(be, conv2);
+    ops->free_buffer(be, skip);
+    ops->free_buffer(be, h);
+    *hp = out;
+    return 1;
+}
+
+/* Head of executor.c:546-603: LN (no affine, eps 1e-5), linear to the
+ * posterior's 2*latent channels, keep the first latent (the mean). */
+static int head_dev(trellis_sparse_backend * be, const enc_model * m, trellis_sparse_buffer * h, int64_t n,
+                    enc_out * eo) {
+    const trellis_sparse_backend_ops * ops = be->ops;
+    const int c = m->channels[m->levels - 1], pc = 2 * m->latent;
+    trellis_sparse_buffer *norm = NULL, *post = NULL;
+    eo->h = fvec((size_t) n * c);
+    CHECK_OK(be, ops->download_f32(be, h, eo->h, (size_t) n * c));
+    CHECK_OK(be, ops->alloc_f32(be, (size_t) n * c, &norm));
+    CHECK_OK(be, ops->alloc_f32(be, (size_t) n * pc, &post));
+    CHECK_OK(be, ops->row_norm(be, h, NULL, NULL, norm, n, c, 1e-5f));
+    CHECK_OK(be, ops->linear(be, norm, m->to_latent_w, m->to_latent_b, post, n, c, pc));
+    float * host = fvec((size_t) n * pc);
+    CHECK_OK(be, ops->download_f32(be, post, host, (size_t) n * pc));
+    eo->latent = fvec((size_t) n * m->latent);
+    for (int64_t r = 0; r < n; ++r) memcpy(eo->latent + r * m->latent, host + r * pc, (size_t) m->latent * 4);
+    free(host);
+    ops->free_buffer(be, norm);
+    ops->free_buffer(be, post);
+    return 1;
+}
+
+static int encode_dev(trellis_sparse_backend * be, const enc_model * m, const int32_t * coords, const float * feats,
+                      int64_t n, enc_out * eo) {
+    const trellis_sparse_backend_ops * ops = be->ops;
+    memset(eo, 0, sizeof(*eo));
+    trellis_sparse_buffer *in = NULL, *h = NULL;
+    trellis_sparse_rulebook * rb = NULL;
+    trellis_sparse_c2s_device_map * cur_map = NULL; /* coordinates of the current level once below level 0 */
+    int64_t cur_n = n;
+    CHECK_OK(be, ops->upload_f32(be, feats, (size_t) n * m->in_c, &in));
+    CHECK_OK(be, ops->alloc_f32(be, (size_t) n * m->channels[0], &h));
+    CHECK_OK(be, ops->linear(be, in, m->input_w, m->input_b, h, n, m->in_c, m->channels[0]));
+    ops->free_buffer(be, in);
+    CHECK_OK(be, ops->build_rulebook(be, coords, n, &rb));
+    for (int level = 0; level < m->levels; ++level) {
+        for (int i = 0; i < m->blocks[level]; ++i) CHECK(convnext_dev(be, &m->block[level], rb, &h, cur_n));
+        if (level == m->levels - 1) break;
+        trellis_sparse_c2s_device_map *fine_map = NULL, *coarse_map = NULL;
+        trellis_sparse_rulebook * coarse_rb = NULL;
+        int64_t coarse_n = 0;
+        CHECK(down_dev(be, &m->down[level], level == 0 ? coords : NULL, cur_map, cur_n, rb, &h, &fine_map,
+                       &coarse_map, &coarse_rb, &coarse_n));
+        /* The guide of this level (encoder_copy_guide, executor.c:136-158). */
+        const int g = eo->n_guides++;
+        eo->guide_n[g] = cur_n;
+        eo->guide_coords[g] = ivec((size_t) cur_n * 4);
+        eo->guide_parent[g] = ivec((size_t) cur_n);
+        eo->guide_subidx[g] = ivec((size_t) cur_n);
+        CHECK_OK(be, ops->download_c2s_map(be, fine_map, eo->guide_coords[g], eo->guide_parent[g],
+                                           eo->guide_subidx[g], cur_n));
+        /* The level's rulebook borrows cur_map's coordinates: free it first. */
+        ops->free_rulebook(be, rb);
+        CHECK_OK(be, trellis_sparse_hip_free_c2s_map(be, fine_map));
+        if (cur_map != NULL) CHECK_OK(be, trellis_sparse_hip_free_c2s_map(be, cur_map));
+        rb = coarse_rb;
+        cur_map = coarse_map;
+        cur_n = coarse_n;
+    }
+    CHECK(head_dev(be, m, h, cur_n, eo));
+    ops->free_buffer(be, h);
+    ops->free_rulebook(be, rb);
+    eo->n = cur_n;
+    eo->coords = ivec((size_t) cur_n * 4);
+    if (cur_map != NULL) {
+        CHECK_OK(be, ops->download_c2s_coords(be, cur_map, eo->coords, cur_n));
+        CHECK_OK(be, trellis_sparse_hip_free_c2s_map(be, cur_map));
+    } else {
+        memcpy(eo->coords, coords, (size_t) n * 16);
+    }
+    return 1;
+}
+
+/* ------------------------------------------------- oracle chain (the CPU) */
+
+static int encode_orc(const enc_model * m, const int32_t * coords, const float * feats, int64_t n, enc_out * eo) {
+    memset(eo, 0, sizeof(*eo));
+    float * in = fvec((size_t) n * m->in_c);
+    memcpy(in, feats, (size_t) n * m->in_c * sizeof(float));
+    round_store(in, (size_t) n * m->in_c);
+    float * h = fvec((size_t) n * m->channels[0]);
+    orc_linear(in, m->input_w, m->input_b, h, n, m->in_c, m->channels[0], 0);
+    round_store(h, (size_t) n * m->channels[0]);
+    free(in);
+    int32_t * cur = ivec((size_t) n * 4);
+    memcpy(cur, coords, (size_t) n * 16);
+    int64_t cur_n = n;
+    for (int level = 0; level < m->levels; ++level) {
+        for (int i = 0; i < m->blocks[level]; ++i) CHECK(convnext_orc(&m->block[level], cur, cur_n, &h));
+        if (level == m->levels - 1) break;
+        const down_w * d = &m->down[level];
+        const int ci = d->ci, co = d->co, pc = d->co / 8;
+        int32_t *cc = NULL, *pp = NULL, *ss = NULL;
+        int64_t cn = 0;
+        CHECK(orc_s2c_map(cur, cur_n, &cc, &pp, &ss, &cn) == 0);
+        float * norm1 = fvec((size_t) cur_n * ci);
+        orc_row_norm(h, d->norm1_g, d->norm1_b, norm1, cur_n, ci, 1e-6f, 1);
+        round_store(norm1, (size_t) cur_n * ci);
+        float * conv1 = fvec((size_t) cur_n * pc);
+        CHECK(conv_orc(cur, cur_n, norm1, d->conv1_w, d->conv1_b, conv1, ci, pc));
+        float * packed = fvec((size_t) cn * co);
+        orc_s2c_pack(conv1, pp, ss, packed, cur_n, cn, co);
+        float * skip = fvec((size_t) cn * co);
+        orc_s2c_skip_mean(h, pp, ss, skip, cur_n, cn, ci, co);
+        round_store(skip, (size_t) cn * co);
+        float * norm2 = fvec((size_t) cn * co);
+        orc_row_norm(packed, NULL, NULL, norm2, cn, co, 1e-6f, 1);
+        round_store(norm2, (size_t) cn * co);
+        float * conv2 = fvec((size_t) cn * co);
+        CHECK(conv_orc(cc, cn, norm2, d->conv2_w, d->conv2_b, conv2, co, co));
+        float * out = fvec((size_t) cn * co);
+        orc_add(conv2, skip, out, (size_t) cn * co);
+        round_store(out, (size_t) cn * co);
+        free(norm1), free(conv1), free(packed), free(skip), free(norm2), free(conv2), free(h);
+        h = out;
+        const int g = eo->n_guides++;
+        eo->guide_n[g] = cur_n;
+        eo->guide_coords[g] = cur;
+        eo->guide_parent[g] = pp;
+        eo->guide_subidx[g] = ss;
+        cur = cc;
+        cur_n = cn;
+    }
+    const int c = m->channels[m->levels - 1], pc = 2 * m->latent;
+    float * norm = fvec((size_t) cur_n * c);
+    orc_row_norm(h, NULL, NULL, norm, cur_n, c, 1e-5f, 0);
+    round_store(norm, (size_t) cur_n * c);
+    float * post = fvec((size_t) cur_n * pc);
+    orc_linear(norm, m->to_latent_w, m->to_latent_b, post, cur_n, c, pc, 0);
+    round_store(post, (size_t) cur_n * pc);
+    eo->latent = fvec((size_t) cur_n * m->latent);
+    for (int64_t r = 0; r < cur_n; ++r) memcpy(eo->latent + r * m->latent, post + r * pc, (size_t) m->latent * 4);
+    free(norm), free(post);
+    eo->n = cur_n;
+    eo->coords = cur;
+    eo->h = h;
+    return 1;
+}
+
+/* ------------------------------------------------------------ comparison */
+
+static int same_guides(const enc_out * a, const enc_out * b) {
+    CHECK(a->n_guides == b->n_guides);
+    for (int g = 0; g < a->n_guides; ++g) {
+        const int64_t n = a->guide_n[g];
+        CHECK(n == b->guide_n[g]);
+        CHECK(memcmp(a->guide_coords[g], b->guide_coords[g], (size_t) n * 16) == 0);
+        CHECK(memcmp(a->guide_parent[g], b->guide_parent[g], (size_t) n * 4) == 0);
+        CHECK(memcmp(a->guide_subidx[g], b->guide_subidx[g], (size_t) n * 4) == 0);
+        printf("guide %d: %lld fine voxels match the oracle's S2C map\n", g, (long long) n);
+    }
+    return 1;
+}
+
+/* test_sparse_encoder_backend.c:98-161, restated: the coarse voxels, the
+ * guide, the coarse features and the closed-form latent. */
+static int tiny_known_answers(const enc_out * eo, const int32_t * coords, float latent_tol) {
+    static const int32_t coarse[3][4] = {{0, 0, 0, 0}, {0, 0, 1, 0}, {0, 1, 0, 0}};
+    static const int32_t parent[5] = {2, 0, 0, 2, 1};
+    static const int32_t subidx[5] = {3, 0, 1, 6, 0};
+    /* Child s of a coarse voxel carries the mean of its fine voxel's two
+     * input channels in channel s (skip group 8*2/8 = 2). */
+    static const float feat[3][8] = {{2, -1, 0, 0, 0, 0, 0, 0}, {2, 0, 0, 0, 0, 0, 0, 0}, {0, 0, 0, 3, 0, 0, 4, 0}};
+    CHECK(eo->n == 3 && eo->n_guides == 1 && eo->guide_n[0] == 5);
+    CHECK(memcmp(eo->coords, coarse, sizeof(coarse)) == 0);
+    CHECK(memcmp(eo->guide_coords[0], coords, 5 * 16) == 0);
+    CHECK(memcmp(eo->guide_parent[0], parent, sizeof(parent)) == 0);
+    CHECK(memcmp(eo->guide_subidx[0], subidx, sizeof(subidx)) == 0);
+    CHECK(memcmp(eo->h, feat, sizeof(feat)) == 0);
+    for (int r = 0; r < 3; ++r) {
+        double mean = 0.0, var = 0.0;
+        for (int j = 0; j < 8; ++j) mean += feat[r][j] / 8.0;
+        for (int j = 0; j < 8; ++j) var += (feat[r][j] - mean) * (feat[r][j] - mean) / 8.0;
+        const double want = (feat[r][0] - mean) / sqrt(var + 1e-5) + 0.125;
+        const double err = fabs(eo->latent[r] - want);
+        printf("tiny latent[%d] = %.6f, closed form %.6f\n", r, eo->latent[r], want);
+        CHECK(err <= latent_tol * fmax(1.0, fabs(want)));
+    }
+    return 1;
+}
+
+/* The model and input voxels of a case. */
+static void make_case(int tiny, enc_model * m, int32_t ** coords, float ** feats, int64_t * n) {
+    if (tiny) {
+        /* test_sparse_encoder_backend.c:84-97. */
+        static const int32_t c5[] = {0, 3, 1, 0, 0, 0, 0, 0, 0, 1, 0, 0, 0, 2, 1, 1, 0, 0, 2, 0};
+        static const float f5[] = {2, 4, 1, 3, -2, 0, 6, 2, 5, -1};
+        model_tiny(m);
+        *n = 5, *coords = ivec(20), *feats = fvec(10);
+        memcpy(*coords, c5, sizeof(c5));
+        memcpy(*feats, f5, sizeof(f5));
+    } else {
+        model_medium(m);
+        *coords = shell_coords(40, 15.0, n);
+        *feats = fvec((size_t) *n * m->in_c);
+        fill_rand(*feats, (size_t) *n * m->in_c, 1.7f);
+    }
+}
+
+int main(int argc, char ** argv) {
+    const int oracle_only = argc == 4 && strcmp(argv[3], "oracle") == 0;
+    if ((argc != 3 && !oracle_only) || (strcmp(argv[1], "tiny") != 0 && strcmp(argv[1], "medium") != 0) ||
+        (strcmp(argv[2], "f32") != 0 && strcmp(argv[2], "bf16") != 0)) {
+        fprintf(stderr, "usage: %s <tiny|medium> <f32|bf16> [oracle]\n", argv[0]);
+        return 1;
+    }
+    const int tiny = strcmp(argv[1], "tiny") == 0;
+    g_dtype = strcmp(argv[2], "bf16") == 0 ? TRELLIS_SPARSE_HIP_BF16 : TRELLIS_SPARSE_HIP_F32;
+    /* Chain tolerance - fp32: 1e-4, as the decoder conformance; bf16: a chain
+     * of ~20 rounded slots mirrored by the oracle, where a one-ulp flip
+     * (2^-8 relative) early on is carried by every later slot.  Known-answer
+     * latent - fp32: the reference test's 3e-4; bf16: the normalised value
+     * and the latent are each stored rounded (2^-9 relative apiece). */
+    const float tol = g_dtype == TRELLIS_SPARSE_HIP_F32 ? 1e-4f : 5e-2f;
+    const float kat_tol = g_dtype == TRELLIS_SPARSE_HIP_F32 ? 3e-4f : 1e-2f;
+    if (!oracle_only && trellis_sparse_hip_device_count() < 1) {
+        fprintf(stderr, "no HIP device: skipped\n");
+        return 77;
+    }
+
+    enc_model m;
+    int32_t * coords;
+    float * feats;
+    int64_t n;
+    make_case(tiny, &m, &coords, &feats, &n);
+    printf("model %s, dtype %s, %lld input voxels\n", argv[1], argv[2], (long long) n);
+    enc_out dev, orc;
+    memset(&dev, 0, sizeof(dev));
+    int ok = encode_orc(&m, coords, feats, n, &orc);
+    if (oracle_only) {
+        /* No device: the oracle chain alone against the reference test's
+         * known answers (tiny; the medium chain only has to run). */
+        if (ok) printf("oracle: %lld output voxels, %d guides\n", (long long) orc.n, orc.n_guides);
+        if (ok && tiny) ok = tiny_known_answers(&orc, coords, kat_tol);
+        enc_out_free(&orc);
+        printf("%s\n", ok ? "encoder oracle passed" : "encoder oracle FAILED");
+        return ok ? 0 : 1;
+    }
+
+    trellis_sparse_hip_policy pol;
+    trellis_sparse_hip_policy_init(&pol);
+    pol.compute_dtype = g_dtype;
+    trellis_sparse_backend * be = NULL;
+    trellis_status st = trellis_sparse_hip_backend_create_ex(0, &pol, &be);
+    if (st != TRELLIS_STATUS_OK) {
+        fprintf(stderr, "backend create: status %d\n", (int) st);
+        return 1;
+    }
+    CHECK(be->ops != NULL && be->kind == TRELLIS_SPARSE_BACKEND_HIP && be->device == 0);
+
+    ok = ok && encode_dev(be, &m, coords, feats, n, &dev);
+    if (ok) {
+        printf("%lld output voxels (oracle %lld), %d guides\n", (long long) dev.n, (long long) orc.n, dev.n_guides);
+        ok = dev.n == orc.n && memcmp(dev.coords, orc.coords, (size_t) orc.n * 16) == 0;
+        if (!ok) fprintf(stderr, "output coordinates differ from the oracle\n");
+        ok = ok && same_guides(&dev, &orc);
+        const int c = m.channels[m.levels - 1];
+        ok = ok && close_all("last-level feats", dev.h, orc.h, (size_t) orc.n * c, tol);
+        ok = ok && close_all("latent", dev.latent, orc.latent, (size_t) orc.n * m.latent, tol);
+    }
+    if (ok && tiny) {
+        ok = tiny_known_answers(&dev, coords, kat_tol);
+        if (!ok) fprintf(stderr, "tiny encoder differs from the reference test's known answers\n");
+    }
+    enc_out_free(&dev);
+    enc_out_free(&orc);
+    be->ops->destroy(be);
+    printf("%s\n", ok ? "encoder conformance passed" : "encoder conformance FAILED");
+    return ok ? 0 : 1;
+}

@@ -10,6 +10,12 @@ The reference decoder builds its blocks from the vtable slots:
   -> c2s_gather_device; skip_repeat_device(h);
   row_norm_silu(h_up, no affine) -> conv(Co->Co) on the child rulebook
   -> add(conv2, skip).
+- The encoder's S2C down-block (src/architectures/sparse_unet_encoder/
+  executor.c:160-360), with the device S2C steps in place of the host build
+  and pack round trip (:209-300): s2c_build_device -> coarse rulebook;
+  row_norm_silu(h) -> conv(Ci->Co/8) on the fine rulebook -> s2c_pack;
+  s2c_skip_mean(h); row_norm_silu(packed, no affine) -> conv(Co->Co) on the
+  coarse rulebook -> add(conv2, skip).
 Here the same sequences run through the C ABI and are compared with the
 oracle's restatement of each slot, chained with the storage rounding the
 backend applies between slots.  Maps stay bit-exact; values meet the
@@ -366,3 +372,78 @@ def test_c2s_upblock_vs_oracle(backends, dtype):
     say(f"c2s up-block dtype={dtype} children={m}")
     rb.free()
     nrb.free()
+
+
+@pytest.mark.parametrize("dtype", [sh.F32, sh.F16, sh.BF16])
+@pytest.mark.parametrize("ci,co", [(64, 128), (128, 256)])
+def test_s2c_downblock_vs_oracle(backends, dtype, ci, co):
+    be = backends[dtype]
+    rnd = lambda a: sh.storage_round(a, dtype)
+    pc = co // 8
+    rng = np.random.default_rng(91 + ci + dtype)
+    coords = shell_coords(6000)
+    n = coords.shape[0]
+    say(f"s2c down-block dtype={dtype} fine={n} {ci}->{co}")
+    h = rnd(rng.standard_normal((n, ci)))
+    g1 = (1 + 0.1 * rng.standard_normal(ci)).astype(np.float32)
+    b1 = (0.1 * rng.standard_normal(ci)).astype(np.float32)
+    w1 = weights(rng, pc, 27, ci, dtype)
+    c1b = (0.1 * rng.standard_normal(pc)).astype(np.float32)
+    w2 = weights(rng, co, 27, co, dtype)
+    c2b = (0.1 * rng.standard_normal(co)).astype(np.float32)
+
+    pmap = be.upload_coords(coords)
+    rb = be.build_rulebook_for_c2s_map(pmap)
+    hb = be.upload(h)
+    fmap, cmap = be.s2c_build_device(coords_map=pmap)
+    rc, ec, ep, es = orc.s2c_map(coords)
+    assert rc == 0
+    m = cmap.n
+    assert np.array_equal(be.download_c2s_coords(cmap), ec)
+    c, p, s = be.download_c2s_map(fmap)
+    assert np.array_equal(c, coords) and np.array_equal(p, ep) and np.array_equal(s, es)
+    crb = be.build_rulebook_for_c2s_map(cmap)
+    assert np.array_equal(be.neighbors(crb), orc.Rulebook(ec).neighbors())
+
+    norm1 = be.alloc(n * ci)
+    be.row_norm(hb, g1, b1, norm1, n, ci, 1e-6, silu=True)
+    conv1 = be.alloc(n * pc)
+    be.conv(rb, norm1, w1, c1b, conv1, ci, pc)
+    packed = be.alloc(m * co)
+    be.s2c_pack_device(conv1, fmap, packed, co)
+    skip = be.alloc(m * co)
+    be.s2c_skip_mean_device(hb, fmap, skip, ci, co)
+    norm2 = be.alloc(m * co)
+    be.row_norm(packed, None, None, norm2, m, co, 1e-6, silu=True)
+    conv2 = be.alloc(m * co)
+    be.conv(crb, norm2, w2, c2b, conv2, co, co)
+    out = be.alloc(m * co)
+    be.add(conv2, skip, out, m * co)
+
+    # Per slot, each on the backend's own input (see the ConvNeXt test).
+    g_n1 = be.download(norm1).reshape(n, ci)
+    assert max_rel_err(g_n1, rnd(orc.row_norm(h, g1, b1, n, ci, 1e-6, silu=True))) <= TOL[dtype]
+    g_c1 = be.download(conv1).reshape(n, pc)
+    assert max_rel_err(g_c1, rnd(orc.Rulebook(coords).conv(g_n1, w1, c1b, ci, pc))) <= TOL[dtype]
+    g_pk = be.download(packed).reshape(m, co)
+    assert np.array_equal(g_pk, orc.s2c_pack(g_c1, ep, es, m, co))
+    g_skip = be.download(skip).reshape(m, co)
+    assert np.array_equal(g_skip, rnd(orc.s2c_skip_mean(h, ep, es, m, ci, co)))
+    g_n2 = be.download(norm2).reshape(m, co)
+    assert max_rel_err(g_n2, rnd(orc.row_norm(g_pk, None, None, m, co, 1e-6, silu=True))) <= TOL[dtype]
+    g_c2 = be.download(conv2).reshape(m, co)
+    assert max_rel_err(g_c2, rnd(orc.Rulebook(ec).conv(g_n2, w2, c2b, co, co))) <= TOL[dtype]
+    got = be.download(out).reshape(m, co)
+    assert max_rel_err(got, rnd(orc.add(g_c2, g_skip))) <= TOL[dtype]
+    # The whole block on the oracle alone, from h: the rounding of each slot
+    # mirrored, the slot errors compounding through two convs and two norms.
+    e_c1 = rnd(orc.Rulebook(coords).conv(rnd(orc.row_norm(h, g1, b1, n, ci, 1e-6, silu=True)), w1, c1b, ci, pc))
+    e_n2 = rnd(orc.row_norm(orc.s2c_pack(e_c1, ep, es, m, co), None, None, m, co, 1e-6, silu=True))
+    e_out = rnd(orc.add(rnd(orc.Rulebook(ec).conv(e_n2, w2, c2b, co, co)), g_skip))
+    assert max_rel_err(got, e_out) <= (1e-4 if dtype == sh.F32 else 5e-2)
+    say(f"s2c down-block dtype={dtype} coarse={m}")
+    rb.free()
+    crb.free()
+    be.free_map(fmap)
+    be.free_map(cmap)
+    be.free_map(pmap)
