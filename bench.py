@@ -155,7 +155,9 @@ class Block:
 
     convnext: on the ~1.26M config-3 children, C = 128:
       conv(128->128) -> row_norm -> linear_silu(128->512) -> linear(512->128) -> add
-      (src/architectures/sparse_unet_decoder/executor.c:176-255).
+      (src/architectures/sparse_unet_decoder/executor.c:176-255).  With
+      --channels 256: on the ~0.32M config-3 parents, C = 256 (the decoder
+      level above the children, decoder.c:248-249).
     convnext_fused: the same block with its tail (row_norm .. add) in the one
       fused entry point trellis_sparse_hip_convnext_mlp.
     convnext_block: the whole block in one call, trellis_sparse_hip_convnext_block
@@ -181,15 +183,18 @@ class Block:
     slot runs on that stream, in call order).
     """
 
-    def __init__(self, be, kind, slots=False):
+    def __init__(self, be, kind, slots=False, channels=128):
         self.be, self.kind, self.fuse_add = be, kind, not slots
         w = wl.workload(3)
         rng = np.random.default_rng(11)
         f32 = lambda a: np.ascontiguousarray(a, np.float32)
         if kind in ("convnext", "convnext_fused", "convnext_block"):
-            c = 128
+            c = channels
             pmap = be.upload_coords(w["parent_coords"])
-            dm = be.build_c2s_map_device(be.upload(w["logits"]), w["parent_coords"].shape[0], coords_map=pmap)
+            if c == 128:
+                dm = be.build_c2s_map_device(be.upload(w["logits"]), w["parent_coords"].shape[0], coords_map=pmap)
+            else:
+                dm = pmap
             self.cmap, self.n, self.c = dm, dm.n, c
             self.h = be.upload(rng.standard_normal((self.n, c)).astype(np.float32))
             self.conv_w = be.keep(f32(rng.standard_normal((c, 27, c)) / np.sqrt(27 * c)))
@@ -390,7 +395,7 @@ class Block:
 
 def run_block(args):
     be = sh.Backend(0, sh.BF16)
-    job = Block(be, args.block, slots=args.slots)
+    job = Block(be, args.block, slots=args.slots, channels=args.channels)
     for _ in range(args.warmup):
         job.step()
     be.synchronize()
@@ -538,6 +543,8 @@ def main():
     ap.add_argument("--block", choices=["convnext", "convnext_fused", "convnext_block", "c2s", "s2c", "mesh"],
                     help="instead of the configuration step, time one decoder block composed from the backend's "
                          "slots at config-3 scale and print its own JSON line")
+    ap.add_argument("--channels", type=int, default=128, choices=[128, 256],
+                    help="ConvNeXt blocks: 128 on the config-3 children, 256 on its parents")
     ap.add_argument("--slots", action="store_true",
                     help="config 2 and the c2s / s2c blocks: run conv -> row_norm_silu and conv -> add as separate "
                          "slots instead of the convs with fused epilogues")

@@ -434,7 +434,9 @@ trellis_status trellis_sparse_hip_dump_map_coords(trellis_sparse_hip_dump * dump
  * NULL).  Each intermediate is rounded to the storage type where the slot
  * sequence stores it; the 4c-wide hidden rows never leave the chip.
  * TRELLIS_STATUS_NOT_IMPLEMENTED unless compute_dtype is F16 or BF16 and
- * c is 64 or 128; callers then run the slot sequence. */
+ * c is 64, 128 or 256 (at 512 and 1024 a 128-row tile's normalised rows
+ * alone take 128 KB of the 160 KB of LDS, leaving no room for the hidden
+ * chunk and the weights); callers then run the slot sequence. */
 trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
                                                const float * gamma, const float * beta, const float * mlp0_w,
                                                const float * mlp0_b, const float * mlp2_w, const float * mlp2_b,
@@ -448,7 +450,7 @@ trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend,
  * intermediate, then the fused tail.  Storage roundings where the slot
  * sequence stores.
  * TRELLIS_STATUS_NOT_IMPLEMENTED unless compute_dtype is F16 or BF16 and c is
- * 64 or 128. */
+ * 64, 128 or 256. */
 trellis_status trellis_sparse_hip_convnext_block(trellis_sparse_backend * backend,
                                                  const trellis_sparse_rulebook * rulebook,
                                                  const trellis_sparse_buffer * h, const float * conv_w,

@@ -135,12 +135,13 @@ def mlp_params(rng, c, dtype):
 
 
 @pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
-@pytest.mark.parametrize("c", [64, 128])
-@pytest.mark.parametrize("n", [1, 63, 65, 4099])
+@pytest.mark.parametrize("c", [64, 128, 256])
+@pytest.mark.parametrize("n", [1, 63, 65, 127, 129, 4099])
 def test_convnext_mlp_fused_vs_oracle(backends, dtype, c, n):
     """The fused tail against the oracle's slot chain with the same storage
-    roundings (norm, hidden, second linear, add); rows past a tile edge and a
-    single row included."""
+    roundings (norm, hidden, second linear, add); rows past a tile edge (64-row
+    tiles at c = 64 and 128, 128-row tiles at c = 256) and a single row
+    included."""
     be = backends[dtype]
     rnd = lambda a: sh.storage_round(a, dtype)
     rng = np.random.default_rng(1000 * c + n + dtype)
@@ -161,7 +162,7 @@ def test_convnext_mlp_fused_vs_oracle(backends, dtype, c, n):
 
 
 @pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
-@pytest.mark.parametrize("c", [64, 128])
+@pytest.mark.parametrize("c", [64, 128, 256])
 def test_convnext_mlp_fused_vs_slots(backends, dtype, c):
     """At a size where blocks walk many tiles (and the weight ring runs
     across tile boundaries), the fused tail matches the slot sequence it
@@ -192,10 +193,11 @@ def test_convnext_mlp_fused_vs_slots(backends, dtype, c):
 
 
 def test_convnext_mlp_rejects_unsupported(backends):
-    """fp32 storage and widths other than 64 / 128 report NOT_IMPLEMENTED
-    (the caller then runs the slot sequence); nothing is launched."""
+    """fp32 storage and widths other than 64 / 128 / 256 report
+    NOT_IMPLEMENTED (the caller then runs the slot sequence); nothing is
+    launched."""
     rng = np.random.default_rng(5)
-    for dtype, c in ((sh.F32, 64), (sh.BF16, 96), (sh.F16, 256)):
+    for dtype, c in ((sh.F32, 64), (sh.BF16, 96), (sh.F16, 512)):
         be = backends[dtype]
         n = 10
         gamma, beta, w0, b0, w2, b2 = mlp_params(rng, c, dtype)
@@ -224,7 +226,7 @@ def oracle_convnext_block(coords, h, params, c, dtype):
 
 
 @pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
-@pytest.mark.parametrize("c", [64, 128])
+@pytest.mark.parametrize("c", [64, 128, 256])
 @pytest.mark.parametrize("n", [1, 300, 6000])
 def test_convnext_block_entry_vs_oracle(backends, dtype, c, n):
     """trellis_sparse_hip_convnext_block (the conv, then the fused tail)
@@ -249,7 +251,7 @@ def test_convnext_block_entry_vs_oracle(backends, dtype, c, n):
 
 
 @pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
-@pytest.mark.parametrize("c", [64, 128])
+@pytest.mark.parametrize("c", [64, 128, 256])
 def test_convnext_block_entry_vs_slots(backends, dtype, c):
     """On the config-2 voxels: the block entry against the five slots on the
     same inputs, to the storage tolerance (the MLP's sums run in another order
@@ -281,13 +283,13 @@ def test_convnext_block_entry_vs_slots(backends, dtype, c):
 
 
 def test_convnext_block_entry_rejects(backends):
-    """fp32 storage, c other than 64 / 128, and out aliasing h are refused
-    before anything is launched."""
+    """fp32 storage, c other than 64 / 128 / 256, and out aliasing h are
+    refused before anything is launched."""
     rng = np.random.default_rng(6)
     coords = shell_coords(50)
     n = coords.shape[0]
     for dtype, c, status in ((sh.F32, 64, sh.NOT_IMPLEMENTED), (sh.BF16, 96, sh.NOT_IMPLEMENTED),
-                             (sh.F16, 256, sh.NOT_IMPLEMENTED)):
+                             (sh.F16, 512, sh.NOT_IMPLEMENTED)):
         be = backends[dtype]
         rb = be.build_rulebook(coords)
         hb, out = be.upload(np.zeros((n, c), np.float32)), be.alloc(n * c)

@@ -675,7 +675,7 @@ trellis_status mlp_impl(trellis_sparse_backend * backend, const trellis_sparse_b
         return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "convnext_mlp: bad argument");
     }
     if (!convnext_mlp_supported(be->policy.compute_dtype, c)) {
-        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, "convnext_mlp: needs bf16/fp16 storage and c = 64 or 128");
+        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, "convnext_mlp: needs bf16/fp16 storage and c = 64, 128 or 256");
     }
     CallScope scope(be);
     const void *g = nullptr, *bt = nullptr, *pw0 = nullptr, *pb0 = nullptr, *pw2 = nullptr, *pb2 = nullptr;
@@ -1022,7 +1022,7 @@ trellis_status block_impl(trellis_sparse_backend * backend, const trellis_sparse
     }
     const int dt = be->policy.compute_dtype;
     if (!convnext_mlp_supported(dt, c)) {
-        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, "convnext_block: needs bf16/fp16 storage and c = 64 or 128");
+        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, "convnext_block: needs bf16/fp16 storage and c = 64, 128 or 256");
     }
     trellis_sparse_buffer * tmp = nullptr;
     trellis_status st = op_alloc_f32(backend, (size_t) n * c, &tmp);

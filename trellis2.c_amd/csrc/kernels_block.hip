@@ -266,6 +266,295 @@ __global__ void __launch_bounds__(512) k_convnext_mlp(const typename Store<DT>::
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same tail for C = 256 (H = 1024).  W0 and W2 (512 KB each in bf16) no
+// longer fit in registers, and a 64-row tile would stream 16 KB of weights
+// per row, so the hidden layer is taken in chunks of 128 units instead:
+// persistent blocks of 8 wavefronts walk 128-row tiles, and per chunk
+//   GEMM 1  (128 x 256 times 256 x 128; 2 row groups x 4 column groups, the
+//           normalised rows and the chunk's W0 columns read from LDS) ->
+//           bias, SiLU, rounding -> the chunk's hidden tile in LDS;
+//   GEMM 2  (128 x 128 times 128 x 256; 8 column groups of 32 outputs over
+//           all 128 rows) accumulates into the tile's fp32 outputs, which
+//           stay in registers across the 8 chunks.
+// The chunk's 64 KB of W0 are fetched once per block straight into LDS
+// (direct-to-LDS loads) while the previous chunk's GEMM 2 runs: fetched per
+// wavefront into registers, each W0 fragment went through the vector-memory
+// path twice (once per row group) and GEMM 1 waited on that path (0.534 ms
+// at 316k rows).  W2 fragments stream through a per-wavefront register ring
+// 2 steps deep that runs on across chunks and tiles, each fetched once per
+// tile and block.  Two barriers per chunk.  The hidden values never leave
+// the CU; GEMM 2's sum over the 1024 hidden units runs in K order, chunk
+// after chunk, as the linear slot's does.  Roundings as above.
+// ---------------------------------------------------------------------------
+template <int DT, int C>
+__global__ void __launch_bounds__(512, 1) k_convnext_mlp_wide(const typename Store<DT>::T * __restrict__ x,
+                                                              const float * __restrict__ gamma,
+                                                              const float * __restrict__ beta,
+                                                              const typename Store<DT>::T * __restrict__ w0,
+                                                              const float * __restrict__ b0,
+                                                              const typename Store<DT>::T * __restrict__ w2,
+                                                              const float * __restrict__ b2,
+                                                              const typename Store<DT>::T * __restrict__ res,
+                                                              typename Store<DT>::T * __restrict__ y, int64_t n,
+                                                              float eps, int n_tiles) {
+    using T = typename Store<DT>::T;
+    using V = typename Mfma<DT>::V;
+    static_assert(C == 256, "C = 256");
+    constexpr int BM = 128;             // rows per tile
+    constexpr int NRB = BM / 16;        // row blocks per tile
+    constexpr int H = 4 * C;            // hidden width
+    constexpr int HC = 128;             // hidden units per chunk
+    constexpr int NCH = H / HC;         // chunks
+    constexpr int KS1 = C / 32;         // K steps of GEMM 1
+    constexpr int KS2 = HC / 32;        // K steps of GEMM 2 per chunk
+    constexpr int NT1 = 2;              // GEMM 1 column tiles per wavefront (32 hidden units)
+    constexpr int NT2 = 2;              // GEMM 2 column tiles per wavefront (32 outputs)
+    constexpr int D2 = 2;               // W2 ring depth (steps)
+    constexpr int LPR = C / 8;          // LayerNorm lanes per row
+    constexpr int RPP = 64 / LPR;       // LayerNorm rows per wavefront pass
+    constexpr int LNP = (BM / 8) / RPP; // LayerNorm passes (BM / 8 rows per wavefront)
+    constexpr int CH = C / 8;           // 16-byte chunks per row
+    constexpr int DP = BM * CH / 512;   // output chunks per thread
+    constexpr int OSTR = C + 8;         // staging row stride (storage elements)
+    static_assert(KS2 % D2 == 0 && (BM / 8) % RPP == 0, "shapes");
+    // LDS: the normalised rows (GEMM 1's A operand), the chunk's hidden tile
+    // (GEMM 2's A operand), the chunk's W0 fragments (GEMM 1's B operand:
+    // fragment (K step s, column group cg, column tile nt) as 64 lanes x 16
+    // bytes at ((s * 4 + cg) * NT1 + nt) KB); the output staging tile reuses
+    // the first two.
+    constexpr int XE = KS1 * NRB * 64 * 8, HE = KS2 * NRB * 64 * 8, WE = KS1 * 4 * NT1 * 64 * 8;
+    static_assert((XE + HE) >= BM * OSTR, "staging fits");
+    __shared__ __attribute__((aligned(16))) T s_lds[XE + HE + WE];
+    T * s_x = s_lds;
+    T * s_h = s_lds + XE;
+    T * s_o = s_lds;
+    const T * s_w0 = s_lds + XE + HE;
+    const uint32_t w0_lds = (uint32_t) (uintptr_t) (s_lds + XE + HE);
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int G = (int) gridDim.x;
+    const int lb = (int) xcd_remap(blockIdx.x, G);
+    auto opnd = [](int kstep, int rb, int i, int c) { return ((kstep * NRB + rb) * 64 + a_granule(i, c)) * 8; };
+
+    // GEMM 1: row group rg (row blocks 4 rg .. 4 rg + 3), column group cg
+    // (hidden units cg*32 .. cg*32+31 of each chunk; packed column
+    // cg*32 + nt*16 + l16 holds unit cg*32 + 2 l16 + nt).
+    const int rg = wave & 1, cg = wave >> 1;
+    // GEMM 2: column group wave (outputs wave*32 .. +31, packed the same way).
+    float bias2[NT2];
+#pragma unroll
+    for (int nt = 0; nt < NT2; ++nt) bias2[nt] = b2 != nullptr ? b2[wave * 32 + l16 * NT2 + nt] : 0.0f;
+    const int li = lane % LPR;
+    // Weight rings.  Step g1 of GEMM 1 (chunk g1 / KS1, K step g1 % KS1) and
+    // step g2 of GEMM 2 (chunk g2 / KS2, K step g2 % KS2), both modulo a
+    // tile's steps: the last steps of a tile fetch the first of the next.
+    // wofs is 0, hidden from the compiler once per tile, so that it keeps
+    // the loads in the rings instead of hoisting them out of the tile loop.
+    int wofs = 0;
+    const T * w2lane = w2 + ((int64_t) lg * C + wave * 32 + l16) * 8;
+    // Chunk j's W0 fragments into s_w0: this wavefront's 8 of the 64 (K step
+    // s = wave, both column tiles of the 4 column groups); lane l16 + 16 lg
+    // of fragment (s, cg, nt) holds packed column j*HC + cg*32 + nt*16 + l16,
+    // K values 8 (4 s + lg) .. + 7.
+    const __amdgpu_buffer_rsrc_t w0res =
+        __builtin_amdgcn_make_buffer_rsrc((void *) w0, 0, C * H * (int) sizeof(T), 0x00020000);
+    static_assert(KS1 == 8, "one K step of W0 per wavefront");
+    auto load_w0 = [&](int j) {
+#pragma unroll
+        for (int f = 0; f < 4 * NT1; ++f) {
+            const int fcg = f / NT1, fnt = f % NT1;
+            const uint32_t voff =
+                (uint32_t) (((wave * 4 + lg) * H + j * HC + fcg * 32 + fnt * 16 + l16) * 16);
+            dma_b128(w0res, w0_lds + (uint32_t) (((wave * 4 + fcg) * NT1 + fnt) * 1024), voff, 0u);
+        }
+    };
+    auto load_w2 = [&](V * f, int g2) {
+        const int j = g2 / KS2, s = g2 % KS2;
+#pragma unroll
+        for (int nt = 0; nt < NT2; ++nt)
+            f[nt] = *(const V *) (w2lane + wofs + ((int64_t) (j * HC / 8 + s * 4) * C + nt * 16) * 8);
+    };
+    V wr2[D2][NT2];
+#pragma unroll
+    for (int r = 0; r < D2; ++r) load_w2(wr2[r], r);
+    load_w0(0);
+    wait_vmcnt<0>();
+    lds_barrier();
+
+    for (int tile = lb; tile < n_tiles; tile += G) {
+        const int64_t row0 = (int64_t) tile * BM;
+        asm volatile("" : "+s"(wofs));
+        // ---- LayerNorm of the tile's rows into s_x (rows past n: zeros) ----
+        {
+            // Scale and shift per tile (wofs keeps them out of the registers
+            // that the tile loop holds).
+            float gv[8], bv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                gv[e] = gamma != nullptr ? gamma[wofs + li * 8 + e] : 1.0f;
+                bv[e] = beta != nullptr ? beta[wofs + li * 8 + e] : 0.0f;
+            }
+            int4 xr[LNP];
+#pragma unroll
+            for (int p = 0; p < LNP; ++p) {
+                const int64_t row = row0 + wave * (BM / 8) + p * RPP + lane / LPR;
+                xr[p] = row < n ? *(const int4 *) (x + row * C + li * 8) : int4{0, 0, 0, 0};
+            }
+            // Mean, then the centred variance, each reduced over the row's
+            // LPR lanes level by level for all LNP rows of the lane at once
+            // (one shuffle round trip per level instead of one per row).
+            float mean[LNP], inv[LNP];
+#pragma unroll
+            for (int p = 0; p < LNP; ++p) {
+                float v[8];
+                unpack_chunk<DT>(xr[p], v);
+                float sm = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sm += v[e];
+                mean[p] = sm;
+            }
+#pragma unroll
+            for (int d = LPR / 2; d >= 1; d >>= 1)
+#pragma unroll
+                for (int p = 0; p < LNP; ++p) mean[p] += __shfl_xor(mean[p], d);
+#pragma unroll
+            for (int p = 0; p < LNP; ++p) {
+                mean[p] /= (float) C;
+                float v[8];
+                unpack_chunk<DT>(xr[p], v);
+                float q = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float dv = v[e] - mean[p];
+                    q += dv * dv;
+                }
+                inv[p] = q;
+            }
+#pragma unroll
+            for (int d = LPR / 2; d >= 1; d >>= 1)
+#pragma unroll
+                for (int p = 0; p < LNP; ++p) inv[p] += __shfl_xor(inv[p], d);
+#pragma unroll
+            for (int p = 0; p < LNP; ++p) {
+                const int rloc = wave * (BM / 8) + p * RPP + lane / LPR;
+                const float iv = 1.0f / sqrtf(inv[p] / (float) C + eps);
+                float v[8];
+                unpack_chunk<DT>(xr[p], v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = (v[e] - mean[p]) * iv * gv[e] + bv[e];
+                *(int4 *) (&s_x[opnd(li / 4, rloc / 16, rloc % 16, li % 4)]) = pack_chunk<DT>(v);
+            }
+        }
+        lds_barrier();
+        f32x4 acc2[NRB][NT2];
+#pragma unroll
+        for (int q = 0; q < NRB; ++q)
+#pragma unroll
+            for (int nt = 0; nt < NT2; ++nt) acc2[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (int j = 0; j < NCH; ++j) {
+            // ---- GEMM 1 of chunk j; bias, SiLU and rounding into s_h ----------
+            {
+                f32x4 acc1[4][NT1];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int nt = 0; nt < NT1; ++nt) acc1[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < KS1; ++s) {
+                    V af[4], bw[NT1];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) af[q] = *(const V *) (&s_x[opnd(s, rg * 4 + q, l16, lg)]);
+#pragma unroll
+                    for (int nt = 0; nt < NT1; ++nt)
+                        bw[nt] = *(const V *) (&s_w0[(((s * 4 + cg) * NT1 + nt) * 64 + lane) * 8]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int nt = 0; nt < NT1; ++nt) acc1[q][nt] = Mfma<DT>::mac(af[q], bw[nt], acc1[q][nt]);
+                }
+                float bias1[NT1];
+#pragma unroll
+                for (int nt = 0; nt < NT1; ++nt)
+                    bias1[nt] = b0 != nullptr ? b0[j * HC + cg * 32 + l16 * NT1 + nt] : 0.0f;
+                using Hv = T __attribute__((ext_vector_type(NT1)));
+                const int kc = cg * 32 + l16 * NT1;  // first hidden unit (in the chunk) of this lane
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        Hv o;
+#pragma unroll
+                        for (int nt = 0; nt < NT1; ++nt) {
+                            float v = acc1[q][nt][i] + bias1[nt];
+                            v = v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+                            o[nt] = round_to_store<DT>(v);
+                        }
+                        *(Hv *) (&s_h[opnd(kc / 32, rg * 4 + q, lg * 4 + i, (kc % 32) / 8) + kc % 8]) = o;
+                    }
+            }
+            lds_barrier();
+            // Every wavefront is done with chunk j's W0: the next chunk's (or,
+            // after the last, the next tile's first) go in during GEMM 2.
+            load_w0(j + 1 < NCH ? j + 1 : 0);
+            // ---- GEMM 2 of chunk j into the tile's outputs --------------------
+#pragma unroll
+            for (int s = 0; s < KS2; ++s) {
+                const int r = s % D2;
+                V af[NRB];
+#pragma unroll
+                for (int q = 0; q < NRB; ++q) af[q] = *(const V *) (&s_h[opnd(s, q, l16, lg)]);
+#pragma unroll
+                for (int q = 0; q < NRB; ++q)
+#pragma unroll
+                    for (int nt = 0; nt < NT2; ++nt) acc2[q][nt] = Mfma<DT>::mac(af[q], wr2[r][nt], acc2[q][nt]);
+                const int g2 = (j * KS2 + s + D2) % (NCH * KS2);
+                load_w2(wr2[r], g2);
+            }
+            // The W0 loads, issued before GEMM 2's KS2 * NT2 ring loads, have
+            // landed (vmcnt retires in order).  s_h (and, after the last
+            // chunk, s_x) is rewritten only after this barrier.
+            wait_vmcnt<KS2 * NT2>();
+            lds_barrier();
+        }
+        // ---- bias, rounding, staging; residual add, 16-byte stores ---------
+        {
+            using Ov = T __attribute__((ext_vector_type(NT2)));
+            const int c0 = wave * 32 + l16 * NT2;
+#pragma unroll
+            for (int q = 0; q < NRB; ++q)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = q * 16 + lg * 4 + i;
+                    Ov o;
+#pragma unroll
+                    for (int nt = 0; nt < NT2; ++nt) o[nt] = round_to_store<DT>(acc2[q][nt][i] + bias2[nt]);
+                    *(Ov *) (&s_o[r * OSTR + c0]) = o;
+                }
+        }
+        lds_barrier();
+#pragma unroll
+        for (int p = 0; p < DP; ++p) {
+            const int e = t + p * 512;
+            const int r = e / CH, jc = e % CH;
+            const int64_t row = row0 + r;
+            if (row >= n) continue;
+            float a[8], b[8];
+            unpack_chunk<DT>(*(const int4 *) (res + row * C + jc * 8), a);
+            unpack_chunk<DT>(*(const int4 *) (&s_o[r * OSTR + jc * 8]), b);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) a[k] += b[k];
+            *(int4 *) (y + row * C + jc * 8) = pack_chunk<DT>(a);
+        }
+        // The next tile's LayerNorm overwrites the staging tile.
+        lds_barrier();
+    }
+}
+
 template <int DT, int C>
 hipError_t launch_mlp_t(const void * x, const float * gamma, const float * beta, const void * w0, const float * b0,
                         const void * w2, const float * b2, const void * res, void * y, int64_t n, float eps, int cus,
@@ -281,17 +570,44 @@ hipError_t launch_mlp_t(const void * x, const float * gamma, const float * beta,
 }
 }  // namespace
 
-bool convnext_mlp_supported(int dtype, int c) { return (dtype == kF16 || dtype == kBF16) && (c == 64 || c == 128); }
+bool convnext_mlp_supported(int dtype, int c) {
+    return (dtype == kF16 || dtype == kBF16) && (c == 64 || c == 128 || c == 256);
+}
 
 void convnext_mlp_groups(int c, int * g0, int * g2) {
+    if (c >= 256) {  // k_convnext_mlp_wide: 32 hidden units and 32 outputs per wavefront
+        *g0 = 2;
+        *g2 = 2;
+        return;
+    }
     *g0 = 4 * c / 8 / 16;  // hidden columns per GEMM 1 wavefront / 16
     *g2 = c / 4 / 16;      // output columns per GEMM 2 wavefront / 16
 }
+
+namespace {
+template <int DT>
+hipError_t launch_mlp_wide_t(const void * x, const float * gamma, const float * beta, const void * w0,
+                             const float * b0, const void * w2, const float * b2, const void * res, void * y,
+                             int64_t n, float eps, int cus, hipStream_t s) {
+    using T = typename Store<DT>::T;
+    const int64_t tiles = (n + 127) / 128;
+    if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+    const int64_t grid = tiles < cus ? tiles : cus;
+    k_convnext_mlp_wide<DT, 256><<<(unsigned) grid, 512, 0, s>>>((const T *) x, gamma, beta, (const T *) w0, b0,
+                                                                (const T *) w2, b2, (const T *) res, (T *) y, n, eps,
+                                                                (int) tiles);
+    return hipGetLastError();
+}
+}  // namespace
 
 hipError_t launch_convnext_mlp(int dtype, const void * x, const float * gamma, const float * beta, const void * w0,
                                const float * b0, const void * w2, const float * b2, const void * res, void * y,
                                int64_t n, int c, float eps, int cus, hipStream_t s) {
     if (!convnext_mlp_supported(dtype, c) || n <= 0 || cus <= 0) return hipErrorInvalidValue;
+    if (c == 256) {
+        return dtype == kBF16 ? launch_mlp_wide_t<kBF16>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, cus, s)
+                              : launch_mlp_wide_t<kF16>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, cus, s);
+    }
     if (dtype == kBF16) {
         return c == 128 ? launch_mlp_t<kBF16, 128>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, cus, s)
                         : launch_mlp_t<kBF16, 64>(x, gamma, beta, w0, b0, w2, b2, res, y, n, eps, cus, s);

@@ -25,6 +25,33 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// s_waitcnt vmcnt(N) alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14;
+// expcnt and lgkmcnt left at their maxima, i.e. not waited for).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Direct-to-LDS load of 16 bytes per lane: the bytes at voff + soff of the
+// buffer land at LDS address lds + 16 * lane (exec-masked lanes load and
+// write nothing).  Inline assembly, so that the compiler neither counts it
+// nor waits for it before later LDS reads (it cannot tell LDS regions apart
+// and would drain every such load at the next read); the caller waits with
+// wait_vmcnt.  M0, which holds the LDS address, is saved and restored, with
+// the wait state that a write of M0 needs before an LDS-DMA instruction.
+__device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+    uint32_t keep;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(keep)
+        : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+        : "memory");
+}
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));

@@ -251,7 +251,7 @@ int linear_mfma_group(int co);
 bool linear_mfma_supported(int dtype, int ci, int co);
 hipError_t launch_linear_mfma(int dtype, const void * x, const void * w16, const float * bias, void * y, int64_t n,
                               int ci, int co, int silu, int cus, hipStream_t s);
-// Fused ConvNeXt MLP tail (kernels_block.hip): bf16/fp16, C = 64 or 128.
+// Fused ConvNeXt MLP tail (kernels_block.hip): bf16/fp16, C = 64, 128 or 256.
 // w0 [C/8][4C][8] and w2 [4C/8][C][8] in the storage type with the grouped
 // column packing of the MFMA linear, groups g0 and g2 from convnext_mlp_groups.
 bool convnext_mlp_supported(int dtype, int c);
