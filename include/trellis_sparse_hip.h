@@ -194,6 +194,14 @@ typedef enum trellis_sparse_hip_conv_algo {
                                               Ci % 128 == 0, Co % 64 == 0 */
 } trellis_sparse_hip_conv_algo;
 
+/* Which code runs the linear and linear_silu slots in 16-bit storage. */
+typedef enum trellis_sparse_hip_linear_algo {
+    TRELLIS_SPARSE_HIP_LINEAR_AUTO = 0,    /* Ci >= 256, Co >= 256 and n >= 2048: the platform GEMM library
+                                              (hipBLASLt, bias and SiLU in its epilogue, fp32 accumulation);
+                                              other shapes: this library's MFMA kernels */
+    TRELLIS_SPARSE_HIP_LINEAR_KERNEL = 1   /* always this library's MFMA / VALU kernels */
+} trellis_sparse_hip_linear_algo;
+
 typedef struct trellis_sparse_hip_policy {
     uint32_t struct_size;      /* sizeof(trellis_sparse_hip_policy) */
     int32_t compute_dtype;     /* trellis_sparse_hip_dtype */
@@ -204,9 +212,10 @@ typedef struct trellis_sparse_hip_policy {
     int32_t reject_duplicates; /* 0: duplicate coordinates resolve to the last row, as the CPU backend does
                                   (trellis_sparse_cpu.c:314-318). 1: build_rulebook returns
                                   TRELLIS_STATUS_INVALID_ARGUMENT on a duplicate. */
+    int32_t linear_algo;       /* trellis_sparse_hip_linear_algo */
 } trellis_sparse_hip_policy;
 
-/* Fills *policy with the defaults: F32, AUTO, cache_weights=1, reject_duplicates=0. */
+/* Fills *policy with the defaults: F32, conv AUTO, cache_weights=1, reject_duplicates=0, linear AUTO. */
 void trellis_sparse_hip_policy_init(trellis_sparse_hip_policy * policy);
 
 /* ------------------------------------------------------------------------ */

@@ -61,8 +61,9 @@ def test_policy_struct_matches_header():
 
     pol = sparse_hip.Policy()
     sparse_hip.LIB.trellis_sparse_hip_policy_init(ctypes.byref(pol))
-    assert pol.struct_size == ctypes.sizeof(sparse_hip.Policy) == 20
-    assert (pol.compute_dtype, pol.conv_algo, pol.cache_weights, pol.reject_duplicates) == (0, 0, 1, 0)
+    assert pol.struct_size == ctypes.sizeof(sparse_hip.Policy) == 24
+    assert (pol.compute_dtype, pol.conv_algo, pol.cache_weights, pol.reject_duplicates, pol.linear_algo) == \
+        (0, 0, 1, 0, sparse_hip.LINEAR_AUTO)
 
 
 def test_create_without_device_reports_unavailable():

@@ -59,6 +59,17 @@ def backend_for(dtype, be32, be16, bebf):
     return {sh.F32: be32, sh.F16: be16, sh.BF16: bebf}[dtype]
 
 
+@pytest.fixture(scope="module")
+def kernel_linears():
+    """16-bit backends whose linear slots always run this library's kernels
+    (policy linear_algo = KERNEL), beside the default ones that send wide
+    shapes to the platform GEMM library."""
+    bes = {dt: sh.Backend(0, dt, linear_algo=sh.LINEAR_KERNEL) for dt in (sh.F16, sh.BF16)}
+    yield bes
+    for b in bes.values():
+        b.destroy()
+
+
 # ------------------------------------------------------------ hash / kernel map
 
 def edge_coord_sets():
@@ -621,8 +632,8 @@ LINEAR_MFMA_CASES = [
 
 @pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
 @pytest.mark.parametrize("ci,co,n", LINEAR_MFMA_CASES)
-def test_linear_mfma_vs_oracle(be16, bebf, dtype, ci, co, n):
-    be = backend_for(dtype, None, be16, bebf)
+def test_linear_mfma_vs_oracle(kernel_linears, dtype, ci, co, n):
+    be = kernel_linears[dtype]
     say(f"linear mfma dtype={dtype} ci={ci} co={co} n={n}")
     rng = np.random.default_rng(ci * 7 + co + n)
     x = sh.storage_round(rng.standard_normal((n, ci)), dtype)
@@ -656,6 +667,36 @@ def test_linear_narrow_vs_oracle(be16, bebf, dtype, ci, co, n):
             be.linear(xb, w, bb, yb, n, ci, co, silu=silu)
             exp = orc.linear(x, w, bb, n, ci, co, silu)
             assert max_rel_err(be.download(yb), exp) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
+@pytest.mark.parametrize("ci,co,n", [(256, 1024, 2048), (1024, 256, 5001), (512, 2048, 3001), (2048, 512, 2050)])
+def test_linear_library_vs_oracle_and_kernel(be16, bebf, kernel_linears, dtype, ci, co, n):
+    """Wide 16-bit shapes (Ci, Co >= 256, n >= 2048) go to the platform GEMM
+    library under the default policy: each result against the oracle
+    (trellis_sparse_cpu.c:122-171) and against this library's MFMA kernel,
+    bias and SiLU on and off."""
+    be, bk = backend_for(dtype, None, be16, bebf), kernel_linears[dtype]
+    say(f"linear library dtype={dtype} ci={ci} co={co} n={n}")
+    rng = np.random.default_rng(ci * 3 + co + n)
+    x = sh.storage_round(rng.standard_normal((n, ci)), dtype)
+    w = sh.storage_round(rng.standard_normal((co, ci)) / math.sqrt(ci), dtype)
+    bias = rng.standard_normal(co).astype(np.float32)
+    xb, yb, yk = be.upload(x), be.alloc(n * co), bk.alloc(n * co)
+    xk = bk.upload(x)
+    for silu, bb in ((True, bias), (False, None), (False, bias)):
+        be.linear(xb, w, bb, yb, n, ci, co, silu=silu)
+        bk.linear(xk, w, bb, yk, n, ci, co, silu=silu)
+        got, ker = be.download(yb), bk.download(yk)
+        exp = orc.linear(x, w, bb, n, ci, co, silu)
+        assert max_rel_err(got, exp) <= TOL[dtype]
+        assert max_rel_err(ker, exp) <= TOL[dtype]
+        assert max_rel_err(got, ker) <= TOL[dtype]
+    # trim(FREE_BUFFERS) takes the library's workspace; the next call takes it
+    # again and gives the same bits.
+    be.trim(sh.TRIM_FREE_BUFFERS)
+    be.linear(xb, w, bias, yb, n, ci, co)
+    assert np.array_equal(be.download(yb), got)
 
 
 def test_linear_mfma_rows_independent(bebf):

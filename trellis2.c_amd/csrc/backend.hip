@@ -80,6 +80,10 @@ struct Backend {
     // Device address of this device's copy of `scratch` (the allocation-free
     // subdivide's working memory), or null when it could not be resolved.
     IntoScratch * into = nullptr;  // build_c2s_map_into's scratch on this backend's device
+    // The platform GEMM library's handle, plans and workspace for the wide
+    // linears (created on first use; the workspace goes with trim(FREE_BUFFERS)).
+    LinearLt * lt = nullptr;
+    DevMem lt_ws;
     // Weight cache.
     std::unordered_map<WeightKey, DevMem, WeightKeyHash> weights;
     std::vector<DevMem> transient;  // uncached weights of the current call
@@ -633,11 +637,32 @@ trellis_status linear_impl(trellis_sparse_backend * backend, const trellis_spars
     // bf16/fp16 with Ci = 64 or Ci % 128 == 0 and Co % 64 == 0: MFMA kernel;
     // Co <= 16 (the subdivide logits): the narrow MFMA kernel; otherwise (and
     // always for fp32) the reference-order VALU kernel.
+    trellis_status st = get_weight(be, bias, (size_t) co, kLayoutVector, 0, co, &bd);
+    if (st != TRELLIS_STATUS_OK) return st;
+    // Wide shapes: the platform GEMM library when it has a plan (workspace
+    // from the pool on first use; without it, or without a plan, the kernels
+    // below run).
+    if (be->policy.linear_algo == TRELLIS_SPARSE_HIP_LINEAR_AUTO && linear_lt_wanted(dt, n, ci, co)) {
+        constexpr size_t kLtWorkspace = size_t(32) << 20;
+        if (be->lt == nullptr) be->lt = linear_lt_create();
+        if (be->lt_ws.ptr == nullptr && dev_alloc(be, kLtWorkspace, &be->lt_ws) != TRELLIS_STATUS_OK) {
+            be->last_error.clear();
+        }
+        const void * w16 = nullptr;
+        if (be->lt_ws.ptr != nullptr) {
+            st = get_weight(be, weight, (size_t) ci * co, kLayoutLinear16, ci, co, &w16);
+            if (st != TRELLIS_STATUS_OK) return st;
+            stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+            const bool done = linear_lt_run(be->lt, dt, x->ptr, w16, (const float *) bd, y->ptr, n, ci, co, silu,
+                                            be->lt_ws.ptr, be->lt_ws.bytes, be->stream);
+            stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
+            if (done) return TRELLIS_STATUS_OK;
+        }
+    }
     const bool mfma = linear_mfma_supported(dt, ci, co);
     const bool narrow = !mfma && linear_narrow_supported(dt, ci, co);
     const int layout = mfma ? kLayoutLinearMfma : (narrow ? kLayoutLinear16 : kLayoutLinearT);
-    trellis_status st = get_weight(be, weight, (size_t) ci * co, layout, ci, co, &wt);
-    if (st == TRELLIS_STATUS_OK) st = get_weight(be, bias, (size_t) co, kLayoutVector, 0, co, &bd);
+    st = get_weight(be, weight, (size_t) ci * co, layout, ci, co, &wt);
     if (st != TRELLIS_STATUS_OK) return st;
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
     hipError_t err;
@@ -1691,6 +1716,7 @@ trellis_status op_trim(trellis_sparse_backend * backend, unsigned flags, size_t 
         be->weights.clear();
     }
     if (flags & TRELLIS_SPARSE_TRIM_FREE_BUFFERS) {
+        dev_release(be, &be->lt_ws);  // the GEMM library's workspace (taken again on the next wide linear)
         for (auto & kv : be->free_blocks) {
             for (void * p : kv.second) {
                 (void) hipFree(p);
@@ -1756,6 +1782,9 @@ void op_destroy(trellis_sparse_backend * backend) {
     be->maps.clear();
     for (auto & kv : be->weights) dev_release(be, &kv.second);
     be->weights.clear();
+    dev_release(be, &be->lt_ws);
+    linear_lt_destroy(be->lt);
+    be->lt = nullptr;
     for (auto & kv : be->free_blocks)
         for (void * p : kv.second) (void) hipFree(p);
     for (auto & m : be->pending) {
@@ -1787,6 +1816,7 @@ void trellis_sparse_hip_policy_init(trellis_sparse_hip_policy * policy) {
     policy->conv_algo = TRELLIS_SPARSE_HIP_CONV_AUTO;
     policy->cache_weights = 1;
     policy->reject_duplicates = 0;
+    policy->linear_algo = TRELLIS_SPARSE_HIP_LINEAR_AUTO;
 }
 
 int trellis_sparse_hip_device_count(void) {
@@ -1809,7 +1839,8 @@ trellis_status trellis_sparse_hip_backend_create_ex(int device, const trellis_sp
         p = *policy;
     }
     if (p.compute_dtype < TRELLIS_SPARSE_HIP_F32 || p.compute_dtype > TRELLIS_SPARSE_HIP_BF16 ||
-        p.conv_algo < TRELLIS_SPARSE_HIP_CONV_AUTO || p.conv_algo > TRELLIS_SPARSE_HIP_CONV_COMPACT) {
+        p.conv_algo < TRELLIS_SPARSE_HIP_CONV_AUTO || p.conv_algo > TRELLIS_SPARSE_HIP_CONV_COMPACT ||
+        p.linear_algo < TRELLIS_SPARSE_HIP_LINEAR_AUTO || p.linear_algo > TRELLIS_SPARSE_HIP_LINEAR_KERNEL) {
         return TRELLIS_STATUS_INVALID_ARGUMENT;
     }
     const int count = trellis_sparse_hip_device_count();

@@ -31,6 +31,7 @@ TRIM_FREE_BUFFERS, TRIM_WEIGHTS = 1, 2
 
 F32, F16, BF16 = 0, 1, 2
 CONV_AUTO, CONV_GENERIC, CONV_MASKED, CONV_COMPACT = 0, 1, 2, 3
+LINEAR_AUTO, LINEAR_KERNEL = 0, 1
 STAGES = ["hash", "map", "conv", "subdivide", "broadcast", "elementwise"]
 
 _p = c_void_p  # opaque pointers (buffer, rulebook, device map, backend)
@@ -81,7 +82,7 @@ class BackendStruct(Structure):
 
 class Policy(Structure):
     _fields_ = [("struct_size", c_uint32), ("compute_dtype", c_int32), ("conv_algo", c_int32),
-                ("cache_weights", c_int32), ("reject_duplicates", c_int32)]
+                ("cache_weights", c_int32), ("reject_duplicates", c_int32), ("linear_algo", c_int32)]
 
 
 class StageTimes(Structure):
@@ -288,11 +289,12 @@ class Backend:
     """One sparse backend instance on one device."""
 
     def __init__(self, device: int = 0, dtype: int = F32, conv_algo: int = CONV_AUTO, cache_weights: bool = True,
-                 reject_duplicates: bool = False):
+                 reject_duplicates: bool = False, linear_algo: int = LINEAR_AUTO):
         pol = Policy()
         LIB.trellis_sparse_hip_policy_init(ctypes.byref(pol))
         pol.compute_dtype = dtype
         pol.conv_algo = conv_algo
+        pol.linear_algo = linear_algo
         pol.cache_weights = 1 if cache_weights else 0
         pol.reject_duplicates = 1 if reject_duplicates else 0
         out = c_void_p()
