@@ -192,6 +192,28 @@ def test_each_slot_reports_out_of_memory_and_recovers(bf):
     rb.free()
 
 
+def test_wide_linear_out_of_memory_and_recovers(bf):
+    """A wide linear (Ci = Co = 256, n >= 2048: the GEMM library's route)
+    under starvation: the library's workspace cannot be taken, the kernel
+    route's weight upload fails too, and the slot returns OUT_OF_MEMORY; with
+    the hook off the same call gives the result of the unstarved call."""
+    be = bf
+    n, ci, co = 2048, 256, 256
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((n, ci)).astype(np.float32)
+    lw = be.keep((rng.standard_normal((co, ci)) * 0.05).astype(np.float32))
+    xb, yb = be.upload(x), be.alloc(n * co)
+    be.linear(xb, lw, None, yb, n, ci, co, silu=True)
+    ref = be.download(yb)
+    y2 = be.alloc(n * co)
+    starve(be)
+    st = be.ops.linear_silu(be.ptr, xb.handle, f32p(lw), None, y2.handle, n, ci, co)
+    be.fail_alloc(-1)
+    assert st == sh.OUT_OF_MEMORY
+    be.linear(xb, lw, None, y2, n, ci, co, silu=True)
+    assert np.array_equal(be.download(y2), ref)
+
+
 def test_retry_releases_the_pool(bf):
     be = bf
     be.synchronize()
