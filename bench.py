@@ -157,7 +157,11 @@ class Block:
       conv(128->128) -> row_norm -> linear_silu(128->512) -> linear(512->128) -> add
       (src/architectures/sparse_unet_decoder/executor.c:176-255).  With
       --channels 256: on the ~0.32M config-3 parents, C = 256 (the decoder
-      level above the children, decoder.c:248-249).
+      level above the children, decoder.c:248-249); --channels 512: on the
+      parents' own parents (the parent coordinates halved, ~0.08M voxels),
+      C = 512, the level above that, whose tail runs composed (row_norm and
+      the two linears through the GEMM library, the residual in the second
+      one's epilogue).
     convnext_fused: the same block with its tail (row_norm .. add) in the one
       fused entry point trellis_sparse_hip_convnext_mlp.
     convnext_block: the whole block in one call, trellis_sparse_hip_convnext_block
@@ -190,7 +194,12 @@ class Block:
         f32 = lambda a: np.ascontiguousarray(a, np.float32)
         if kind in ("convnext", "convnext_fused", "convnext_block"):
             c = channels
-            pmap = be.upload_coords(w["parent_coords"])
+            if c == 512:
+                pc = w["parent_coords"].copy()
+                pc[:, 1:] >>= 1
+                pmap = be.upload_coords(np.ascontiguousarray(np.unique(pc, axis=0), dtype=np.int32))
+            else:
+                pmap = be.upload_coords(w["parent_coords"])
             if c == 128:
                 dm = be.build_c2s_map_device(be.upload(w["logits"]), w["parent_coords"].shape[0], coords_map=pmap)
             else:
@@ -543,8 +552,8 @@ def main():
     ap.add_argument("--block", choices=["convnext", "convnext_fused", "convnext_block", "c2s", "s2c", "mesh"],
                     help="instead of the configuration step, time one decoder block composed from the backend's "
                          "slots at config-3 scale and print its own JSON line")
-    ap.add_argument("--channels", type=int, default=128, choices=[128, 256],
-                    help="ConvNeXt blocks: 128 on the config-3 children, 256 on its parents")
+    ap.add_argument("--channels", type=int, default=128, choices=[128, 256, 512],
+                    help="ConvNeXt blocks: 128 on the config-3 children, 256 on its parents, 512 on theirs")
     ap.add_argument("--slots", action="store_true",
                     help="config 2 and the c2s / s2c blocks: run conv -> row_norm_silu and conv -> add as separate "
                          "slots instead of the convs with fused epilogues")

@@ -438,14 +438,21 @@ trellis_status trellis_sparse_hip_dump_map_coords(trellis_sparse_hip_dump * dump
 /* ------------------------------------------------------------------------ */
 
 /* y = residual + mlp2(SiLU(mlp0(row_norm(x, gamma, beta, eps)))), x, residual
- * and y [n][c] in the backend's compute_dtype; mlp0_w fp32 [4c][c],
- * mlp0_b [4c], mlp2_w fp32 [c][4c], mlp2_b [c] (biases, gamma and beta may be
- * NULL).  Each intermediate is rounded to the storage type where the slot
- * sequence stores it; the 4c-wide hidden rows never leave the chip.
- * TRELLIS_STATUS_NOT_IMPLEMENTED unless compute_dtype is F16 or BF16 and
- * c is 64, 128 or 256 (at 512 and 1024 a 128-row tile's normalised rows
- * alone take 128 KB of the 160 KB of LDS, leaving no room for the hidden
- * chunk and the weights); callers then run the slot sequence. */
+ * and y [n][c] in the backend's compute_dtype (y may be residual);
+ * mlp0_w fp32 [4c][c], mlp0_b [4c], mlp2_w fp32 [c][4c], mlp2_b [c] (biases,
+ * gamma and beta may be NULL).
+ *   c = 64, 128, 256: one kernel; each intermediate is rounded to the storage
+ * type where the slot sequence stores it, and the 4c-wide hidden rows never
+ * leave the chip.
+ *   c a multiple of 128 from 512 (the decoder's 512 and 1024 levels, where a
+ * 128-row tile's normalised rows alone would take 128 KB of the 160 KB of
+ * LDS): row_norm, then mlp0 + SiLU and mlp2 as GEMMs through n x c and
+ * n x 4c intermediates, the residual added to mlp2's fp32 sums in the GEMM
+ * library's epilogue (one rounding where the slots round mlp2's output and
+ * then the sum; with the LINEAR_KERNEL policy, or rows the library does not
+ * take, the slots' two roundings).
+ * TRELLIS_STATUS_NOT_IMPLEMENTED for other widths or unless compute_dtype is
+ * F16 or BF16; callers then run the slot sequence. */
 trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend, const trellis_sparse_buffer * x,
                                                const float * gamma, const float * beta, const float * mlp0_w,
                                                const float * mlp0_b, const float * mlp2_w, const float * mlp2_b,
@@ -456,10 +463,9 @@ trellis_status trellis_sparse_hip_convnext_mlp(trellis_sparse_backend * backend,
  * out = h + mlp2(SiLU(mlp0(row_norm(sparse_conv3d(h), gamma, beta, eps)))),
  * h and out [n][c] (out must not be h), conv_w fp32 [c][27][c], conv_b [c],
  * the rest as in trellis_sparse_hip_convnext_mlp: the conv into one n x c
- * intermediate, then the fused tail.  Storage roundings where the slot
- * sequence stores.
+ * intermediate, then the tail (roundings as there).
  * TRELLIS_STATUS_NOT_IMPLEMENTED unless compute_dtype is F16 or BF16 and c is
- * 64, 128 or 256. */
+ * 64, 128, 256 or a multiple of 128 from 512. */
 trellis_status trellis_sparse_hip_convnext_block(trellis_sparse_backend * backend,
                                                  const trellis_sparse_rulebook * rulebook,
                                                  const trellis_sparse_buffer * h, const float * conv_w,

@@ -192,12 +192,89 @@ def test_convnext_mlp_fused_vs_slots(backends, dtype, c):
     assert err <= TOL[dtype]
 
 
+def oracle_mlp_rows(x, res, params, c, dtype, idx):
+    """The tail's slot chain on the oracle for the rows idx only (every slot
+    is row-wise), rounded where the slots store."""
+    rnd = lambda a: sh.storage_round(a, dtype)
+    gamma, beta, w0, b0, w2, b2 = params
+    m = len(idx)
+    e = rnd(orc.row_norm(np.ascontiguousarray(x[idx]), gamma, beta, m, c, 1e-6))
+    e = rnd(orc.linear(e, w0, b0, m, c, 4 * c, silu=True))
+    e = rnd(orc.linear(e, w2, b2, m, 4 * c, c))
+    return rnd(orc.add(np.ascontiguousarray(res[idx]), e))
+
+
+def sample_idx(n, step):
+    """Every step-th row, the last row and the first of each 128-row tile edge."""
+    return np.unique(np.concatenate([np.arange(0, n, step), [n - 1], np.arange(127, n, 128)[:8]]))
+
+
+@pytest.fixture(scope="module")
+def kernel_backends():
+    """16-bit backends whose linears never take the GEMM library."""
+    bes = {dt: sh.Backend(0, dt, linear_algo=sh.LINEAR_KERNEL) for dt in (sh.F16, sh.BF16)}
+    yield bes
+    for b in bes.values():
+        b.destroy()
+
+
+@pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
+@pytest.mark.parametrize("c", [512, 1024])
+@pytest.mark.parametrize("n", [1, 300, 2100])
+def test_convnext_mlp_composed_vs_oracle(backends, kernel_backends, dtype, c, n):
+    """Widths 512 and 1024 (the decoder's two deepest levels): the tail runs
+    as row_norm, mlp0 + SiLU and mlp2 with the residual added to its sums.
+    Both routes against the oracle's slot chain on sampled rows: the GEMM
+    library's (n >= 2048; one rounding of residual + mlp2 where the slots
+    round twice, within the storage tolerance) and the kernels' (n < 2048, or
+    the LINEAR_KERNEL policy: the slot roundings), and the two against each
+    other."""
+    rnd = lambda a: sh.storage_round(a, dtype)
+    rng = np.random.default_rng(7000 + c + n + dtype)
+    say(f"convnext_mlp composed dtype={dtype} c={c} n={n}")
+    x = rnd(2 * rng.standard_normal((n, c)) + 0.5)
+    res = rnd(rng.standard_normal((n, c)))
+    params = mlp_params(rng, c, dtype)
+    idx = sample_idx(n, 37)
+    exp = oracle_mlp_rows(x, res, params, c, dtype, idx)
+    outs = []
+    for be in (backends[dtype], kernel_backends[dtype]):
+        xb, rb_, yb = be.upload(x), be.upload(res), be.alloc(n * c)
+        be.convnext_mlp(xb, *params, rb_, yb, n, c, 1e-6)
+        got = be.download(yb).reshape(n, c)
+        err = max_rel_err(got[idx], exp)
+        say(f"convnext_mlp composed dtype={dtype} c={c} n={n} linear_algo={be.linear_algo} max_rel_err={err:.3e}")
+        assert err <= TOL[dtype]
+        outs.append(got)
+        xb.free(), rb_.free(), yb.free()
+    err = max_rel_err(outs[0], outs[1])
+    say(f"convnext_mlp composed dtype={dtype} c={c} n={n} library vs kernels max_rel_err={err:.3e}")
+    assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [sh.BF16])
+def test_convnext_mlp_composed_residual_is_output(backends, dtype):
+    """y may be the residual buffer itself (the library adds C = y in place;
+    the kernels' fallback goes through the row_norm intermediate)."""
+    c, n = 512, 2100
+    rnd = lambda a: sh.storage_round(a, dtype)
+    rng = np.random.default_rng(77)
+    x = rnd(rng.standard_normal((n, c)))
+    res = rnd(rng.standard_normal((n, c)))
+    params = mlp_params(rng, c, dtype)
+    be = backends[dtype]
+    xb, rb_, yb = be.upload(x), be.upload(res), be.alloc(n * c)
+    be.convnext_mlp(xb, *params, rb_, yb, n, c, 1e-6)
+    be.convnext_mlp(xb, *params, rb_, rb_, n, c, 1e-6)
+    assert np.array_equal(be.download(yb), be.download(rb_))
+
+
 def test_convnext_mlp_rejects_unsupported(backends):
-    """fp32 storage and widths other than 64 / 128 / 256 report
-    NOT_IMPLEMENTED (the caller then runs the slot sequence); nothing is
-    launched."""
+    """fp32 storage and widths other than 64 / 128 / 256 or a multiple of 128
+    from 512 report NOT_IMPLEMENTED (the caller then runs the slot sequence);
+    nothing is launched."""
     rng = np.random.default_rng(5)
-    for dtype, c in ((sh.F32, 64), (sh.BF16, 96), (sh.F16, 512)):
+    for dtype, c in ((sh.F32, 64), (sh.BF16, 96), (sh.F16, 384), (sh.BF16, 576), (sh.F32, 512)):
         be = backends[dtype]
         n = 10
         gamma, beta, w0, b0, w2, b2 = mlp_params(rng, c, dtype)
@@ -226,8 +303,7 @@ def oracle_convnext_block(coords, h, params, c, dtype):
 
 
 @pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
-@pytest.mark.parametrize("c", [64, 128, 256])
-@pytest.mark.parametrize("n", [1, 300, 6000])
+@pytest.mark.parametrize("c,n", [(c, n) for c in (64, 128, 256) for n in (1, 300, 6000)] + [(512, 300), (512, 2100)])
 def test_convnext_block_entry_vs_oracle(backends, dtype, c, n):
     """trellis_sparse_hip_convnext_block (the conv, then the fused tail)
     against the oracle's slot chain from the block input; the tolerance is the
@@ -283,13 +359,13 @@ def test_convnext_block_entry_vs_slots(backends, dtype, c):
 
 
 def test_convnext_block_entry_rejects(backends):
-    """fp32 storage, c other than 64 / 128 / 256, and out aliasing h are
-    refused before anything is launched."""
+    """fp32 storage, c other than 64 / 128 / 256 or a multiple of 128 from
+    512, and out aliasing h are refused before anything is launched."""
     rng = np.random.default_rng(6)
     coords = shell_coords(50)
     n = coords.shape[0]
     for dtype, c, status in ((sh.F32, 64, sh.NOT_IMPLEMENTED), (sh.BF16, 96, sh.NOT_IMPLEMENTED),
-                             (sh.F16, 512, sh.NOT_IMPLEMENTED)):
+                             (sh.F16, 384, sh.NOT_IMPLEMENTED)):
         be = backends[dtype]
         rb = be.build_rulebook(coords)
         hb, out = be.upload(np.zeros((n, c), np.float32)), be.alloc(n * c)

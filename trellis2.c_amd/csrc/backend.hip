@@ -622,12 +622,21 @@ void op_free_buffer(trellis_sparse_backend * backend, trellis_sparse_buffer * bu
     free(buffer);
 }
 
+// y = x W^T + b (then SiLU).  With a residual (no SiLU): y = residual +
+// (x W^T + b), residual [n][co] (may be y): the GEMM library adds it to the
+// fp32 sums before the one rounding; the kernels write the rounded linear
+// output to scratch ([n][co], neither y nor residual) and the add kernel
+// forms the sum.
 trellis_status linear_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * weight,
-                           const float * bias, trellis_sparse_buffer * y, int64_t n, int ci, int co, int silu) {
+                           const float * bias, trellis_sparse_buffer * y, int64_t n, int ci, int co, int silu,
+                           const trellis_sparse_buffer * residual = nullptr, trellis_sparse_buffer * scratch = nullptr) {
     if (backend == nullptr) return TRELLIS_STATUS_INVALID_ARGUMENT;
     Backend * be = as_backend(backend);
     if (weight == nullptr || n <= 0 || ci <= 0 || co <= 0 || !float_buffer_ok(be, x, (size_t) n * ci) ||
-        !float_buffer_ok(be, y, (size_t) n * co)) {
+        !float_buffer_ok(be, y, (size_t) n * co) ||
+        (residual != nullptr && (silu || !float_buffer_ok(be, residual, (size_t) n * co) ||
+                                 !float_buffer_ok(be, scratch, (size_t) n * co) || scratch->ptr == y->ptr ||
+                                 scratch->ptr == residual->ptr))) {
         return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "linear: bad argument");
     }
     CallScope scope(be);
@@ -653,8 +662,9 @@ trellis_status linear_impl(trellis_sparse_backend * backend, const trellis_spars
             st = get_weight(be, weight, (size_t) ci * co, kLayoutLinear16, ci, co, &w16);
             if (st != TRELLIS_STATUS_OK) return st;
             stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
-            const bool done = linear_lt_run(be->lt, dt, x->ptr, w16, (const float *) bd, y->ptr, n, ci, co, silu,
-                                            be->lt_ws.ptr, be->lt_ws.bytes, be->stream);
+            const bool done =
+                linear_lt_run(be->lt, dt, x->ptr, w16, (const float *) bd, residual ? residual->ptr : nullptr, y->ptr,
+                              n, ci, co, silu, be->lt_ws.ptr, be->lt_ws.bytes, be->stream);
             stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
             if (done) return TRELLIS_STATUS_OK;
         }
@@ -666,12 +676,16 @@ trellis_status linear_impl(trellis_sparse_backend * backend, const trellis_spars
     if (st != TRELLIS_STATUS_OK) return st;
     stage_begin(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
     hipError_t err;
+    void * out = residual != nullptr ? scratch->ptr : y->ptr;
     if (mfma) {
-        err = launch_linear_mfma(dt, x->ptr, wt, (const float *) bd, y->ptr, n, ci, co, silu, be->cus, be->stream);
+        err = launch_linear_mfma(dt, x->ptr, wt, (const float *) bd, out, n, ci, co, silu, be->cus, be->stream);
     } else if (narrow) {
-        err = launch_linear_narrow(dt, x->ptr, wt, (const float *) bd, y->ptr, n, ci, co, silu, be->cus, be->stream);
+        err = launch_linear_narrow(dt, x->ptr, wt, (const float *) bd, out, n, ci, co, silu, be->cus, be->stream);
     } else {
-        err = launch_linear(dt, x->ptr, (const float *) wt, (const float *) bd, y->ptr, n, ci, co, silu, be->stream);
+        err = launch_linear(dt, x->ptr, (const float *) wt, (const float *) bd, out, n, ci, co, silu, be->stream);
+    }
+    if (err == hipSuccess && residual != nullptr) {
+        err = launch_add(dt, residual->ptr, out, y->ptr, n * co, be->stream);
     }
     stage_end(be, TRELLIS_SPARSE_HIP_STAGE_ELEMENTWISE);
     return hip_status(be, err, "linear");
@@ -687,7 +701,34 @@ trellis_status op_linear_silu(trellis_sparse_backend * backend, const trellis_sp
     return linear_impl(backend, x, weight, bias, y, n, ci, co, 1);
 }
 
-// The ConvNeXt block's MLP tail fused: y = residual + W2 SiLU(W0 LN(x) + b0) + b2.
+trellis_status norm_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * gamma,
+                         const float * beta, trellis_sparse_buffer * y, int64_t n, int c, float eps, int silu);
+
+// The tail at c >= 512 (a multiple of 128), where a tile's normalised rows
+// would fill the LDS: row_norm into an n x c intermediate, mlp0 + SiLU into
+// an n x 4c intermediate, and mlp2 with the residual added to its fp32 sums
+// (GEMM library epilogue; the kernels' fallback adds the rounded mlp2 output
+// as the slot sequence does).  The n x c intermediate is mlp2's scratch for
+// that fallback.
+bool mlp_composed_supported(int dtype, int c) { return (dtype == kF16 || dtype == kBF16) && c >= 512 && c % 128 == 0; }
+
+trellis_status mlp_composed(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * gamma,
+                            const float * beta, const float * w0, const float * b0, const float * w2,
+                            const float * b2, const trellis_sparse_buffer * residual, trellis_sparse_buffer * y,
+                            int64_t n, int c, float eps) {
+    trellis_sparse_buffer *xn = nullptr, *hid = nullptr;
+    trellis_status st = op_alloc_f32(backend, (size_t) n * c, &xn);
+    if (st == TRELLIS_STATUS_OK) st = op_alloc_f32(backend, (size_t) n * 4 * c, &hid);
+    if (st == TRELLIS_STATUS_OK) st = norm_impl(backend, x, gamma, beta, xn, n, c, eps, 0);
+    if (st == TRELLIS_STATUS_OK) st = linear_impl(backend, xn, w0, b0, hid, n, c, 4 * c, 1);
+    if (st == TRELLIS_STATUS_OK) st = linear_impl(backend, hid, w2, b2, y, n, 4 * c, c, 0, residual, xn);
+    if (hid != nullptr) op_free_buffer(backend, hid);
+    if (xn != nullptr) op_free_buffer(backend, xn);
+    return st;
+}
+
+// The ConvNeXt block's MLP tail: y = residual + W2 SiLU(W0 LN(x) + b0) + b2,
+// in one kernel for c = 64, 128 and 256, composed for wider rows.
 trellis_status mlp_impl(trellis_sparse_backend * backend, const trellis_sparse_buffer * x, const float * gamma,
                         const float * beta, const float * w0, const float * b0, const float * w2, const float * b2,
                         const trellis_sparse_buffer * residual, trellis_sparse_buffer * y, int64_t n, int c,
@@ -700,7 +741,11 @@ trellis_status mlp_impl(trellis_sparse_backend * backend, const trellis_sparse_b
         return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "convnext_mlp: bad argument");
     }
     if (!convnext_mlp_supported(be->policy.compute_dtype, c)) {
-        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, "convnext_mlp: needs bf16/fp16 storage and c = 64, 128 or 256");
+        if (mlp_composed_supported(be->policy.compute_dtype, c)) {
+            return mlp_composed(backend, x, gamma, beta, w0, b0, w2, b2, residual, y, n, c, eps);
+        }
+        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED,
+                    "convnext_mlp: needs bf16/fp16 storage and c = 64, 128, 256 or a multiple of 128 from 512");
     }
     CallScope scope(be);
     const void *g = nullptr, *bt = nullptr, *pw0 = nullptr, *pb0 = nullptr, *pw2 = nullptr, *pb2 = nullptr;
@@ -1046,8 +1091,9 @@ trellis_status block_impl(trellis_sparse_backend * backend, const trellis_sparse
         return fail(be, TRELLIS_STATUS_INVALID_ARGUMENT, "convnext_block: bad argument");
     }
     const int dt = be->policy.compute_dtype;
-    if (!convnext_mlp_supported(dt, c)) {
-        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED, "convnext_block: needs bf16/fp16 storage and c = 64, 128 or 256");
+    if (!convnext_mlp_supported(dt, c) && !mlp_composed_supported(dt, c)) {
+        return fail(be, TRELLIS_STATUS_NOT_IMPLEMENTED,
+                    "convnext_block: needs bf16/fp16 storage and c = 64, 128, 256 or a multiple of 128 from 512");
     }
     trellis_sparse_buffer * tmp = nullptr;
     trellis_status st = op_alloc_f32(backend, (size_t) n * c, &tmp);

@@ -17,8 +17,10 @@
 // Column-major view of the row-major buffers: W [co][ci] is a ci x co matrix
 // (ld ci) used transposed, x [n][ci] a ci x n matrix (ld ci), y [n][co] a
 // co x n matrix (ld co): y^T = W x^T, m = co, n = n, k = ci; the bias runs
-// along m.  Plans (descriptor, layouts, the heuristic's algorithm) are kept
-// per shape.
+// along m.  With a residual r [n][co] (same layout as y) the call computes
+// y = r + x W^T + b with beta = 1: the residual is added to the fp32 sums
+// before the one rounding.  Plans (descriptor, layouts, the heuristic's
+// algorithm) are kept per shape.
 #include "tsh_internal.h"
 
 #include <hipblaslt/hipblaslt.h>
@@ -118,11 +120,13 @@ static LinearLt::Plan * plan_for(LinearLt * lt, int dtype, int64_t n, int ci, in
     return good ? &p : nullptr;
 }
 
-// Enqueues the GEMM on stream s.  Returns false (nothing enqueued) when the
-// library has no plan for the shape or refuses the call; the caller then runs
-// its own kernel.
-bool linear_lt_run(LinearLt * lt, int dtype, const void * x, const void * w16, const float * bias, void * y,
-                   int64_t n, int ci, int co, int silu, void * workspace, size_t workspace_bytes, hipStream_t s) {
+// Enqueues the GEMM on stream s (residual: nullptr, or r of y = r + x W^T + b;
+// it may be y itself).  Returns false (nothing enqueued) when the library has
+// no plan for the shape or refuses the call; the caller then runs its own
+// kernel.
+bool linear_lt_run(LinearLt * lt, int dtype, const void * x, const void * w16, const float * bias,
+                   const void * residual, void * y, int64_t n, int ci, int co, int silu, void * workspace,
+                   size_t workspace_bytes, hipStream_t s) {
     LinearLt::Plan * p = plan_for(lt, dtype, n, ci, co, silu, bias != nullptr, workspace_bytes);
     if (p == nullptr) return false;
     if (bias != nullptr &&
@@ -130,8 +134,9 @@ bool linear_lt_run(LinearLt * lt, int dtype, const void * x, const void * w16, c
             HIPBLAS_STATUS_SUCCESS) {
         return false;
     }
-    const float alpha = 1.0f, beta = 0.0f;
-    return hipblasLtMatmul(lt->handle, p->desc, &alpha, w16, p->la, x, p->lb, &beta, y, p->ld, y, p->ld, &p->algo,
+    const float alpha = 1.0f, beta = residual != nullptr ? 1.0f : 0.0f;
+    const void * c = residual != nullptr ? residual : y;
+    return hipblasLtMatmul(lt->handle, p->desc, &alpha, w16, p->la, x, p->lb, &beta, c, p->ld, y, p->ld, &p->algo,
                            workspace, p->workspace, s) == HIPBLAS_STATUS_SUCCESS;
 }
 

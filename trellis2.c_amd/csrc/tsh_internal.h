@@ -255,12 +255,15 @@ hipError_t launch_linear_mfma(int dtype, const void * x, const void * w16, const
 // 16-bit storage with Ci, Co >= 256 and n >= 2048; weights [co][ci] in the
 // storage type.  linear_lt_run enqueues on s and returns true, or returns
 // false with nothing enqueued (no plan for the shape, or the library refused).
+// A non-null residual r (same layout as y, may be y) gives y = r + x W^T + b,
+// added to the fp32 sums before the one rounding.
 struct LinearLt;
 bool linear_lt_wanted(int dtype, int64_t n, int ci, int co);
 LinearLt * linear_lt_create();
 void linear_lt_destroy(LinearLt * lt);
-bool linear_lt_run(LinearLt * lt, int dtype, const void * x, const void * w16, const float * bias, void * y,
-                   int64_t n, int ci, int co, int silu, void * workspace, size_t workspace_bytes, hipStream_t s);
+bool linear_lt_run(LinearLt * lt, int dtype, const void * x, const void * w16, const float * bias,
+                   const void * residual, void * y, int64_t n, int ci, int co, int silu, void * workspace,
+                   size_t workspace_bytes, hipStream_t s);
 // Fused ConvNeXt MLP tail (kernels_block.hip): bf16/fp16, C = 64, 128 or 256.
 // w0 [C/8][4C][8] and w2 [4C/8][C][8] in the storage type with the grouped
 // column packing of the MFMA linear, groups g0 and g2 from convnext_mlp_groups.

@@ -305,6 +305,7 @@ class Backend:
         self.struct = ctypes.cast(out, POINTER(BackendStruct)).contents
         self.ops = self.struct.ops.contents
         self.dtype = dtype
+        self.linear_algo = linear_algo
         self.alive = True
         self._keep = []  # host arrays whose pointers the weight cache is keyed on
 
