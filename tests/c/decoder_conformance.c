@@ -292,7 +292,9 @@ int main(int argc, char ** argv) {
     /* fp32: the reference test's 1e-4 (test_sparse_decoder_backend.c:238);
      * bf16: a chain of ~20 slots, each rounding to bf16 with the oracle
      * mirroring every rounding; a one-ulp flip (2^-8 relative) early in the
-     * chain is carried by every later slot. */
+     * chain is carried by every later slot (measured on the medium model:
+     * 2.7e-2 at the output).  Each slot on its own meets 2e-2 against the
+     * oracle fed the device's own input (tests/test_gpu_blocks.py). */
     const float tol = g_dtype == TRELLIS_SPARSE_HIP_F32 ? 1e-4f : 5e-2f;
 
     model m;

@@ -376,7 +376,10 @@ int main(int argc, char ** argv) {
     g_dtype = strcmp(argv[2], "bf16") == 0 ? TRELLIS_SPARSE_HIP_BF16 : TRELLIS_SPARSE_HIP_F32;
     /* Chain tolerance - fp32: 1e-4, as the decoder conformance; bf16: a chain
      * of ~20 rounded slots mirrored by the oracle, where a one-ulp flip
-     * (2^-8 relative) early on is carried by every later slot.  Known-answer
+     * (2^-8 relative) early on is carried by every later slot (measured on
+     * the medium model: 3.5e-2 on the last level's features, 3.8e-2 on the
+     * latent; each slot on its own meets 2e-2, tests/test_gpu_blocks.py and
+     * tests/test_gpu_s2c.py).  Known-answer
      * latent - fp32: the reference test's 3e-4; bf16: the normalised value
      * and the latent are each stored rounded (2^-9 relative apiece). */
     const float tol = g_dtype == TRELLIS_SPARSE_HIP_F32 ? 1e-4f : 5e-2f;
