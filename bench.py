@@ -625,11 +625,12 @@ def main():
     # map 16 N + 108 N + 8 P + 216, the 108 N being an [N][27] neighbour
     # table), and the bytes the production build moves, which writes row
     # masks and per-tile pair lists instead of that table (hash 28 N; map
-    # 16 N coordinates + 4 N masks + 8 P pairs + 2 x 108 bytes per 256-row
+    # 16 N coordinates + 4 N masks + 5 P pairs (a 4-byte source row and a
+    # 1-byte destination row within the tile) + 2 x 108 bytes per 256-row
     # tile of counts and list starts).
     hm_def_bytes = wl.hash_bytes(job.m) + wl.map_bytes(job.m, job.pairs)
     tiles = (job.m + 255) // 256
-    hm_moved_bytes = 28.0 * job.m + 16.0 * job.m + 4.0 * job.m + 8.0 * job.pairs + 216.0 * tiles
+    hm_moved_bytes = 28.0 * job.m + 16.0 * job.m + 4.0 * job.m + 5.0 * job.pairs + 216.0 * tiles
     hm_gbs = hm_def_bytes / (hm_ms * 1e-3) / 1e9 if hm_ms > 0 else 0.0
     elem = 4 if spec["dtype"] == sh.F32 else 2
     # The conv's binding roofline: compute (2 P Ci Co at the dtype's MFMA or

@@ -858,7 +858,7 @@ trellis_status map_pass(Backend * be, trellis_sparse_rulebook * r, hipStream_t s
                                        r->table_slots, (const int32_t *) r->pool.ptr, (int32_t *) r->nbr.ptr,
                                        (uint32_t *) r->mask.ptr, (int32_t *) r->tile_counts.ptr,
                                        (int32_t *) r->tile_off.ptr, (int32_t *) r->pair_src.ptr,
-                                       (int32_t *) r->pair_dst.ptr, (int32_t *) r->counters.ptr, s),
+                                       (uint8_t *) r->pair_dst.ptr, (int32_t *) r->counters.ptr, s),
                       "kernel map");
 }
 
@@ -888,7 +888,7 @@ trellis_status rulebook_build_device(Backend * be, const int32_t * coords, int64
         {&r->tile_counts, (size_t) r->n_tiles * 27 * 4},
         {&r->tile_off, (size_t) r->n_tiles * 27 * 4},
         {&r->pair_src, (size_t) r->n_tiles * kMapTile * 27 * 4},
-        {&r->pair_dst, (size_t) r->n_tiles * kMapTile * 27 * 4},
+        {&r->pair_dst, (size_t) r->n_tiles * kMapTile * 27},
     };
     for (const Need & q : need) {
         if (q.bytes == 0) continue;
@@ -1011,7 +1011,7 @@ trellis_status conv_impl(trellis_sparse_backend * backend, const trellis_sparse_
                                  (const float *) bd, out->ptr, n, ci, co, be->stream);
         } else if (algo == TRELLIS_SPARSE_HIP_CONV_COMPACT) {
             err = launch_conv_mfma_stream(dt, feats->ptr, (const int32_t *) rulebook->pair_src.ptr,
-                                          (const int32_t *) rulebook->pair_dst.ptr,
+                                          (const uint8_t *) rulebook->pair_dst.ptr,
                                           (const int32_t *) rulebook->tile_off.ptr,
                                           (const int32_t *) rulebook->tile_counts.ptr,
                                           (const uint32_t *) rulebook->mask.ptr, w, (const float *) bd, out->ptr, n,
@@ -2029,12 +2029,13 @@ trellis_status trellis_sparse_hip_download_pairs(trellis_sparse_backend * backen
     // The device lists are tile-major; reorder them to the canonical
     // offset-major order (destination ascending within an offset).
     const size_t span = (size_t) tiles * tsh::kMapTile * 27;  // every tile's region
-    std::vector<int32_t> hs(span), hd(span);
+    std::vector<int32_t> hs(span);
+    std::vector<uint8_t> hd(span);
     err = hipMemcpyAsync(off.data(), rulebook->tile_off.ptr, off.size() * 4, hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess && total > 0)
         err = hipMemcpyAsync(hs.data(), rulebook->pair_src.ptr, span * 4, hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess && total > 0)
-        err = hipMemcpyAsync(hd.data(), rulebook->pair_dst.ptr, span * 4, hipMemcpyDeviceToHost, be->stream);
+        err = hipMemcpyAsync(hd.data(), rulebook->pair_dst.ptr, span, hipMemcpyDeviceToHost, be->stream);
     if (err == hipSuccess) err = hipStreamSynchronize(be->stream);
     if (err != hipSuccess) return tsh::hip_status(be, err, "download_pairs");
     int64_t at = 0;
@@ -2043,7 +2044,9 @@ trellis_status trellis_sparse_hip_download_pairs(trellis_sparse_backend * backen
             const int64_t from = off[(size_t) t * 27 + k], c = cnt[(size_t) t * 27 + k];
             if (c <= 0) continue;
             if (src_out != nullptr) memcpy(src_out + at, hs.data() + from, (size_t) c * 4);
-            if (dst_out != nullptr) memcpy(dst_out + at, hd.data() + from, (size_t) c * 4);
+            if (dst_out != nullptr) {
+                for (int64_t j = 0; j < c; ++j) dst_out[at + j] = (int32_t) (t * tsh::kMapTile + hd[(size_t) (from + j)]);
+            }
             at += c;
         }
     }

@@ -360,7 +360,7 @@ __global__ void __launch_bounds__(256) k_conv_mfma_masked(const typename Store<D
 template <int DT, int BN, int DEPTH, int NW, int RG, int UPB>
 __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Store<DT>::T * __restrict__ x,
                                                                const int32_t * __restrict__ pair_src,
-                                                               const int32_t * __restrict__ pair_dst,
+                                                               const uint8_t * __restrict__ pair_dst,
                                                                const int32_t * __restrict__ tile_off,
                                                                const int32_t * __restrict__ tile_counts,
                                                                const typename Store<DT>::T * __restrict__ w16,
@@ -420,8 +420,9 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
     const int CU = (tile_rows + PASS - 1) / PASS;
     const int64_t region = tile * TM * 27;
     const int le = t & (PASS - 1);
-    const int32_t * list = t < PASS ? pair_src : pair_dst;
-    const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
+    // Entry pos of this thread's list: sources (threads 0..PASS-1) or the
+    // destinations' rows within the map tile (threads PASS..2 PASS-1).
+    auto list_at = [&](int64_t pos) -> int32_t { return t < PASS ? pair_src[pos] : (int32_t) pair_dst[pos]; };
     // One round trip for the tile's counts and starts and the centre units'
     // lists among the first 2 UPB units (the ring fill below).
     int32_t cnt_v = 0, off_v = 0;
@@ -433,7 +434,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
 #pragma unroll
     for (int j = 0; j < 2 * UPB; ++j) {
         const int cj = tile_rows - j * PASS < PASS ? tile_rows - j * PASS : PASS;
-        ring_v[j] = (t < 2 * PASS && j < CU) ? list[region + j * PASS + (le < cj ? le : cj - 1)] : 0;
+        ring_v[j] = (t < 2 * PASS && j < CU) ? list_at(region + j * PASS + (le < cj ? le : cj - 1)) : 0;
     }
     if (t < 27) {
         s_cnt[t] = cnt_v;
@@ -475,14 +476,14 @@ __global__ void __launch_bounds__(64 * NW) k_conv_mfma_stream(const typename Sto
         if (t >= 2 * PASS) return 0;
         const int lu = u < U ? u : U - 1;
         const int c = s_ucnt[lu];
-        return list[s_ustart[lu] + (le < c ? le : c - 1)];
+        return list_at(s_ustart[lu] + (le < c ? le : c - 1));
     };
     auto list_store = [&](int u, int32_t v) {
         if (t < PASS) {
             s_rsrc[u & (RING - 1)][le] = v;
         } else if (t < 2 * PASS) {
             const int c = s_ucnt[u < U ? u : U - 1];
-            s_rdst[u & (RING - 1)][le] = (uint16_t) (le < c ? v - list_bias : TM);
+            s_rdst[u & (RING - 1)][le] = (uint16_t) (le < c ? v : TM);
         }
     };
 #pragma unroll
@@ -740,7 +741,7 @@ __device__ __forceinline__ float row16_sum(float v) {
 template <int DT, int BN, int RG, int UPB, int DEPTH, int TMR, int NW, int AP = 1>
 __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,
                                                         const int32_t * __restrict__ pair_src,
-                                                        const int32_t * __restrict__ pair_dst,
+                                                        const uint8_t * __restrict__ pair_dst,
                                                         const int32_t * __restrict__ tile_off,
                                                         const int32_t * __restrict__ tile_counts,
                                                         const uint32_t * __restrict__ mask,
@@ -828,8 +829,11 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
     // order, so this block's rows start `half * TM` entries into it.
     const int64_t region = tile * kMapTile * 27 + half * TM;
     const int le = t & (PASS - 1);
-    const int32_t * list = t < PASS ? pair_src : pair_dst;
-    const int32_t list_bias = t < PASS ? 0 : (int32_t) row0;
+    // Entry pos of this thread's list: sources (threads 0..PASS-1) or the
+    // destinations' rows within the map tile (threads PASS..2 PASS-1; this
+    // block's rows start at half * TM of the tile).
+    auto list_at = [&](int64_t pos) -> int32_t { return t < PASS ? pair_src[pos] : (int32_t) pair_dst[pos]; };
+    const int32_t list_bias = half * TM;
     // One round trip for the tile's counts and starts and the centre units'
     // lists among the first 2 UPB units (the ring fill below).
     int32_t cnt_v = 0, off_v = 0;
@@ -841,7 +845,7 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
 #pragma unroll
     for (int j = 0; j < 2 * UPB; ++j) {
         const int cj = tile_rows - j * PASS < PASS ? tile_rows - j * PASS : PASS;
-        ring_v[j] = (t < 2 * PASS && j < CU) ? list[region + j * PASS + (le < cj ? le : cj - 1)] : 0;
+        ring_v[j] = (t < 2 * PASS && j < CU) ? list_at(region + j * PASS + (le < cj ? le : cj - 1)) : 0;
     }
     if (t < 27) {
         s_cnt[t] = cnt_v;
@@ -906,7 +910,7 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
         if (t >= 2 * PASS) return 0;
         const int lu = u < U ? u : U - 1;
         const int c = s_ucnt[lu];
-        return list[s_ustart[lu] + (le < c ? le : c - 1)];
+        return list_at(s_ustart[lu] + (le < c ? le : c - 1));
     };
     auto list_store = [&](int u, int32_t v) {
         if (t < PASS) {
@@ -1449,7 +1453,7 @@ bool conv_stream_supported(int dtype, int ci, int co) {
 
 namespace {
 template <int DT, int BN, int DEPTH, int NW, int RG, int UPB>
-hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
+hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const uint8_t * pair_dst,
                            const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
                            const void * w16, const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
                            const ConvEpilogue & epi) {
@@ -1501,7 +1505,7 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const int32
 }
 
 template <int DT>
-hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const int32_t * pair_dst,
+hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const uint8_t * pair_dst,
                             const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
                             const void * w16, const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
                             const ConvEpilogue & epi) {
@@ -1543,7 +1547,7 @@ hipError_t launch_conv_os(int dtype, const void * x, const int32_t * pair_src, c
     return hipGetLastError();
 }
 
-hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const int32_t * pair_dst,
+hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const uint8_t * pair_dst,
                                    const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
                                    hipStream_t s, const ConvEpilogue & epi) {

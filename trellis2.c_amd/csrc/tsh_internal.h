@@ -147,7 +147,7 @@ struct trellis_sparse_rulebook {
     tsh::DevMem tile_counts; // int32  [n_tiles][27]
     tsh::DevMem tile_off;    // int32  [n_tiles][27] start of (tile, k) in the pair arrays
     tsh::DevMem pair_src;    // int32  [n_tiles][kMapTile * 27]: per tile, offsets ascending, dst ascending
-    tsh::DevMem pair_dst;    // int32  [n_tiles][kMapTile * 27]
+    tsh::DevMem pair_dst;    // uint8  [n_tiles][kMapTile * 27]: destination row within the tile
 };
 
 struct trellis_sparse_c2s_device_map {
@@ -187,7 +187,7 @@ hipError_t launch_voxel_insert(const int32_t * coords, int64_t n, const uint64_t
 // [t * kMapTile * 27, (t + 1) * kMapTile * 27) of the pair arrays.
 hipError_t launch_map_tiles(const int32_t * coords, int64_t n, const uint64_t * table,
                             int64_t slots, const int32_t * pool, int32_t * nbr, uint32_t * mask,
-                            int32_t * tile_counts, int32_t * tile_off, int32_t * pair_src, int32_t * pair_dst,
+                            int32_t * tile_counts, int32_t * tile_off, int32_t * pair_src, uint8_t * pair_dst,
                             int32_t * counters, hipStream_t s);
 
 // Convolution (kernels_conv.hip).  Weight layouts are produced by the backend.
@@ -222,7 +222,7 @@ enum { kEpiNone = 0, kEpiNorm = 1, kEpiAdd = 2 };
 bool conv_wide_supported(int ci, int co);
 int conv_stream_group(int ci, int co);
 bool conv_stream_supported(int dtype, int ci, int co);
-hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const int32_t * pair_dst,
+hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const uint8_t * pair_dst,
                                    const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
                                    hipStream_t s, const ConvEpilogue & epi = ConvEpilogue());
