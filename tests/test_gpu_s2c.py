@@ -116,6 +116,42 @@ def test_s2c_from_device_coords_and_rejects(backends):
     check_map(be, fine, fmap2, cmap2)
 
 
+def test_s2c_repeat_found_at_any_distance(backends):
+    """A repeated fine voxel is a parse error wherever the repeat sits.  The
+    build compares each row with the up to 8 rows before it in its coarse
+    voxel (in input order); of any 9 rows of one coarse voxel two share a
+    child slot, so that finds every repeat.  Cases: all eight children of one
+    coarse voxel between the two rows, with rows of other coarse voxels
+    interleaved (the repeat is then exactly 8 rows back in its coarse voxel),
+    a coarse voxel with two repeats, and random sets with one row repeated at
+    a random later position; a set without repeats still builds."""
+    be = backends[sh.BF16]
+    children = [[0, x, y, z] for x in (2, 3) for y in (4, 5) for z in (6, 7)]
+    others = [[0, 10 + 2 * i, 0, 0] for i in range(8)]
+    rows = []
+    for c, o in zip(children, others):
+        rows += [c, o]
+    rows.append(children[0])
+    with pytest.raises(sh.HipError) as ei:
+        be.s2c_build_device(np.array(rows, np.int32))
+    assert ei.value.status == sh.PARSE_ERROR
+    rows2 = children + [children[5], children[2]]
+    with pytest.raises(sh.HipError) as ei:
+        be.s2c_build_device(np.array(rows2, np.int32))
+    assert ei.value.status == sh.PARSE_ERROR
+    rng = np.random.default_rng(123)
+    for trial in range(12):
+        fine = random_fine_set(rng, int(rng.integers(20, 3000)), int(rng.integers(3, 12)), 2)
+        i = int(rng.integers(0, len(fine)))
+        j = int(rng.integers(i + 1, len(fine) + 1))
+        dup = np.ascontiguousarray(np.insert(fine, j, fine[i], axis=0))
+        with pytest.raises(sh.HipError) as ei:
+            be.s2c_build_device(dup)
+        assert ei.value.status == sh.PARSE_ERROR, (trial, len(fine), i, j)
+        fmap, cmap = be.s2c_build_device(fine)
+        check_map(be, fine, fmap, cmap)
+
+
 @pytest.mark.parametrize("dtype", [sh.F32, sh.F16, sh.BF16])
 @pytest.mark.parametrize("ci,co", [(2, 8), (64, 128), (128, 256), (96, 64), (256, 16)])
 def test_s2c_pack_and_skip_mean_vs_oracle(backends, dtype, ci, co):

@@ -16,19 +16,24 @@
 // then fine row).  Here the order comes from a least-significant-digit radix
 // sort of a key holding the coarse voxel in just the bits its coordinates use
 // (b highest, then x/2, y/2, z/2, each field as wide as its largest value)
-// and the child slot in the lowest 3 bits; at most 127 bits, in two words;
-// the fine row is the payload.  Within one coarse voxel the order is by child
-// slot instead of fine row, which changes nothing the map records (parent,
-// subidx and the child table are slot-indexed) and puts the two rows of a
-// repeated fine voxel next to each other, so every repeat is found (the
-// reference compares neighbours in fine-row order and misses a repeat with
-// another child of the same coarse voxel between them).  Per 8-bit pass: a
-// per-tile digit histogram, one exclusive scan over the digit-major
-// [256][tiles] counts, and a stable scatter (ranks within a 64-element round
-// from eight ballots, running per-digit counters per wavefront in LDS).
-// Afterwards head flags, a scan of them and one pass that writes parent,
-// the coarse voxels and the [coarse][8] child table, which makes pack and
-// skip mean plain gathers with coalesced stores.
+// above the child slot in the lowest 3 bits; at most 127 bits, in two words;
+// the fine row is the payload.  The passes cover the coarse-voxel bits only
+// (digits from bit 3): the slot bits ride along unsorted, so within one
+// coarse voxel the rows keep their input order, as in the reference, and the
+// config-3 children's 27-bit key takes 3 passes instead of 4.  Nothing the
+// map records depends on that order (parent, subidx and the child table are
+// slot-indexed).  A repeated fine voxel (two rows in one child slot) is found
+// by each row comparing its whole key with the up to 8 rows before it in its
+// coarse voxel: of any 9 rows of one coarse voxel two share a slot, so a
+// repeat always lies within 8 rows of another (the reference compares
+// neighbours in fine-row order only and misses a repeat with another child of
+// the same coarse voxel between them).  Per 8-bit pass: a per-tile digit
+// histogram, one exclusive scan over the digit-major [256][tiles] counts, and
+// a stable scatter (ranks within a 64-element round from eight ballots,
+// running per-digit counters per wavefront in LDS).  Afterwards head flags,
+// a scan of them and one pass that writes parent, the coarse voxels and the
+// [coarse][8] child table, which makes pack and skip mean plain gathers with
+// coalesced stores.
 #include "tsh_internal.h"
 
 namespace tsh {
@@ -152,8 +157,11 @@ __global__ void __launch_bounds__(256) k_s2c_keys(const int32_t * __restrict__ c
     }
 }
 
+// The 8-bit digit at bit `shift` of the key (lo, hi); digits start at bit 3,
+// so one of them may straddle the two words.
 template <bool WIDE> __device__ inline int digit_of(uint64_t lo, uint64_t hi, int shift) {
     if (WIDE && shift >= 64) return (int) ((hi >> (shift - 64)) & 255u);
+    if (WIDE && shift > 56) return (int) (((lo >> shift) | (hi << (64 - shift))) & 255u);
     return (int) ((lo >> shift) & 255u);
 }
 
@@ -249,17 +257,25 @@ __global__ void __launch_bounds__(kSortBlock) k_radix_scatter(const uint64_t * _
 }
 
 // head[i] = 1 where sorted key i starts a coarse voxel; flags[0] bit 1 when a
-// whole key repeats (the same fine voxel twice).
+// whole key repeats (the same fine voxel twice) within the 8 rows before it
+// in its coarse voxel, which finds every repeat (see the top of this file).
 template <bool WIDE>
 __global__ void __launch_bounds__(256) k_s2c_heads(const uint64_t * __restrict__ klo, const uint64_t * __restrict__ khi,
                                                    int64_t n, int32_t * __restrict__ head, int32_t * __restrict__ flags) {
     for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t) gridDim.x * blockDim.x) {
-        bool h = true;
-        if (i > 0) {
-            const bool hi_same = !WIDE || khi[i] == khi[i - 1];
-            h = !hi_same || (klo[i] >> 3) != (klo[i - 1] >> 3);
-            if (hi_same && klo[i] == klo[i - 1]) atomicOr(&flags[0], 2);
+        const uint64_t lo = klo[i];
+        const uint64_t hi = WIDE ? khi[i] : 0;
+        bool h = true, repeat = false;
+#pragma unroll
+        for (int j = 1; j <= 8; ++j) {
+            if (i - j < 0) break;
+            const uint64_t pl = klo[i - j];
+            const bool same = (!WIDE || khi[i - j] == hi) && (pl >> 3) == (lo >> 3);
+            if (!same) break;
+            if (j == 1) h = false;
+            repeat = repeat || pl == lo;
         }
+        if (repeat) atomicOr(&flags[0], 2);
         head[i] = h ? 1 : 0;
     }
 }
@@ -411,7 +427,7 @@ hipError_t launch_s2c_sort(const int32_t * coords, int64_t n, const int shifts[4
     hipError_t err = hipGetLastError();
     const int n_tiles = (int) ((n + kSortTile - 1) / kSortTile);
     int cur = 0;
-    for (int shift = 0; shift < key_bits && err == hipSuccess; shift += 8) {
+    for (int shift = 3; shift < key_bits && err == hipSuccess; shift += 8) {
         if (wide) {
             k_radix_count<true><<<n_tiles, kSortBlock, 0, s>>>(klo[cur], khi[cur], n, shift, hist, n_tiles);
         } else {
