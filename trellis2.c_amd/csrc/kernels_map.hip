@@ -230,9 +230,10 @@ __global__ void __launch_bounds__(kBlock) k_voxel_insert(const int4 * __restrict
 // order, starting at the region's start: a consumer can find it without the
 // tile's counts.
 // Seven wavefronts per SIMD (at most 72 registers): 4 % faster than six on
-// config 3's map, while eight spill.
+// config 3's map, while eight spill.  The launch that also writes the
+// neighbour table holds 28 KB of LDS per block, which allows five.
 template <bool NBR>
-__global__ void __launch_bounds__(kBlock, 7) k_map_tiles(const int4 * __restrict__ coords, int64_t n,
+__global__ void __launch_bounds__(kBlock, NBR ? 5 : 7) k_map_tiles(const int4 * __restrict__ coords, int64_t n,
                                                       const uint64_t * __restrict__ table, uint64_t hmask,
                                                       const int32_t * __restrict__ pool, int32_t empty_brick,
                                                       int32_t * __restrict__ nbr,
