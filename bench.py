@@ -402,6 +402,185 @@ class Block:
                 + 2 * self.n * self.ci * 8)
 
 
+class Decoder:
+    """The whole shape decoder of the sparse U-Net VAE at the reference's widths, through the backend's entry
+    points in the executor's order (src/architectures/sparse_unet_decoder/decoder.c:248-249: channels
+    {1024, 512, 256, 128, 64}, ConvNeXt blocks {4, 16, 8, 4, 0}; executor.c:560-760):
+      from_latent linear 32 -> 1024 and the rulebook on the latent voxels;
+      per level its ConvNeXt blocks (trellis_sparse_hip_convnext_block: fused tail at 256 and below, composed
+      at 512 and 1024), then a C2S up-block to the next width (subdivision logits linear(Ci -> 8) ->
+      build_c2s_map_device -> build_rulebook_for_c2s_map; row_norm_silu -> conv(Ci -> 8 Co) on the parents ->
+      c2s_gather_device; skip_repeat_device; row_norm_silu -> conv(Co -> Co) + the skip, as one
+      trellis_sparse_hip_conv_add where Co % 128 == 0, else conv and add);
+      the output head: row_norm (eps 1e-5, no affine) -> linear 64 -> 7.
+    Latent voxels: the config-3 parent shell (R = 256) reduced to R = 64 (coordinates >> 2, unique), 32 random
+    channels.  Every layer has its own random weights; the subdivision logits come from random weights with
+    zero bias, so each up-block keeps about half of the children (about four times the parent count).
+    """
+
+    CHANNELS = (1024, 512, 256, 128, 64)
+    BLOCKS = (4, 16, 8, 4, 0)
+    LATENT = 32
+    OUT = 7
+
+    def __init__(self, be):
+        self.be = be
+        rng = np.random.default_rng(17)
+        w = wl.workload(3)
+        pc = w["parent_coords"].copy()
+        pc[:, 1:] >>= 2
+        self.coords0 = np.ascontiguousarray(np.unique(pc, axis=0), dtype=np.int32)
+        self.n0 = self.coords0.shape[0]
+        self.map0 = be.upload_coords(self.coords0)
+        self.latent = be.upload(rng.standard_normal((self.n0, self.LATENT), dtype=np.float32))
+
+        def rnd(shape, fan_in):
+            return be.keep(np.ascontiguousarray(rng.standard_normal(shape, dtype=np.float32) / np.float32(np.sqrt(fan_in))))
+
+        def small(count, scale=0.1, one=False):
+            v = rng.standard_normal(count, dtype=np.float32) * np.float32(scale)
+            return be.keep(np.ascontiguousarray(v + np.float32(1) if one else v))
+
+        C = self.CHANNELS
+        self.w_in, self.b_in = rnd((C[0], self.LATENT), self.LATENT), small(C[0])
+        self.blocks = []
+        for lv, nb in enumerate(self.BLOCKS):
+            c = C[lv]
+            self.blocks.append([(rnd((c, 27, c), 27 * c), small(c), small(c, one=True), small(c),
+                                 rnd((4 * c, c), c), small(4 * c), rnd((c, 4 * c), 4 * c), small(c))
+                                for _ in range(nb)])
+        self.ups = []
+        for lv in range(len(C) - 1):
+            ci, co = C[lv], C[lv + 1]
+            self.ups.append({"ws": rnd((8, ci), ci), "bs": be.keep(np.zeros(8, np.float32)),
+                             "g1": small(ci, one=True), "b1": small(ci),
+                             "w1": rnd((8 * co, 27, ci), 27 * ci), "c1b": small(8 * co),
+                             "w2": rnd((co, 27, co), 27 * co), "c2b": small(co)})
+        self.w_out, self.b_out = rnd((self.OUT, C[-1]), C[-1]), small(self.OUT)
+        self.stats = None
+
+    def forward(self, marks=False, stats=False):
+        """One forward; with marks, HIP events 0.. at the stage boundaries; with stats, the per-level sizes
+        (read back from the device: the host waits, so those forwards are not the timed ones)."""
+        be = self.be
+        C = self.CHANNELS
+        ev = iter(range(16))
+        names = []
+
+        def mark(name):
+            if marks:
+                be.event(next(ev))
+                names.append(name)
+
+        stat_rows = []
+        mark("start")
+        n = self.n0
+        h = be.alloc(n * C[0])
+        be.linear(self.latent, self.w_in, self.b_in, h, n, self.LATENT, C[0])
+        dmap = self.map0
+        rb = be.build_rulebook_for_c2s_map(dmap)
+        mark("from_latent")
+        owned = None  # the current level's map when an up-block made it
+        for lv, c in enumerate(C):
+            pairs = be.rulebook_stats(rb)["pairs"] if stats else 0
+            for p in self.blocks[lv]:
+                out = be.alloc(n * c)
+                be.convnext_block(rb, h, *p, out, c, 1e-6)
+                h.free()
+                h = out
+            mark(f"level{lv}_convnext")
+            stat_rows.append({"channels": c, "voxels": int(n), "pairs": int(pairs), "convnext_blocks": len(self.blocks[lv])})
+            if lv == len(C) - 1:
+                break
+            u, co = self.ups[lv], C[lv + 1]
+            subdiv = be.alloc(n * 8)
+            be.linear(h, u["ws"], u["bs"], subdiv, n, c, 8)
+            cmap = be.build_c2s_map_device(subdiv, n, coords_map=dmap)
+            m = cmap.n
+            crb = be.build_rulebook_for_c2s_map(cmap)
+            norm1, conv1 = be.alloc(n * c), be.alloc(n * 8 * co)
+            be.row_norm(h, u["g1"], u["b1"], norm1, n, c, 1e-6, silu=True)
+            be.conv(rb, norm1, u["w1"], u["c1b"], conv1, c, 8 * co)
+            h_up, skip, norm2, out = be.alloc(m * co), be.alloc(m * co), be.alloc(m * co), be.alloc(m * co)
+            be.c2s_gather_device(conv1, cmap, h_up, co)
+            be.skip_repeat_device(h, cmap, skip, c, co)
+            be.row_norm(h_up, None, None, norm2, m, co, 1e-6, silu=True)
+            if co % 128 == 0:
+                be.conv_add(crb, norm2, u["w2"], u["c2b"], skip, out, co, co)
+            else:
+                conv2 = be.alloc(m * co)
+                be.conv(crb, norm2, u["w2"], u["c2b"], conv2, co, co)
+                be.add(conv2, skip, out, m * co)
+                conv2.free()
+            if stats:
+                stat_rows[-1]["up_parent_pairs"] = int(pairs)
+                stat_rows[-1]["up_child_pairs"] = int(be.rulebook_stats(crb)["pairs"])
+            for b in (subdiv, norm1, conv1, h_up, skip, norm2, h):
+                b.free()
+            rb.free()
+            if owned is not None:
+                be.free_map(owned)
+            h, n, rb, dmap, owned = out, m, crb, cmap, cmap
+            mark(f"level{lv}_c2s")
+        norm, y = be.alloc(n * C[-1]), be.alloc(n * self.OUT)
+        be.row_norm(h, None, None, norm, n, C[-1], 1e-5)
+        be.linear(norm, self.w_out, self.b_out, y, n, C[-1], self.OUT)
+        mark("head")
+        for b in (norm, y, h):
+            b.free()
+        rb.free()
+        if owned is not None:
+            be.free_map(owned)
+        if stats:
+            self.stats = stat_rows
+        if marks:
+            self.marks = names
+
+    def flops(self):
+        """Convs (2 P Ci Co), the ConvNeXt MLPs and the up-blocks' convs, at the sizes the stats forward read back."""
+        C, f = self.CHANNELS, 0.0
+        for lv, st in enumerate(self.stats):
+            c, n = C[lv], st["voxels"]
+            f += st["convnext_blocks"] * (wl.conv_flops(st["pairs"], c, c) + 2 * (2 * n * c * 4 * c))
+            if "up_child_pairs" in st:
+                co = C[lv + 1]
+                f += wl.conv_flops(st["up_parent_pairs"], c, 8 * co) + wl.conv_flops(st["up_child_pairs"], co, co)
+        return f
+
+
+def run_decoder(args):
+    be = sh.Backend(0, sh.BF16)
+    log("bench: building the decoder's random weights")
+    dec = Decoder(be)
+    log(f"bench: decoder from {dec.n0} latent voxels")
+    for _ in range(max(1, args.warmup)):
+        dec.forward()
+    be.synchronize()
+    dec.forward(stats=True)  # sizes
+    be.synchronize()
+    dec.forward(marks=True)  # the stage split, from a forward with no read-backs of its own
+    be.synchronize()
+    split = {dec.marks[i]: round(be.elapsed(i - 1, i), 3) for i in range(1, len(dec.marks))}
+    be.synchronize()
+    be.event(14)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dec.forward()
+    be.event(15)
+    be.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    dev = be.elapsed(14, 15) / args.steps
+    ms = max(dev, wall)
+    print(json.dumps({"bench": "decoder", "dtype": "bf16",
+                      "data": "synthetic (config-3 parent shell reduced to R = 64 as the latent voxels; random weights "
+                              "per layer; subdivision from random logits)",
+                      "steps": args.steps, "warmup": max(1, args.warmup), "ms_per_forward": round(ms, 3),
+                      "device_ms_per_forward": round(dev, 3), "wall_ms_per_forward": round(wall, 3),
+                      "effective_tflops": round(dec.flops() / (ms * 1e-3) / 1e12, 1),
+                      "levels": dec.stats, "stage_ms": split}))
+    be.destroy()
+
+
 def run_block(args):
     be = sh.Backend(0, sh.BF16)
     job = Block(be, args.block, slots=args.slots, channels=args.channels)
@@ -557,6 +736,9 @@ def main():
     ap.add_argument("--slots", action="store_true",
                     help="config 2 and the c2s / s2c blocks: run conv -> row_norm_silu and conv -> add as separate "
                          "slots instead of the convs with fused epilogues")
+    ap.add_argument("--decoder", action="store_true",
+                    help="instead of the configuration step, time the whole shape decoder at the reference's widths "
+                         "(5 levels, 32 ConvNeXt blocks, 4 up-blocks) and print its own JSON line")
     ap.add_argument("--calibrate", action="store_true",
                     help="run one fp32 add over 2 x 64Mi-element inputs (512 MiB read, 256 MiB written) so PMC "
                          "byte counters can be scaled against a streaming kernel of known traffic")
@@ -582,6 +764,8 @@ def main():
     if sh.device_count() < 1:
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
+    if args.decoder:
+        return run_decoder(args)
     if args.block is not None:
         run_block(args)
         return

@@ -190,6 +190,66 @@ def test_conv_deep_channels_vs_oracle(backends, dtype, ci, co, n):
     rb.free()
 
 
+def mixed_density_sets(rng):
+    """A solid 12^3 box and, far from it, a 40^3 region filled at 30 %.  Of
+    the map tiles' offsets with pairs, 9 in 10 have more than 128 in the box
+    (Co % 256 == 0 takes the 256-column layout there), 1 in 27 in the sparse
+    part and 1 in 8 in the union (the 128-column layout)."""
+    g = np.stack(np.meshgrid(*(np.arange(12),) * 3, indexing="ij"), -1).reshape(-1, 3)
+    box = np.concatenate([np.zeros((g.shape[0], 1), np.int64), g], 1)
+    pts = rng.integers(0, 40, (int(0.3 * 40 ** 3), 3)) + 100
+    sparse = np.unique(np.concatenate([np.zeros((pts.shape[0], 1), np.int64), pts], 1), axis=0)
+    sparse = sparse[rng.permutation(sparse.shape[0])]
+    return np.ascontiguousarray(box.astype(np.int32)), np.ascontiguousarray(sparse.astype(np.int32))
+
+
+@pytest.mark.parametrize("ci,co", [(128, 256), (256, 512), (512, 256)])
+def test_conv_layouts_bitexact(backends, ci, co):
+    """Co % 256 == 0 runs the 256-column layout on dense sets and the
+    128-column one on sparse sets (the kernel map's statistics decide).  The
+    box alone takes the first, the union of box and sparse part the second:
+    the union's rows must equal, bit for bit, the same rows computed from
+    each part alone (a row's sums are formed in the same order in both
+    layouts, and the parts are too far apart to be neighbours), with and
+    without the residual epilogue (in place), and match the oracle on a
+    sample."""
+    be = backends[sh.BF16]
+    rng = np.random.default_rng(ci + co)
+    box, sparse = mixed_density_sets(rng)
+    both = np.ascontiguousarray(np.concatenate([box, sparse]))
+    nb, n = box.shape[0], both.shape[0]
+    x = sh.storage_round(rng.standard_normal((n, ci)), sh.BF16)
+    w = sh.storage_round(rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci), sh.BF16)
+    bias = (0.1 * rng.standard_normal(co)).astype(np.float32)
+    res = sh.storage_round(rng.standard_normal((n, co)), sh.BF16)
+    say(f"conv layouts ci={ci} co={co} box={nb} sparse={n - nb}")
+
+    def run(coords, xs, rs):
+        rb = be.build_rulebook(coords)
+        m = coords.shape[0]
+        xb, yb = be.upload(xs), be.alloc(m * co)
+        be.conv(rb, xb, w, bias, yb, ci, co)
+        plain = be.download(yb).reshape(m, co)
+        r = be.upload(rs)
+        be.conv_add(rb, xb, w, bias, r, r, ci, co)  # in place: the output overwrites the residual
+        added = be.download(r).reshape(m, co)
+        rb.free()
+        return plain, added
+
+    p_all, a_all = run(both, x, res)
+    p_box, a_box = run(box, x[:nb], res[:nb])
+    p_sp, a_sp = run(sparse, x[nb:], res[nb:])
+    assert np.array_equal(p_all[:nb], p_box) and np.array_equal(p_all[nb:], p_sp)
+    assert np.array_equal(a_all[:nb], a_box) and np.array_equal(a_all[nb:], a_sp)
+    rows = sample_rows(n, 300)
+    exp = orc.Rulebook(both).conv(x, w, bias, ci, co, rows=rows)
+    err = max_rel_err(p_all[rows[0]:rows[1]:rows[2]], exp)
+    e_add = sh.storage_round(orc.add(sh.storage_round(exp, sh.BF16), res[rows[0]:rows[1]:rows[2]]), sh.BF16)
+    err_add = max_rel_err(a_all[rows[0]:rows[1]:rows[2]], e_add)
+    say(f"conv layouts ci={ci} co={co} max_rel_err={err:.3e} add={err_add:.3e}")
+    assert err <= TOL[sh.BF16] and err_add <= TOL[sh.BF16]
+
+
 @pytest.mark.parametrize("ci,co,n", [(512, 128, 2100), (384, 64, 1500)])
 def test_conv_deep_channels_masked_vs_oracle(ci, co, n):
     """The masked schedule on the same deep shapes (it walks K in 32-channel

@@ -1015,7 +1015,8 @@ trellis_status conv_impl(trellis_sparse_backend * backend, const trellis_sparse_
                                           (const int32_t *) rulebook->tile_off.ptr,
                                           (const int32_t *) rulebook->tile_counts.ptr,
                                           (const uint32_t *) rulebook->mask.ptr, w, (const float *) bd, out->ptr, n,
-                                          ci, co, be->stream, epi);
+                                          ci, co, be->stream, epi,
+                                          (const int32_t *) rulebook->counters.ptr + kLayoutStats);
         } else {
             st = rulebook_ensure_nbr(be, rulebook);
             if (st != TRELLIS_STATUS_OK) return st;

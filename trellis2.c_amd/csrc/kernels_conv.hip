@@ -738,7 +738,7 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-template <int DT, int BN, int RG, int UPB, int DEPTH, int TMR, int NW, int AP = 1>
+template <int DT, int BN, int RG, int UPB, int DEPTH, int TMR, int NW, int AP = 1, bool PACK64 = false>
 __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,
                                                         const int32_t * __restrict__ pair_src,
                                                         const uint8_t * __restrict__ pair_dst,
@@ -748,7 +748,8 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
                                                         const typename Store<DT>::T * __restrict__ w16,
                                                         const float * __restrict__ bias,
                                                         typename Store<DT>::T * __restrict__ y, int64_t n, int ci,
-                                                        int co, int64_t n_col_tiles, ConvEpilogue epi) {
+                                                        int co, int64_t n_col_tiles, ConvEpilogue epi,
+                                                        int layout_sel, const int32_t * __restrict__ layout_stats) {
     using T = typename Store<DT>::T;
     using V = typename Mfma<DT>::V;
     // NW wavefronts; a unit holds AP 16-row blocks per wavefront.
@@ -784,12 +785,28 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int rh = wave % RG, ch = wave / RG;
     const int l16 = lane & 15, lg = lane >> 4;
+    // Layout choice for Co % 256 == 0 (layout_sel 1: this launch runs the
+    // conv if the 256-column layout takes it, 2: if the 128-column one does).
+    // The 256-column blocks cover half tiles with one unit per offset and
+    // half, the 128-column ones whole tiles with one unit per offset, two
+    // where more than half the tile's rows have a neighbour at the offset.
+    // The kernel map counts, over all tiles, the offsets with pairs and
+    // those with more than 128; where at least 3 in 10 have more than 128
+    // (dense sets: configs 3 and 5 at about 1 in 2) the wide layout's
+    // MFMAs per fetched byte win, else (sparse sets: about 1 in 20) its
+    // half-empty units lose to the narrow layout's fuller ones.
+    if (layout_sel != 0) {
+        const int32_t offsets = layout_stats[0], busy = layout_stats[1];
+        if ((10 * busy >= 3 * offsets) != (layout_sel == 1)) return;
+    }
     const int64_t logical = xcd_remap(blockIdx.x, (int64_t) gridDim.x);
-    // Blocks of one map tile are adjacent: (tile, half, column block).
-    const int64_t tile = logical / (n_col_tiles * HALVES);
-    const int half = HALVES == 1 ? 0 : (int) ((logical / n_col_tiles) % HALVES);
+    // Column block slowest, then tile, then half: an XCD's range of blocks
+    // covers few column blocks, so each XCD fetches few columns' weights.
+    const int64_t row_tiles = ((n + kMapTile - 1) / kMapTile) * HALVES;
+    const int64_t tile = (logical % row_tiles) / HALVES;
+    const int half = HALVES == 1 ? 0 : (int) (logical % HALVES);
     const int64_t row0 = tile * kMapTile + half * TM;
-    const int col0 = (int) (logical % n_col_tiles) * BN;
+    const int col0 = (int) (logical / row_tiles) * BN;
     if (row0 >= n) return;  // the empty second half of a short last tile
     const int ci8 = ci >> 3;
     const int KS = ci / BK;
@@ -989,6 +1006,16 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
     // Flush: add a unit's products into the tile sums (as in
     // k_conv_mfma_stream: one vector read-modify-write per row, padding rows
     // into the spare row TM, reads batched ahead of the writes).
+    // Tile-sum column of this lane's products (NT consecutive floats).  With
+    // the weights packed for WN-channel wavefronts (channel b * WN + l * NT + j
+    // at packed position b * WN + 16 * j + l) the tile sums are in channel
+    // order.  PACK64: the weights are packed for 64-channel wavefronts (the
+    // 256-column layout's) and this kernel's wavefronts take 32 of those
+    // packed columns each, channels 64 b + 4 l + 2 h + j (h = ch % 2) for
+    // lane l's product j; they are written at ch * 32 + 2 l + j all the same,
+    // so that a row's writes stay contiguous, and the epilogue reorders.
+    static_assert(!PACK64 || WN == 32, "packing for 64-channel wavefronts read by 32-channel ones");
+    const int acc_col = ch * WN + l16 * NT;
     auto flush = [&](int unit) {
         const int slot = unit & (RING - 1);
         const bool first = unit < CU;  // a centre unit: its rows' first sums
@@ -1002,7 +1029,7 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
                 const ushort4 d = *(const ushort4 *) &s_rdst[slot][(rh + RG * (q0 + qq)) * 16 + lg * 4];
                 const int rows[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) dst[qq][i] = (Row *) (s_acc + rows[i] * BN + ch * WN + l16 * NT);
+                for (int i = 0; i < 4; ++i) dst[qq][i] = (Row *) (s_acc + rows[i] * BN + acc_col);
             }
             if (first) {
 #pragma unroll
@@ -1133,8 +1160,19 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
             // Whole 16-byte chunks through the packed conversions: sum +
             // bias, rounded to the storage type (and widened again).
             float v[8];
+            if constexpr (PACK64) {
+                // Channels cc .. cc + 7 (64 b + 4 l + j, l = 2 q', 2 q' + 1):
+                // j = 0, 1 at 64 b + 4 q' .. + 3, j = 2, 3 at 64 b + 32 + 4 q'.
+                const int c0 = rr * BN + (cc & ~63) + (cc & 63) / 2;
+                const float4 lo = *(const float4 *) &s_acc[c0];
+                const float4 hi = *(const float4 *) &s_acc[c0 + 32];
+                const float t8[8] = {lo.x, lo.y, hi.x, hi.y, lo.z, lo.w, hi.z, hi.w};
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = s_acc[rr * BN + cc + u] + bv[u];
+                for (int u = 0; u < 8; ++u) v[u] = t8[u] + bv[u];
+            } else {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = s_acc[rr * BN + cc + u] + bv[u];
+            }
             int4 o = pack_chunk<DT>(v);
             if constexpr (MODE == kEpiNorm) {
                 unpack_chunk<DT>(o, v);
@@ -1452,11 +1490,11 @@ bool conv_stream_supported(int dtype, int ci, int co) {
 }
 
 namespace {
-template <int DT, int BN, int DEPTH, int NW, int RG, int UPB>
+template <int DT, int BN, int DEPTH, int NW, int RG, int UPB, bool PACK64 = false>
 hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const uint8_t * pair_dst,
                            const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
                            const void * w16, const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
-                           const ConvEpilogue & epi) {
+                           const ConvEpilogue & epi, int layout_sel = 0, const int32_t * layout_stats = nullptr) {
     using T = typename Store<DT>::T;
     const int64_t tiles = (n + kMapTile - 1) / kMapTile;
     const int64_t col_tiles = co / BN;
@@ -1471,7 +1509,7 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const uint8
         if (epi.mode == kEpiNorm || UPB != 1 || ci % 128 != 0) return hipErrorInvalidValue;
         k_conv_mfma_wreg<DT, 256, 2, 1, 4, kMapTile / 2, 8><<<(unsigned) grid, 512, 0, s>>>(
             (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n, ci,
-            co, col_tiles, epi);
+            co, col_tiles, epi, layout_sel, layout_stats);
     } else if constexpr (BN == 128) {
         // Weights in registers; blocks of 8 steps when a unit is a whole
         // number of them (Ci % 256 == 0), else 4.
@@ -1483,17 +1521,18 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const uint8
             // slower this way and keep whole tiles).
             const int64_t hgrid = tiles * col_tiles * 2;
             if (hgrid > 0x7fffffffLL) return hipErrorInvalidValue;
-            k_conv_mfma_wreg<DT, BN, 1, 1, 4, kMapTile / 2, 4><<<(unsigned) hgrid, 256, 0, s>>>(
+            k_conv_mfma_wreg<DT, BN, 1, 1, 4, kMapTile / 2, 4, 1, PACK64><<<(unsigned) hgrid, 256, 0, s>>>(
                 (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n, ci,
-                co, col_tiles, epi);
+                co, col_tiles, epi, layout_sel, layout_stats);
         } else if (UPB == 1) {
-            k_conv_mfma_wreg<DT, BN, 2, UPB, UPB == 1 ? 8 : 4, kMapTile, 8><<<(unsigned) grid, 512, 0, s>>>(
+            k_conv_mfma_wreg<DT, BN, 2, UPB, UPB == 1 ? 8 : 4, kMapTile, 8, 1, PACK64><<<(unsigned) grid, 512, 0, s>>>(
                 (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n,
-                ci, co, col_tiles, epi);
+                ci, co, col_tiles, epi, layout_sel, layout_stats);
         } else {
+            if (PACK64 || layout_sel != 0) return hipErrorInvalidValue;  // Ci = 64 never takes the 256-column layout
             k_conv_mfma_wreg<DT, BN, 2, UPB, 4, kMapTile, 8><<<(unsigned) grid, 512, 0, s>>>(
                 (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n,
-                ci, co, col_tiles, epi);
+                ci, co, col_tiles, epi, 0, nullptr);
         }
     } else {
         if (epi.mode != kEpiNone) return hipErrorInvalidValue;  // 64-channel blocks: plain epilogue only
@@ -1508,14 +1547,24 @@ template <int DT>
 hipError_t launch_stream_dt(const void * x, const int32_t * pair_src, const uint8_t * pair_dst,
                             const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
                             const void * w16, const float * bias, void * y, int64_t n, int ci, int co, hipStream_t s,
-                            const ConvEpilogue & epi) {
+                            const ConvEpilogue & epi, const int32_t * layout_stats) {
     const bool wide = co % 128 == 0;
     const bool pair = ci == 64;  // two 2-step units per 4-step block
 #define TSH_STREAM(BNV, UV)                                                                                      \
     launch_stream_t<DT, BNV, 4, TSH_STREAM_WAVES, TSH_STREAM_ROW_GROUPS, UV>(x, pair_src, pair_dst, tile_off,     \
                                                                            tile_counts, mask, w16, bias, y, n, ci, \
                                                                            co, s, epi)
-    if (conv_wide_supported(ci, co) && epi.mode != kEpiNorm) return TSH_STREAM(256, 1);
+    if (conv_wide_supported(ci, co) && epi.mode != kEpiNorm) {
+        // The 256-column layout or the 128-column one, as the kernel map's
+        // statistics decide on the device (layout_sel): both are launched,
+        // over the same 64-channel weight packing, and the one not chosen
+        // returns at once.  A row's sums are formed in the same order in both.
+        const hipError_t e = launch_stream_t<DT, 256, 4, TSH_STREAM_WAVES, TSH_STREAM_ROW_GROUPS, 1>(
+            x, pair_src, pair_dst, tile_off, tile_counts, mask, w16, bias, y, n, ci, co, s, epi, 1, layout_stats);
+        if (e != hipSuccess) return e;
+        return launch_stream_t<DT, 128, 4, TSH_STREAM_WAVES, TSH_STREAM_ROW_GROUPS, 1, true>(
+            x, pair_src, pair_dst, tile_off, tile_counts, mask, w16, bias, y, n, ci, co, s, epi, 2, layout_stats);
+    }
     if (wide) return pair ? TSH_STREAM(128, 2) : TSH_STREAM(128, 1);
     if (co == 16) return pair ? TSH_STREAM(16, 2) : TSH_STREAM(16, 1);
     if (co == 32) return pair ? TSH_STREAM(32, 2) : TSH_STREAM(32, 1);
@@ -1550,16 +1599,17 @@ hipError_t launch_conv_os(int dtype, const void * x, const int32_t * pair_src, c
 hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const uint8_t * pair_dst,
                                    const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
-                                   hipStream_t s, const ConvEpilogue & epi) {
+                                   hipStream_t s, const ConvEpilogue & epi, const int32_t * layout_stats) {
     if (!conv_stream_supported(dtype, ci, co) || (epi.mode == kEpiNorm && co != 128) ||
-        (epi.mode != kEpiNone && co % 128 != 0)) {
+        (epi.mode != kEpiNone && co % 128 != 0) || layout_stats == nullptr) {
         return hipErrorInvalidValue;
     }
     if (dtype == kBF16) {
         return launch_stream_dt<kBF16>(x, pair_src, pair_dst, tile_off, tile_counts, mask, w16, bias, y, n, ci, co, s,
-                                       epi);
+                                       epi, layout_stats);
     }
-    return launch_stream_dt<kF16>(x, pair_src, pair_dst, tile_off, tile_counts, mask, w16, bias, y, n, ci, co, s, epi);
+    return launch_stream_dt<kF16>(x, pair_src, pair_dst, tile_off, tile_counts, mask, w16, bias, y, n, ci, co, s, epi,
+                                  layout_stats);
 }
 
 }  // namespace tsh

@@ -370,6 +370,14 @@ __global__ void __launch_bounds__(kBlock, NBR ? 5 : 7) k_map_tiles(const int4 * 
             if (lane >= d) incl += o;
         }
         if (t < 27) s_koff[k] = incl - cnt;
+        // Layout statistics for the convs with 256-column blocks: this
+        // tile's offsets with pairs, and with more than half the tile.
+        const int with = __popcll(__ballot(cnt > 0));
+        const int busy = __popcll(__ballot(cnt > kBlock / 2));
+        if (t == 0) {
+            atomicAdd(&counters[kLayoutStats], with);
+            atomicAdd(&counters[kLayoutStats + 1], busy);
+        }
     }
     __syncthreads();
     const int64_t base = tile * kBlock * 27;

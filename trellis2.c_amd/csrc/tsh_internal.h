@@ -105,9 +105,11 @@ template <int DT> __device__ inline int4 pack_chunk(const float * v) {
 // Work split of a rulebook build / conv: rows per tile of the kernel map.
 constexpr int kMapTile = 256;
 constexpr int kBrickCells = 64;  // 4x4x4 cells per brick
-// Build counters: [1] duplicate flag, [4] internal-error flags, and the
-// brick count (statistics) summed over kBrickCounters counters from
-// counters[kBrickCounter].
+// Build counters: [1] duplicate flag, [4] internal-error flags, the conv
+// layout statistics at kLayoutStats (summed over the map tiles: offsets with
+// pairs, then offsets with more than kMapTile / 2 pairs), and the brick count
+// (statistics) summed over kBrickCounters counters from counters[kBrickCounter].
+constexpr int kLayoutStats = 2;
 constexpr int kBrickCounters = 64;
 constexpr int kBrickCounter = 64;
 constexpr int kCounterInts = kBrickCounter + kBrickCounters;
@@ -139,7 +141,7 @@ struct trellis_sparse_rulebook {
     int64_t table_slots;
     tsh::DevMem table;       // brick table: [table_slots] x {uint64 key, int32 idx, pad}
     tsh::DevMem pool;        // int32  [cap_bricks][64] voxel rows, -1 = empty
-    tsh::DevMem counters;    // int32  [kCounterInts]: [1] duplicate flag, [4] internal-error flags, [64..] brick counts
+    tsh::DevMem counters;    // int32  [kCounterInts]: [1] duplicate flag, [2..3] layout statistics, [4] internal-error flags, [64..] brick counts
     // Kernel map.
     tsh::DevMem nbr;         // int32  [n][27]
     tsh::DevMem mask;        // uint32 [n] bit k set when nbr[i][k] >= 0
@@ -217,15 +219,17 @@ enum { kEpiNone = 0, kEpiNorm = 1, kEpiAdd = 2 };
 // Streamed compacted schedule over the tile-major pair lists (needs ci == 64 or ci % 128 == 0).
 // Its weights use the grouped packing: [27][ci/8][co][8] whose packed column
 // b*16g + nt*16 + l holds channel b*16g + l*g + nt, g = conv_stream_group(ci, co).
-// Co % 256 == 0 with Ci % 128 == 0 runs 256-channel blocks over half map
-// tiles (conv_wide_supported), which need the row masks.
+// Co % 256 == 0 with Ci % 128 == 0 (conv_wide_supported) runs 256-channel
+// blocks over half map tiles (which need the row masks) or 128-channel
+// blocks over whole tiles, as the rulebook's layout statistics
+// (counters + kLayoutStats, written by the kernel map) decide on the device.
 bool conv_wide_supported(int ci, int co);
 int conv_stream_group(int ci, int co);
 bool conv_stream_supported(int dtype, int ci, int co);
 hipError_t launch_conv_mfma_stream(int dtype, const void * x, const int32_t * pair_src, const uint8_t * pair_dst,
                                    const int32_t * tile_off, const int32_t * tile_counts, const uint32_t * mask,
                                    const void * w16, const float * bias, void * y, int64_t n, int ci, int co,
-                                   hipStream_t s, const ConvEpilogue & epi = ConvEpilogue());
+                                   hipStream_t s, const ConvEpilogue & epi, const int32_t * layout_stats);
 
 // Output-stationary MFMA conv for Ci = Co = 64 over the tile-major pair lists
 // and the row masks (weights in the grouped packing of conv_stream_group(64, 64)).
