@@ -738,6 +738,8 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+static_assert(kLayoutSlots == 64, "one layout statistics slot per lane");
+
 template <int DT, int BN, int RG, int UPB, int DEPTH, int TMR, int NW, int AP = 1, bool PACK64 = false>
 __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wreg(const typename Store<DT>::T * __restrict__ x,
                                                         const int32_t * __restrict__ pair_src,
@@ -796,7 +798,13 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
     // MFMAs per fetched byte win, else (sparse sets: about 1 in 20) its
     // half-empty units lose to the narrow layout's fuller ones.
     if (layout_sel != 0) {
-        const int32_t offsets = layout_stats[0], busy = layout_stats[1];
+        // Lane l holds slot l of both sums (kLayoutSlots == 64 slots each).
+        int32_t offsets = layout_stats[threadIdx.x & 63], busy = layout_stats[64 + (threadIdx.x & 63)];
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            offsets += __shfl_xor(offsets, d);
+            busy += __shfl_xor(busy, d);
+        }
         if ((10 * busy >= 3 * offsets) != (layout_sel == 1)) return;
     }
     const int64_t logical = xcd_remap(blockIdx.x, (int64_t) gridDim.x);

@@ -375,8 +375,9 @@ __global__ void __launch_bounds__(kBlock, NBR ? 5 : 7) k_map_tiles(const int4 * 
         const int with = __popcll(__ballot(cnt > 0));
         const int busy = __popcll(__ballot(cnt > kBlock / 2));
         if (t == 0) {
-            atomicAdd(&counters[kLayoutStats], with);
-            atomicAdd(&counters[kLayoutStats + 1], busy);
+            const int slot = (int) (blockIdx.x % kLayoutSlots);
+            atomicAdd(&counters[kLayoutStats + slot], with);
+            atomicAdd(&counters[kLayoutStats + kLayoutSlots + slot], busy);
         }
     }
     __syncthreads();

@@ -105,14 +105,18 @@ template <int DT> __device__ inline int4 pack_chunk(const float * v) {
 // Work split of a rulebook build / conv: rows per tile of the kernel map.
 constexpr int kMapTile = 256;
 constexpr int kBrickCells = 64;  // 4x4x4 cells per brick
-// Build counters: [1] duplicate flag, [4] internal-error flags, the conv
-// layout statistics at kLayoutStats (summed over the map tiles: offsets with
-// pairs, then offsets with more than kMapTile / 2 pairs), and the brick count
-// (statistics) summed over kBrickCounters counters from counters[kBrickCounter].
-constexpr int kLayoutStats = 2;
+// Build counters: [1] duplicate flag, [4] internal-error flags, the brick
+// count (statistics) summed over kBrickCounters counters from
+// counters[kBrickCounter], and the conv layout statistics from
+// counters[kLayoutStats]: over the map tiles, the offsets with pairs (summed
+// over kLayoutSlots counters), then the offsets with more than kMapTile / 2
+// pairs (the next kLayoutSlots).  Spread over slots because one address that
+// every tile adds to serialises the kernel map.
 constexpr int kBrickCounters = 64;
 constexpr int kBrickCounter = 64;
-constexpr int kCounterInts = kBrickCounter + kBrickCounters;
+constexpr int kLayoutSlots = 64;
+constexpr int kLayoutStats = kBrickCounter + kBrickCounters;
+constexpr int kCounterInts = kLayoutStats + 2 * kLayoutSlots;
 
 struct Backend;
 
@@ -141,7 +145,7 @@ struct trellis_sparse_rulebook {
     int64_t table_slots;
     tsh::DevMem table;       // brick table: [table_slots] x {uint64 key, int32 idx, pad}
     tsh::DevMem pool;        // int32  [cap_bricks][64] voxel rows, -1 = empty
-    tsh::DevMem counters;    // int32  [kCounterInts]: [1] duplicate flag, [2..3] layout statistics, [4] internal-error flags, [64..] brick counts
+    tsh::DevMem counters;    // int32  [kCounterInts]: [1] duplicate flag, [4] internal-error flags, [64..] brick counts, [128..] layout statistics
     // Kernel map.
     tsh::DevMem nbr;         // int32  [n][27]
     tsh::DevMem mask;        // uint32 [n] bit k set when nbr[i][k] >= 0
