@@ -548,36 +548,173 @@ class Decoder:
         return f
 
 
-def run_decoder(args):
+class Encoder:
+    """The whole shape encoder of the sparse U-Net VAE at the reference's widths, through the backend's entry
+    points in the executor's order (src/architectures/sparse_unet_encoder/weights.c:257-262: channels
+    {64, 128, 256, 512, 1024}, ConvNeXt blocks {0, 4, 8, 16, 4}, 6 input and 32 latent channels;
+    executor.c:160-360 and 392-649):
+      input_layer linear 6 -> 64 and the rulebook on the input voxels;
+      per level its ConvNeXt blocks (trellis_sparse_hip_convnext_block), then, below the last level, an S2C
+      down-block to the next width: row_norm_silu -> conv(Ci -> Co / 8) on the fine voxels -> s2c_build_device
+      -> s2c_pack_device and s2c_skip_mean_device -> build_rulebook_for_c2s_map on the coarse voxels ->
+      row_norm_silu (no affine) -> conv(Co -> Co) + the skip as one trellis_sparse_hip_conv_add;
+      the output head: row_norm (eps 1e-5, no affine) -> to_latent linear 1024 -> 64 (executor.c:551-596: the
+      latent is the first 32 channels).
+    Input voxels: the config-4 shell set (R = 1024, 3.79M voxels), 6 random channels; random weights per layer.
+    """
+
+    CHANNELS = (64, 128, 256, 512, 1024)
+    BLOCKS = (0, 4, 8, 16, 4)
+    IN = 6
+    LATENT = 32
+
+    def __init__(self, be):
+        self.be = be
+        rng = np.random.default_rng(23)
+        self.coords0 = np.ascontiguousarray(wl.make_coords(4), dtype=np.int32)
+        self.n0 = self.coords0.shape[0]
+        self.map0 = be.upload_coords(self.coords0)
+        self.x = be.upload(rng.standard_normal((self.n0, self.IN), dtype=np.float32))
+
+        def rnd(shape, fan_in):
+            return be.keep(np.ascontiguousarray(rng.standard_normal(shape, dtype=np.float32) / np.float32(np.sqrt(fan_in))))
+
+        def small(count, scale=0.1, one=False):
+            v = rng.standard_normal(count, dtype=np.float32) * np.float32(scale)
+            return be.keep(np.ascontiguousarray(v + np.float32(1) if one else v))
+
+        C = self.CHANNELS
+        self.w_in, self.b_in = rnd((C[0], self.IN), self.IN), small(C[0])
+        self.blocks = []
+        for lv, nb in enumerate(self.BLOCKS):
+            c = C[lv]
+            self.blocks.append([(rnd((c, 27, c), 27 * c), small(c), small(c, one=True), small(c),
+                                 rnd((4 * c, c), c), small(4 * c), rnd((c, 4 * c), 4 * c), small(c))
+                                for _ in range(nb)])
+        self.downs = []
+        for lv in range(len(C) - 1):
+            ci, co = C[lv], C[lv + 1]
+            self.downs.append({"g1": small(ci, one=True), "b1": small(ci),
+                               "w1": rnd((co // 8, 27, ci), 27 * ci), "c1b": small(co // 8),
+                               "w2": rnd((co, 27, co), 27 * co), "c2b": small(co)})
+        self.w_out, self.b_out = rnd((2 * self.LATENT, C[-1]), C[-1]), small(2 * self.LATENT)
+        self.stats = None
+
+    def forward(self, marks=False, stats=False):
+        """One forward; with marks, HIP events 0.. at the stage boundaries; with stats, the per-level sizes
+        (read back from the device: the host waits, so those forwards are not the timed ones)."""
+        be = self.be
+        C = self.CHANNELS
+        ev = iter(range(16))
+        names = []
+
+        def mark(name):
+            if marks:
+                be.event(next(ev))
+                names.append(name)
+
+        stat_rows = []
+        mark("start")
+        n = self.n0
+        h = be.alloc(n * C[0])
+        be.linear(self.x, self.w_in, self.b_in, h, n, self.IN, C[0])
+        dmap = self.map0
+        rb = be.build_rulebook_for_c2s_map(dmap)
+        mark("input_layer")
+        owned = None  # the current level's map when a down-block made it
+        for lv, c in enumerate(C):
+            pairs = be.rulebook_stats(rb)["pairs"] if stats else 0
+            for p in self.blocks[lv]:
+                out = be.alloc(n * c)
+                be.convnext_block(rb, h, *p, out, c, 1e-6)
+                h.free()
+                h = out
+            mark(f"level{lv}_convnext")
+            stat_rows.append({"channels": c, "voxels": int(n), "pairs": int(pairs), "convnext_blocks": len(self.blocks[lv])})
+            if lv == len(C) - 1:
+                break
+            d, co = self.downs[lv], C[lv + 1]
+            norm1, conv1 = be.alloc(n * c), be.alloc(n * (co // 8))
+            be.row_norm(h, d["g1"], d["b1"], norm1, n, c, 1e-6, silu=True)
+            be.conv(rb, norm1, d["w1"], d["c1b"], conv1, c, co // 8)
+            fmap, cmap = be.s2c_build_device(coords_map=dmap)
+            m = cmap.n
+            packed, skip, norm2, out = be.alloc(m * co), be.alloc(m * co), be.alloc(m * co), be.alloc(m * co)
+            be.s2c_pack_device(conv1, fmap, packed, co)
+            be.s2c_skip_mean_device(h, fmap, skip, c, co)
+            crb = be.build_rulebook_for_c2s_map(cmap)
+            be.row_norm(packed, None, None, norm2, m, co, 1e-6, silu=True)
+            be.conv_add(crb, norm2, d["w2"], d["c2b"], skip, out, co, co)
+            if stats:
+                stat_rows[-1]["down_fine_pairs"] = int(pairs)
+                stat_rows[-1]["down_coarse_pairs"] = int(be.rulebook_stats(crb)["pairs"])
+            for b in (norm1, conv1, packed, skip, norm2, h):
+                b.free()
+            rb.free()
+            be.free_map(fmap)
+            if owned is not None:
+                be.free_map(owned)
+            h, n, rb, dmap, owned = out, m, crb, cmap, cmap
+            mark(f"level{lv}_s2c")
+        norm, y = be.alloc(n * C[-1]), be.alloc(n * 2 * self.LATENT)
+        be.row_norm(h, None, None, norm, n, C[-1], 1e-5)
+        be.linear(norm, self.w_out, self.b_out, y, n, C[-1], 2 * self.LATENT)
+        mark("to_latent")
+        for b in (norm, y, h):
+            b.free()
+        rb.free()
+        if owned is not None:
+            be.free_map(owned)
+        if stats:
+            self.stats = stat_rows
+        if marks:
+            self.marks = names
+
+    def flops(self):
+        """Convs (2 P Ci Co), the ConvNeXt MLPs and the down-blocks' convs, at the sizes the stats forward read
+        back."""
+        C, f = self.CHANNELS, 0.0
+        for lv, st in enumerate(self.stats):
+            c, n = C[lv], st["voxels"]
+            f += st["convnext_blocks"] * (wl.conv_flops(st["pairs"], c, c) + 2 * (2 * n * c * 4 * c))
+            if "down_coarse_pairs" in st:
+                co = C[lv + 1]
+                f += wl.conv_flops(st["down_fine_pairs"], c, co // 8) + wl.conv_flops(st["down_coarse_pairs"], co, co)
+        return f
+
+
+def run_model(args, kind):
     be = sh.Backend(0, sh.BF16)
-    log("bench: building the decoder's random weights")
-    dec = Decoder(be)
-    log(f"bench: decoder from {dec.n0} latent voxels")
+    log(f"bench: building the {kind}'s random weights")
+    net = Decoder(be) if kind == "decoder" else Encoder(be)
+    log(f"bench: {kind} from {net.n0} voxels")
     for _ in range(max(1, args.warmup)):
-        dec.forward()
+        net.forward()
     be.synchronize()
-    dec.forward(stats=True)  # sizes
+    net.forward(stats=True)  # sizes
     be.synchronize()
-    dec.forward(marks=True)  # the stage split, from a forward with no read-backs of its own
+    net.forward(marks=True)  # the stage split, from a forward with no read-backs of its own
     be.synchronize()
-    split = {dec.marks[i]: round(be.elapsed(i - 1, i), 3) for i in range(1, len(dec.marks))}
+    split = {net.marks[i]: round(be.elapsed(i - 1, i), 3) for i in range(1, len(net.marks))}
     be.synchronize()
     be.event(14)
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        dec.forward()
+        net.forward()
     be.event(15)
     be.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / args.steps
     dev = be.elapsed(14, 15) / args.steps
     ms = max(dev, wall)
-    print(json.dumps({"bench": "decoder", "dtype": "bf16",
-                      "data": "synthetic (config-3 parent shell reduced to R = 64 as the latent voxels; random weights "
-                              "per layer; subdivision from random logits)",
+    data = ("synthetic (config-3 parent shell reduced to R = 64 as the latent voxels; random weights per layer; "
+            "subdivision from random logits)" if kind == "decoder" else
+            "synthetic (config-4 shell set, R = 1024, as the input voxels; 6 random input channels; random weights "
+            "per layer)")
+    print(json.dumps({"bench": kind, "dtype": "bf16", "data": data,
                       "steps": args.steps, "warmup": max(1, args.warmup), "ms_per_forward": round(ms, 3),
                       "device_ms_per_forward": round(dev, 3), "wall_ms_per_forward": round(wall, 3),
-                      "effective_tflops": round(dec.flops() / (ms * 1e-3) / 1e12, 1),
-                      "levels": dec.stats, "stage_ms": split}))
+                      "effective_tflops": round(net.flops() / (ms * 1e-3) / 1e12, 1),
+                      "levels": net.stats, "stage_ms": split}))
     be.destroy()
 
 
@@ -739,6 +876,10 @@ def main():
     ap.add_argument("--decoder", action="store_true",
                     help="instead of the configuration step, time the whole shape decoder at the reference's widths "
                          "(5 levels, 32 ConvNeXt blocks, 4 up-blocks) and print its own JSON line")
+    ap.add_argument("--encoder", action="store_true",
+                    help="instead of the configuration step, time the whole shape encoder at the reference's widths "
+                         "(5 levels, 32 ConvNeXt blocks, 4 S2C down-blocks) from the config-4 voxels and print its "
+                         "own JSON line")
     ap.add_argument("--calibrate", action="store_true",
                     help="run one fp32 add over 2 x 64Mi-element inputs (512 MiB read, 256 MiB written) so PMC "
                          "byte counters can be scaled against a streaming kernel of known traffic")
@@ -765,7 +906,9 @@ def main():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
     if args.decoder:
-        return run_decoder(args)
+        return run_model(args, "decoder")
+    if args.encoder:
+        return run_model(args, "encoder")
     if args.block is not None:
         run_block(args)
         return
