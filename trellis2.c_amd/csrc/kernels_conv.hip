@@ -793,10 +793,12 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
     // half, the 128-column ones whole tiles with one unit per offset, two
     // where more than half the tile's rows have a neighbour at the offset.
     // The kernel map counts, over all tiles, the offsets with pairs and
-    // those with more than 128; where at least 3 in 10 have more than 128
-    // (dense sets: configs 3 and 5 at about 1 in 2) the wide layout's
-    // MFMAs per fetched byte win, else (sparse sets: about 1 in 20) its
-    // half-empty units lose to the narrow layout's fuller ones.
+    // those with more than 128.  On dense sets (about 1 in 2 with more than
+    // 128) the wide layout's MFMAs per fetched byte win, on sparse ones
+    // (about 1 in 20) its half-empty units lose to the narrow layout's
+    // fuller ones.  The crossover moves with Ci (measured): the wide layout
+    // runs from 4 in 10 with Ci >= 512 (config 5: 0.52, wide 5 % faster),
+    // from 6 in 10 with Ci <= 256 (0.49 and 0.56: narrow 5 and 1-2 % faster).
     if (layout_sel != 0) {
         // Lane l holds slot l of both sums (kLayoutSlots == 64 slots each).
         int32_t offsets = layout_stats[threadIdx.x & 63], busy = layout_stats[64 + (threadIdx.x & 63)];
@@ -805,7 +807,7 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
             offsets += __shfl_xor(offsets, d);
             busy += __shfl_xor(busy, d);
         }
-        if ((10 * busy >= 3 * offsets) != (layout_sel == 1)) return;
+        if ((10 * busy >= (ci <= 256 ? 6 : 4) * offsets) != (layout_sel == 1)) return;
     }
     const int64_t logical = xcd_remap(blockIdx.x, (int64_t) gridDim.x);
     // Column block slowest, then tile, then half: an XCD's range of blocks
