@@ -648,6 +648,30 @@ def test_linear_mfma_vs_oracle(kernel_linears, dtype, ci, co, n):
             assert max_rel_err(be.download(yb), exp) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [sh.F32, sh.F16, sh.BF16])
+@pytest.mark.parametrize("ci,co,n", [(6, 64, 100003), (1, 8, 1), (16, 256, 1031), (3, 24, 77), (6, 64, 1000003)])
+def test_linear_small_k_bitexact(be32, be16, bebf, dtype, ci, co, n):
+    """Few input channels (the encoder's 6 -> 64 input layer, Ci <= 16): one
+    thread per row and 8 outputs.  Bias, then the products in channel order,
+    as the oracle (and the reference's linear) sums them: the outputs equal
+    the oracle's rounded to the storage type, bit for bit, without SiLU (its
+    expf differs from libm by an ulp), and to the storage tolerance with it."""
+    be = backend_for(dtype, be32, be16, bebf)
+    say(f"linear small K dtype={dtype} ci={ci} co={co} n={n}")
+    rng = np.random.default_rng(ci * 7 + co + n)
+    x = sh.storage_round(rng.standard_normal((n, ci)), dtype)
+    w = rng.standard_normal((co, ci)).astype(np.float32)
+    bias = rng.standard_normal(co).astype(np.float32)
+    xb = be.upload(x)
+    yb = be.alloc(n * co)
+    for bb in (bias, None):
+        be.linear(xb, w, bb, yb, n, ci, co)
+        exp = orc.linear(x, w, bb, n, ci, co)
+        assert np.array_equal(be.download(yb).reshape(n, co), sh.storage_round(exp, dtype))
+    be.linear(xb, w, bias, yb, n, ci, co, silu=True)
+    assert max_rel_err(be.download(yb), orc.linear(x, w, bias, n, ci, co, True)) <= TOL[dtype]
+
+
 @pytest.mark.parametrize("dtype", [sh.F16, sh.BF16])
 @pytest.mark.parametrize("ci,co,n", [(256, 8, 316027), (64, 8, 1), (128, 16, 17), (1024, 3, 1000), (32, 1, 50),
                                      (512, 8, 4099)])

@@ -150,6 +150,57 @@ __global__ void __launch_bounds__(256) k_linear(const typename Store<DT>::T * __
     }
 }
 
+// Linear with few input channels (Ci <= kSmallK, Co % 8 == 0, Co <= kSmallKCo:
+// the encoder's 6 -> 64 input layer): one thread per row and 8 output
+// channels, the weights in LDS, one 16-byte store per thread (32 for fp32)
+// instead of k_linear's 2-byte stores.  Each output is the bias, then each
+// input channel's product added in order, without contraction, and stored
+// as k_linear stores it: the outputs are bit-identical to k_linear's.
+constexpr int kSmallK = 16;
+constexpr int kSmallKCo = 256;
+
+template <int DT>
+__global__ void __launch_bounds__(256) k_linear_smallk(const typename Store<DT>::T * __restrict__ x,
+                                                       const float * __restrict__ wt, const float * __restrict__ bias,
+                                                       typename Store<DT>::T * __restrict__ y, int64_t n, int ci,
+                                                       int co, int silu) {
+#pragma clang fp contract(off)
+    using T = typename Store<DT>::T;
+    __shared__ float s_w[kSmallK * kSmallKCo];
+    __shared__ float s_b[kSmallKCo];
+    for (int e = threadIdx.x; e < ci * co; e += blockDim.x) s_w[e] = wt[e];
+    for (int e = threadIdx.x; e < co; e += blockDim.x) s_b[e] = bias != nullptr ? bias[e] : 0.0f;
+    __syncthreads();
+    const int groups = co / 8;
+    const int64_t total = n * groups;
+    for (int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; id < total;
+         id += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t row = id / groups;
+        const int col = (int) (id - row * groups) * 8;
+        float acc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = s_b[col + j];
+        for (int c = 0; c < ci; ++c) {
+            const float a = Store<DT>::ld(x, row * ci + c);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = acc[j] + a * s_w[c * co + col + j];
+        }
+        union {
+            T h[8];
+            int4 v[sizeof(T) / 2];
+        } o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float v = acc[j];
+            if (silu) v = v / (1.0f + expf(-v));
+            Store<DT>::st_signed(o.h, j, v);
+        }
+        int4 * dst = (int4 *) (y + row * co + col);
+#pragma unroll
+        for (int k = 0; k < (int) (sizeof(T) / 2); ++k) dst[k] = o.v[k];
+    }
+}
+
 template <int DT>
 __global__ void k_c2s_count(const typename Store<DT>::T * __restrict__ logits, int64_t n,
                             int32_t * __restrict__ counts) {
@@ -583,6 +634,24 @@ hipError_t launch_row_norm(int dtype, const void * x, const float * gamma, const
 
 hipError_t launch_linear(int dtype, const void * x, const float * wt, const float * bias, void * y, int64_t n, int ci,
                          int co, int silu, hipStream_t s) {
+    if (ci <= kSmallK && co % 8 == 0 && co <= kSmallKCo) {
+        const int g = blocks_for(n * (co / 8), 256, 16384);
+        switch (dtype) {
+            case kF32:
+                k_linear_smallk<kF32><<<g, 256, 0, s>>>((const float *) x, wt, bias, (float *) y, n, ci, co, silu);
+                break;
+            case kF16:
+                k_linear_smallk<kF16><<<g, 256, 0, s>>>((const _Float16 *) x, wt, bias, (_Float16 *) y, n, ci, co,
+                                                        silu);
+                break;
+            case kBF16:
+                k_linear_smallk<kBF16><<<g, 256, 0, s>>>((const uint16_t *) x, wt, bias, (uint16_t *) y, n, ci, co,
+                                                         silu);
+                break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned) ((n + 31) / 32), (unsigned) ((co + 63) / 64));
     switch (dtype) {
         case kF32: k_linear<kF32><<<grid, 256, 0, s>>>((const float *) x, wt, bias, (float *) y, n, ci, co, silu); break;
