@@ -750,8 +750,8 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
                                                         const typename Store<DT>::T * __restrict__ w16,
                                                         const float * __restrict__ bias,
                                                         typename Store<DT>::T * __restrict__ y, int64_t n, int ci,
-                                                        int co, int64_t n_col_tiles, ConvEpilogue epi,
-                                                        int layout_sel, const int32_t * __restrict__ layout_stats) {
+                                                        int co, ConvEpilogue epi, int layout_sel,
+                                                        const int32_t * __restrict__ layout_stats) {
     using T = typename Store<DT>::T;
     using V = typename Mfma<DT>::V;
     // NW wavefronts; a unit holds AP 16-row blocks per wavefront.
@@ -1519,7 +1519,7 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const uint8
         if (epi.mode == kEpiNorm || UPB != 1 || ci % 128 != 0) return hipErrorInvalidValue;
         k_conv_mfma_wreg<DT, 256, 2, 1, 4, kMapTile / 2, 8><<<(unsigned) grid, 512, 0, s>>>(
             (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n, ci,
-            co, col_tiles, epi, layout_sel, layout_stats);
+            co, epi, layout_sel, layout_stats);
     } else if constexpr (BN == 128) {
         // Weights in registers; blocks of 8 steps when a unit is a whole
         // number of them (Ci % 256 == 0), else 4.
@@ -1533,16 +1533,16 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const uint8
             if (hgrid > 0x7fffffffLL) return hipErrorInvalidValue;
             k_conv_mfma_wreg<DT, BN, 1, 1, 4, kMapTile / 2, 4, 1, PACK64><<<(unsigned) hgrid, 256, 0, s>>>(
                 (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n, ci,
-                co, col_tiles, epi, layout_sel, layout_stats);
+                co, epi, layout_sel, layout_stats);
         } else if (UPB == 1) {
             k_conv_mfma_wreg<DT, BN, 2, UPB, UPB == 1 ? 8 : 4, kMapTile, 8, 1, PACK64><<<(unsigned) grid, 512, 0, s>>>(
                 (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n,
-                ci, co, col_tiles, epi, layout_sel, layout_stats);
+                ci, co, epi, layout_sel, layout_stats);
         } else {
             if (PACK64 || layout_sel != 0) return hipErrorInvalidValue;  // Ci = 64 never takes the 256-column layout
             k_conv_mfma_wreg<DT, BN, 2, UPB, 4, kMapTile, 8><<<(unsigned) grid, 512, 0, s>>>(
                 (const T *) x, pair_src, pair_dst, tile_off, tile_counts, mask, (const T *) w16, bias, (T *) y, n,
-                ci, co, col_tiles, epi, 0, nullptr);
+                ci, co, epi, 0, nullptr);
         }
     } else {
         if (epi.mode != kEpiNone) return hipErrorInvalidValue;  // 64-channel blocks: plain epilogue only
