@@ -402,6 +402,20 @@ class Block:
                 + 2 * self.n * self.ci * 8)
 
 
+def random_weights(be, rng):
+    """Two makers of device-cached random fp32 weights: rnd(shape, fan_in) ~ N(0, 1/fan_in); small(count) ~ N(0,
+    0.1), or 1 + N(0, 0.1) with one=True (norm scales)."""
+
+    def rnd(shape, fan_in):
+        return be.keep(np.ascontiguousarray(rng.standard_normal(shape, dtype=np.float32) / np.float32(np.sqrt(fan_in))))
+
+    def small(count, scale=0.1, one=False):
+        v = rng.standard_normal(count, dtype=np.float32) * np.float32(scale)
+        return be.keep(np.ascontiguousarray(v + np.float32(1) if one else v))
+
+    return rnd, small
+
+
 class Decoder:
     """The whole shape decoder of the sparse U-Net VAE at the reference's widths, through the backend's entry
     points in the executor's order (src/architectures/sparse_unet_decoder/decoder.c:248-249: channels
@@ -434,12 +448,7 @@ class Decoder:
         self.map0 = be.upload_coords(self.coords0)
         self.latent = be.upload(rng.standard_normal((self.n0, self.LATENT), dtype=np.float32))
 
-        def rnd(shape, fan_in):
-            return be.keep(np.ascontiguousarray(rng.standard_normal(shape, dtype=np.float32) / np.float32(np.sqrt(fan_in))))
-
-        def small(count, scale=0.1, one=False):
-            v = rng.standard_normal(count, dtype=np.float32) * np.float32(scale)
-            return be.keep(np.ascontiguousarray(v + np.float32(1) if one else v))
+        rnd, small = random_weights(be, rng)
 
         C = self.CHANNELS
         self.w_in, self.b_in = rnd((C[0], self.LATENT), self.LATENT), small(C[0])
@@ -576,12 +585,7 @@ class Encoder:
         self.map0 = be.upload_coords(self.coords0)
         self.x = be.upload(rng.standard_normal((self.n0, self.IN), dtype=np.float32))
 
-        def rnd(shape, fan_in):
-            return be.keep(np.ascontiguousarray(rng.standard_normal(shape, dtype=np.float32) / np.float32(np.sqrt(fan_in))))
-
-        def small(count, scale=0.1, one=False):
-            v = rng.standard_normal(count, dtype=np.float32) * np.float32(scale)
-            return be.keep(np.ascontiguousarray(v + np.float32(1) if one else v))
+        rnd, small = random_weights(be, rng)
 
         C = self.CHANNELS
         self.w_in, self.b_in = rnd((C[0], self.IN), self.IN), small(C[0])
