@@ -203,8 +203,9 @@ def mixed_density_sets(rng):
     return np.ascontiguousarray(box.astype(np.int32)), np.ascontiguousarray(sparse.astype(np.int32))
 
 
+@pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])
 @pytest.mark.parametrize("ci,co", [(128, 256), (256, 512), (512, 256)])
-def test_conv_layouts_bitexact(backends, ci, co):
+def test_conv_layouts_bitexact(backends, dtype, ci, co):
     """Co % 256 == 0 runs the 256-column layout on dense sets and the
     128-column one on sparse sets (the kernel map's statistics decide).  The
     box alone takes the first, the union of box and sparse part the second:
@@ -213,16 +214,16 @@ def test_conv_layouts_bitexact(backends, ci, co):
     layouts, and the parts are too far apart to be neighbours), with and
     without the residual epilogue (in place), and match the oracle on a
     sample."""
-    be = backends[sh.BF16]
+    be = backends[dtype]
     rng = np.random.default_rng(ci + co)
     box, sparse = mixed_density_sets(rng)
     both = np.ascontiguousarray(np.concatenate([box, sparse]))
     nb, n = box.shape[0], both.shape[0]
-    x = sh.storage_round(rng.standard_normal((n, ci)), sh.BF16)
-    w = sh.storage_round(rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci), sh.BF16)
+    x = sh.storage_round(rng.standard_normal((n, ci)), dtype)
+    w = sh.storage_round(rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci), dtype)
     bias = (0.1 * rng.standard_normal(co)).astype(np.float32)
-    res = sh.storage_round(rng.standard_normal((n, co)), sh.BF16)
-    say(f"conv layouts ci={ci} co={co} box={nb} sparse={n - nb}")
+    res = sh.storage_round(rng.standard_normal((n, co)), dtype)
+    say(f"conv layouts dtype={dtype} ci={ci} co={co} box={nb} sparse={n - nb}")
 
     def run(coords, xs, rs):
         rb = be.build_rulebook(coords)
@@ -244,10 +245,10 @@ def test_conv_layouts_bitexact(backends, ci, co):
     rows = sample_rows(n, 300)
     exp = orc.Rulebook(both).conv(x, w, bias, ci, co, rows=rows)
     err = max_rel_err(p_all[rows[0]:rows[1]:rows[2]], exp)
-    e_add = sh.storage_round(orc.add(sh.storage_round(exp, sh.BF16), res[rows[0]:rows[1]:rows[2]]), sh.BF16)
+    e_add = sh.storage_round(orc.add(sh.storage_round(exp, dtype), res[rows[0]:rows[1]:rows[2]]), dtype)
     err_add = max_rel_err(a_all[rows[0]:rows[1]:rows[2]], e_add)
     say(f"conv layouts ci={ci} co={co} max_rel_err={err:.3e} add={err_add:.3e}")
-    assert err <= TOL[sh.BF16] and err_add <= TOL[sh.BF16]
+    assert err <= TOL[dtype] and err_add <= TOL[dtype]
 
 
 @pytest.mark.parametrize("ci,co,n", [(512, 128, 2100), (384, 64, 1500)])
