@@ -204,7 +204,7 @@ def mixed_density_sets(rng):
 
 
 @pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])
-@pytest.mark.parametrize("ci,co", [(128, 256), (256, 512), (512, 256)])
+@pytest.mark.parametrize("ci,co", [(128, 256), (256, 512), (512, 256), (256, 1024), (512, 2048)])
 def test_conv_layouts_bitexact(backends, dtype, ci, co):
     """Co % 256 == 0 runs the 256-column layout on dense sets and the
     128-column one on sparse sets (the kernel map's statistics decide).  The
