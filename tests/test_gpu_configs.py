@@ -251,6 +251,46 @@ def test_conv_layouts_bitexact(backends, dtype, ci, co):
     assert err <= TOL[dtype] and err_add <= TOL[dtype]
 
 
+def decoder_level_set(levels):
+    """The decoder's voxel sets: the config-3 parent shell reduced to R = 64,
+    subdivided `levels` times with seeded random logits (about half the
+    children kept), as `bench.py --decoder` builds them; 7-11 neighbours per
+    voxel, the sparse sets that take the 128-column conv layout."""
+    pc = wl.workload(3)["parent_coords"].copy()
+    pc[:, 1:] >>= 2
+    cur = np.ascontiguousarray(np.unique(pc, axis=0), dtype=np.int32)
+    rng = np.random.default_rng(41)
+    for _ in range(levels):
+        rc, cur, _, _ = orc.c2s_map(cur, rng.standard_normal((cur.shape[0], 8)).astype(np.float32))
+        assert rc == 0
+    return np.ascontiguousarray(cur, dtype=np.int32)
+
+
+@pytest.mark.parametrize("levels,ci,co", [(1, 512, 512), (1, 512, 2048), (2, 256, 256), (2, 256, 1024), (3, 128, 512)])
+def test_conv_decoder_levels_vs_oracle(backends, levels, ci, co):
+    """The decoder's sparse levels at their real size and widths (the
+    ConvNeXt convs and the up-blocks' Ci -> 8 Co convs), bf16, against the
+    oracle on a strided sample that puts a row in every 256-row map tile."""
+    be = backends[sh.BF16]
+    coords = decoder_level_set(levels)
+    n = coords.shape[0]
+    rng = np.random.default_rng(levels * 1000 + ci + co)
+    x = sh.storage_round(rng.standard_normal((n, ci)), sh.BF16)
+    w = sh.storage_round(rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci), sh.BF16)
+    bias = (0.1 * rng.standard_normal(co)).astype(np.float32)
+    say(f"decoder level {levels} conv {ci}->{co} n={n}")
+    rb = be.build_rulebook(coords)
+    xb, yb = be.upload(x), be.alloc(n * co)
+    be.conv(rb, xb, w, bias, yb, ci, co)
+    got = be.download(yb).reshape(n, co)
+    rows = (5, n, 255)
+    exp = orc.Rulebook(coords).conv(x, w, bias, ci, co, rows=rows)
+    err = max_rel_err(got[rows[0]:rows[1]:rows[2]], exp)
+    say(f"decoder level {levels} conv {ci}->{co} rows={exp.shape[0]} max_rel_err={err:.3e}")
+    assert err <= TOL[sh.BF16]
+    rb.free()
+
+
 @pytest.mark.parametrize("ci,co,n", [(512, 128, 2100), (384, 64, 1500)])
 def test_conv_deep_channels_masked_vs_oracle(ci, co, n):
     """The masked schedule on the same deep shapes (it walks K in 32-channel
