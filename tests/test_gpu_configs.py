@@ -291,6 +291,49 @@ def test_conv_decoder_levels_vs_oracle(backends, levels, ci, co):
     rb.free()
 
 
+_ENCODER_SETS = {}
+
+
+def encoder_level_set(level):
+    """The encoder's voxel sets: the config-4 shells (R = 1024) and their S2C
+    coarsenings, as `bench.py --encoder` builds them (13-16 neighbours per
+    voxel below the input level)."""
+    if not _ENCODER_SETS:
+        cur = np.ascontiguousarray(wl.make_coords(4), dtype=np.int32)
+        _ENCODER_SETS[0] = cur
+        for lv in range(1, 5):
+            rc, cur, _, _ = orc.s2c_map(cur)
+            assert rc == 0
+            _ENCODER_SETS[lv] = np.ascontiguousarray(cur, dtype=np.int32)
+    return _ENCODER_SETS[level]
+
+
+@pytest.mark.parametrize("level,ci,co", [(0, 64, 16), (1, 128, 32), (2, 256, 256), (3, 512, 512), (3, 512, 128),
+                                         (4, 1024, 1024)])
+def test_conv_encoder_levels_vs_oracle(backends, level, ci, co):
+    """The encoder's levels at their real size and widths (the ConvNeXt convs
+    and the down-blocks' Ci -> Co / 8 convs), bf16, against the oracle on a
+    strided sample that puts a row in every 256-row map tile."""
+    be = backends[sh.BF16]
+    coords = encoder_level_set(level)
+    n = coords.shape[0]
+    rng = np.random.default_rng(level * 1000 + ci + co)
+    x = sh.storage_round(rng.standard_normal((n, ci)), sh.BF16)
+    w = sh.storage_round(rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci), sh.BF16)
+    bias = (0.1 * rng.standard_normal(co)).astype(np.float32)
+    say(f"encoder level {level} conv {ci}->{co} n={n}")
+    rb = be.build_rulebook(coords)
+    xb, yb = be.upload(x), be.alloc(n * co)
+    be.conv(rb, xb, w, bias, yb, ci, co)
+    got = be.download(yb).reshape(n, co)
+    rows = (7, n, 255)
+    exp = orc.Rulebook(coords).conv(x, w, bias, ci, co, rows=rows)
+    err = max_rel_err(got[rows[0]:rows[1]:rows[2]], exp)
+    say(f"encoder level {level} conv {ci}->{co} rows={exp.shape[0]} max_rel_err={err:.3e}")
+    assert err <= TOL[sh.BF16]
+    rb.free()
+
+
 @pytest.mark.parametrize("ci,co,n", [(512, 128, 2100), (384, 64, 1500)])
 def test_conv_deep_channels_masked_vs_oracle(ci, co, n):
     """The masked schedule on the same deep shapes (it walks K in 32-channel
