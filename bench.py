@@ -904,7 +904,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU sharding design is described in DESIGN.md)", file=sys.stderr)
+              "(more than one GPU is a design only: the sharding of the path is not built)", file=sys.stderr)
         sys.exit(2)
     if sh.device_count() < 1:
         print("bench.py: no HIP device visible", file=sys.stderr)

@@ -96,7 +96,7 @@ def test_neighbors_wrap_like_reference_keys():
 
 
 def test_config1_pairs_match_reference_calibration():
-    # BASELINE.md / survey calibration of the compiled reference: N=14,648, P=261,416.
+    # The compiled reference's CPU path (trellis_sparse_cpu.c), run on this set: N=14,648, P=261,416.
     c = wl.make_coords(1)
     assert c.shape[0] == 14648
     nbr = orc.Rulebook(c).neighbors()
