@@ -1013,9 +1013,6 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Flush: add a unit's products into the tile sums (as in
-    // k_conv_mfma_stream: one vector read-modify-write per row, padding rows
-    // into the spare row TM, reads batched ahead of the writes).
     // Tile-sum column of this lane's products (NT consecutive floats).  With
     // the weights packed for WN-channel wavefronts (channel b * WN + l * NT + j
     // at packed position b * WN + 16 * j + l) the tile sums are in channel
@@ -1026,6 +1023,9 @@ __global__ void __launch_bounds__(64 * NW, NW * AP == 8 ? 1 : 2) k_conv_mfma_wre
     // so that a row's writes stay contiguous, and the epilogue reorders.
     static_assert(!PACK64 || WN == 32, "packing for 64-channel wavefronts read by 32-channel ones");
     const int acc_col = ch * WN + l16 * NT;
+    // Flush: add a unit's products into the tile sums (as in
+    // k_conv_mfma_stream: one vector read-modify-write per row, padding rows
+    // into the spare row TM, reads batched ahead of the writes).
     auto flush = [&](int unit) {
         const int slot = unit & (RING - 1);
         const bool first = unit < CU;  // a centre unit: its rows' first sums
