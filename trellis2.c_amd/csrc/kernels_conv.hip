@@ -1523,12 +1523,15 @@ hipError_t launch_stream_t(const void * x, const int32_t * pair_src, const uint8
     } else if constexpr (BN == 128) {
         // Weights in registers; blocks of 8 steps when a unit is a whole
         // number of them (Ci % 256 == 0), else 4.
-        if (UPB == 1 && ci % 256 != 0) {
+        if (UPB == 1 && (ci % 256 != 0 || (PACK64 && ci == 256))) {
             // 4-step units (Ci = 128, 384, ...): half map tiles, 64-pair
             // units and 4 wavefronts, so that two blocks (81 KB of LDS each)
             // share a CU and one's barriers overlap the other's MFMAs
             // (config 2: 0.636 -> 0.602 ms; 8-step units measured 1.5 %
-            // slower this way and keep whole tiles).
+            // slower this way and keep whole tiles).  On the sparse sets that
+            // take this layout for Co % 256 == 0, Ci = 256 runs half tiles
+            // too (the encoder's 256 -> 256 and the up-blocks' 256 -> 1024:
+            // 1.4-3.6 % faster; Ci = 512 was 4-10 % slower).
             const int64_t hgrid = tiles * col_tiles * 2;
             if (hgrid > 0x7fffffffLL) return hipErrorInvalidValue;
             k_conv_mfma_wreg<DT, BN, 1, 1, 4, kMapTile / 2, 4, 1, PACK64><<<(unsigned) hgrid, 256, 0, s>>>(
