@@ -251,6 +251,33 @@ def test_conv_layouts_bitexact(backends, dtype, ci, co):
     assert err <= TOL[dtype] and err_add <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [sh.BF16, sh.F16])
+@pytest.mark.parametrize("n", [1, 2, 127, 129, 257])
+@pytest.mark.parametrize("ci,co", [(256, 512), (128, 256), (512, 256)])
+def test_conv_wide_outputs_tiny_sets(backends, dtype, n, ci, co):
+    """Co % 256 == 0 on sets of one to two map tiles (a single voxel, a short
+    second half tile, one row past a tile), with the plain and the in-place
+    residual epilogue, against the oracle on every row."""
+    be = backends[dtype]
+    g = np.stack(np.meshgrid(*(np.arange(7),) * 3, indexing="ij"), -1).reshape(-1, 3)[:n]
+    coords = np.ascontiguousarray(np.concatenate([np.zeros((n, 1), np.int64), g], 1).astype(np.int32))
+    rng = np.random.default_rng(n * 3 + ci + co + dtype)
+    x = sh.storage_round(rng.standard_normal((n, ci)), dtype)
+    w = sh.storage_round(rng.standard_normal((co, 27, ci)) / math.sqrt(27 * ci), dtype)
+    bias = (0.1 * rng.standard_normal(co)).astype(np.float32)
+    res = sh.storage_round(rng.standard_normal((n, co)), dtype)
+    rb = be.build_rulebook(coords)
+    xb, yb = be.upload(x), be.alloc(n * co)
+    be.conv(rb, xb, w, bias, yb, ci, co)
+    exp = orc.Rulebook(coords).conv(x, w, bias, ci, co)
+    assert max_rel_err(be.download(yb).reshape(n, co), exp) <= TOL[dtype]
+    r = be.upload(res)
+    be.conv_add(rb, xb, w, bias, r, r, ci, co)
+    e_add = sh.storage_round(orc.add(sh.storage_round(exp, dtype), res), dtype)
+    assert max_rel_err(be.download(r).reshape(n, co), e_add) <= TOL[dtype]
+    rb.free()
+
+
 def decoder_level_set(levels):
     """The decoder's voxel sets: the config-3 parent shell reduced to R = 64,
     subdivided `levels` times with seeded random logits (about half the
